@@ -1,0 +1,267 @@
+/*
+ * qmla.h -- C ABI of the MI355X (gfx950) MLA attention library (libqmla.so).
+ *
+ * This is the drop-in boundary for qmoe-rs's MLA attention hot path.  Each
+ * entry point names the reference interface it replaces (paths relative to
+ * the qmoe-rs source tree).  Plain C: no C++ types, no exceptions, no torch
+ * types.  Device pointers are HIP device addresses (e.g. from
+ * qmla_buffer_alloc); streams are hipStream_t passed as void* (NULL = the
+ * default stream).
+ *
+ * Conventions
+ *  - Every call returns a qmla_status.  On failure qmla_last_error() holds a
+ *    message for the calling thread.  Shapes and pointers are validated
+ *    before anything is launched; nothing aborts the process.
+ *  - Compute calls are asynchronous on the given stream and allocate no
+ *    device memory; scratch comes from a caller-provided workspace whose
+ *    size is returned by the matching *_workspace_bytes query.
+ *  - Tensors are row-major and contiguous, in the layouts documented at
+ *    each call.  bf16 values are stored as uint16 bit patterns.
+ *  - No global mutable state apart from the per-thread error string and a
+ *    per-device cached CU count, so calls on different streams may run from
+ *    different threads.  A cache object must not be mutated concurrently.
+ */
+#ifndef QMLA_H
+#define QMLA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QMLA_VERSION 100 /* 0.1.0 */
+
+#if defined(__GNUC__)
+#define QMLA_API __attribute__((visibility("default")))
+#else
+#define QMLA_API
+#endif
+
+typedef enum {
+  QMLA_OK = 0,
+  QMLA_ERR_INVALID_ARG = 1, /* null pointer, bad enum, non-positive size      */
+  QMLA_ERR_SHAPE = 2,       /* dimensions inconsistent or out of range        */
+  QMLA_ERR_UNSUPPORTED = 3, /* valid request this build does not implement    */
+  QMLA_ERR_HIP = 4,         /* a HIP runtime call failed                      */
+  QMLA_ERR_OOM = 5,         /* device allocation failed                       */
+  QMLA_ERR_CAPACITY = 6,    /* cache append beyond a sequence's capacity      */
+  QMLA_ERR_WORKSPACE = 7    /* workspace missing or smaller than required     */
+} qmla_status;
+
+typedef enum { QMLA_F32 = 0, QMLA_BF16 = 1 } qmla_dtype;
+
+typedef void *qmla_stream; /* hipStream_t */
+
+/* ------------------------------------------------------------ library ---- */
+QMLA_API int qmla_version(void);
+/* Message of the last failed call on this thread ("" if none). */
+QMLA_API const char *qmla_last_error(void);
+QMLA_API const char *qmla_status_string(qmla_status s);
+/* Current device ordinal, its compute-unit count and gfx name (>= 16 bytes). */
+QMLA_API qmla_status qmla_device_info(int *device, int *cu_count, char *arch_name, size_t arch_len);
+
+/* ------------------------------------------------ HBM-resident buffers ---
+ * Replaces the host-only storage of src/tensor.rs:1-122 (PackedQMoETensor
+ * owns mmap'd or Vec storage) with device buffers the engine owns.        */
+QMLA_API qmla_status qmla_buffer_alloc(size_t bytes, void **out);
+QMLA_API qmla_status qmla_buffer_free(void *ptr);
+QMLA_API qmla_status qmla_memcpy_h2d(void *dst, const void *src, size_t bytes, qmla_stream stream);
+QMLA_API qmla_status qmla_memcpy_d2h(void *dst, const void *src, size_t bytes, qmla_stream stream);
+QMLA_API qmla_status qmla_memcpy_d2d(void *dst, const void *src, size_t bytes, qmla_stream stream);
+QMLA_API qmla_status qmla_memset_zero(void *dst, size_t bytes, qmla_stream stream);
+QMLA_API qmla_status qmla_stream_create(qmla_stream *out);
+QMLA_API qmla_status qmla_stream_destroy(qmla_stream stream);
+QMLA_API qmla_status qmla_stream_synchronize(qmla_stream stream);
+/* Convert n f32 values to bf16 (round to nearest even) on the device. */
+QMLA_API qmla_status qmla_f32_to_bf16(const float *src, uint16_t *dst, size_t n, qmla_stream stream);
+/* Fill n f32 values with N(mean, std^2) from a counter-based generator
+ * (a deterministic function of (seed, index); not bit-identical to any host
+ * generator).  For synthetic benchmark inputs. */
+QMLA_API qmla_status qmla_fill_normal_f32(float *dst, size_t n, uint64_t seed, float mean, float std_,
+                                 qmla_stream stream);
+
+/* ------------------------------------------- attention_kernel.rs -------- */
+typedef struct {
+  int32_t batch;        /* b                                              */
+  int32_t heads;        /* h                                              */
+  int32_t seq_q;        /* query rows per (b, h)                          */
+  int32_t seq_k;        /* key rows per (b, h)                            */
+  int32_t qk_nope;      /* dn (q_nope / k width)                          */
+  int32_t qk_rope;      /* dr (q_rope / k_rope width, may be 0)           */
+  int32_t v_dim;        /* dv                                             */
+  int32_t k_rope_heads; /* 1: one rope key shared by all heads (latent
+                           layout); heads: per-head copy (reference layout) */
+  int32_t q_offset;     /* absolute position of query row 0 in the causal
+                           mask (0 for plain prefill; cached length for a
+                           chunk appended after a cache)                   */
+} qmla_prefill_dims;
+
+/* fused_prefill_attn, src/attention_kernel.rs:64-107:
+ *   out = softmax((q_nope k^T + q_rope k_rope^T) * scale + mask) v
+ * with the causal mask of make_causal_mask (:14-31): key j is masked for
+ * query row i when q_offset + i < j.
+ *   q_nope [b,h,seq_q,dn]  q_rope [b,h,seq_q,dr]  k [b,h,seq_k,dn]
+ *   k_rope [b,k_rope_heads,seq_k,dr]  v [b,h,seq_k,dv]  out [b,h,seq_q,dv]
+ * dtype QMLA_F32: f32 in/out, f32 math (parity mode).
+ * dtype QMLA_BF16: bf16 in/out, bf16 MFMA with f32 accumulation.
+ * q_offset >= 0, so every query row sees key 0; with causal = 0, q_offset
+ * must be 0 and seq_q and seq_k may differ.  seq_k == 0 yields zeros. */
+QMLA_API qmla_status qmla_fused_prefill_attn(const qmla_prefill_dims *dims, qmla_dtype dtype,
+                                    const void *q_nope, const void *q_rope, const void *k,
+                                    const void *k_rope, const void *v, double scale, int causal,
+                                    void *out, qmla_stream stream);
+
+/* reference_eager_attn, src/attention_kernel.rs:110-134 (and the intended
+ * math of eager_prefill_attn, :34-57): single-part scores q k^T.
+ *   q, k [b,h,s,d]  v [b,h,s,dv]  out [b,h,s,dv]                          */
+QMLA_API qmla_status qmla_reference_eager_attn(int32_t b, int32_t h, int32_t s, int32_t d, int32_t dv,
+                                      qmla_dtype dtype, const void *q, const void *k,
+                                      const void *v, double scale, int causal, void *out,
+                                      qmla_stream stream);
+QMLA_API qmla_status qmla_eager_prefill_attn(int32_t b, int32_t h, int32_t s, int32_t d, int32_t dv,
+                                    qmla_dtype dtype, const void *q, const void *k,
+                                    const void *v, double scale, int causal, void *out,
+                                    qmla_stream stream);
+
+/* --------------------------------------- latent KV cache (model.rs) -----
+ * Replaces KVCache, src/model.rs:86-105 ({k, v, k_rope} decompressed
+ * per-head tensors grown by Tensor::cat on every append) with one latent row
+ * per token, [c_kv (kv_lora_rank) | k_pe (rope_dim)], stored once for all
+ * heads.  Sequence i owns rows [offset_i, offset_i + capacity_i) of one
+ * contiguous HBM pool; its current length lives in a device int32 table
+ * (mirrored on the host for validation, so no call needs a device sync).  */
+typedef struct qmla_kv_cache qmla_kv_cache;
+
+typedef struct {
+  int32_t num_seqs;
+  int32_t kv_lora_rank;
+  int32_t rope_dim;
+  qmla_dtype dtype;  /* element type of the rows                    */
+  int64_t row_elems; /* kv_lora_rank + rope_dim                      */
+  int64_t total_rows;
+  void *rows;        /* device: [total_rows, row_elems]               */
+  int64_t *offsets;  /* device: [num_seqs] first row of each sequence */
+  int32_t *lengths;  /* device: [num_seqs] current lengths            */
+  int32_t *capacity; /* device: [num_seqs]                            */
+} qmla_cache_desc;
+
+/* KVCache::new, src/model.rs:95-97.  capacity[num_seqs] is a host array of
+ * per-sequence token capacities; all lengths start at 0. */
+QMLA_API qmla_status qmla_cache_create(int32_t num_seqs, const int32_t *capacity, int32_t kv_lora_rank,
+                              int32_t rope_dim, qmla_dtype dtype, qmla_kv_cache **out);
+QMLA_API qmla_status qmla_cache_destroy(qmla_kv_cache *cache);
+/* #[derive(Clone)] on KVCache, src/model.rs:87: deep copy of rows and lengths. */
+QMLA_API qmla_status qmla_cache_clone(const qmla_kv_cache *cache, qmla_kv_cache **out, qmla_stream stream);
+/* KVCache::append, src/model.rs:99-104: appends n_new tokens to each of
+ * sequences 0..n_seqs-1.  rows [n_seqs, n_new, kv_lora_rank + rope_dim] on
+ * the device, f32 (converted to the cache dtype, bf16 by round-to-nearest-
+ * even) or already in the cache dtype (rows_dtype == cache dtype).  O(new
+ * rows) work, never a copy of the existing cache. */
+QMLA_API qmla_status qmla_cache_append(qmla_kv_cache *cache, const void *rows, qmla_dtype rows_dtype,
+                              int32_t n_seqs, int32_t n_new, qmla_stream stream);
+/* Ragged form: appends n_new rows to sequence `seq` only. */
+QMLA_API qmla_status qmla_cache_append_seq(qmla_kv_cache *cache, int32_t seq, const void *rows,
+                                  qmla_dtype rows_dtype, int32_t n_new, qmla_stream stream);
+/* Sets every sequence's length (host array [num_seqs]) without writing
+ * rows: rows past the old length keep whatever the pool holds.  Used to
+ * truncate, or after filling the pool directly through qmla_cache_describe. */
+QMLA_API qmla_status qmla_cache_set_lengths(qmla_kv_cache *cache, const int32_t *lengths,
+                                   qmla_stream stream);
+/* Length read (`cache.k.dim(2)`, src/model.rs:259) from the host mirror. */
+QMLA_API qmla_status qmla_cache_lengths(const qmla_kv_cache *cache, int32_t *lengths_out);
+QMLA_API qmla_status qmla_cache_describe(const qmla_kv_cache *cache, qmla_cache_desc *out);
+
+/* ------------------------------------------- absorbed latent decode ------
+ * The attention core of MlaAttention::forward_with_cache,
+ * src/model.rs:294-303, in absorbed form over the latent cache.  For query
+ * row m of sequence i (rows are heads x new tokens; every row attends every
+ * cached token, as :297-302 applies no mask):
+ *   s_t = scale * (q_latent[i,m] . c_t + q_rope[i,m] . kpe_t)
+ *   out_latent[i,m] = sum_t softmax(s)_t c_t,  out_lse[i,m] = logsumexp(s)
+ * q_latent [batch, rows, kv_lora_rank], q_rope [batch, rows, rope_dim] are
+ * f32 (QMLA_F32) or bf16 (QMLA_BF16); out_latent is f32 [batch, rows, r];
+ * out_lse f32 [batch, rows] or NULL.  Sequences 0..batch-1 of the cache are
+ * used with their current device lengths (a zero-length sequence yields 0
+ * and lse = -inf).  f32 cache: f32 math.  bf16 cache: bf16 MFMA, f32
+ * accumulation; q is rounded to bf16.
+ * The token range of all sequences is split evenly over the device's
+ * compute units; partial results are merged by log-sum-exp.               */
+typedef struct {
+  int32_t batch;
+  int32_t rows;         /* query rows per sequence (heads x new tokens) */
+  int32_t kv_lora_rank; /* must equal the cache's                       */
+  int32_t rope_dim;     /* must equal the cache's                       */
+} qmla_decode_dims;
+
+QMLA_API qmla_status qmla_decode_workspace_bytes(const qmla_decode_dims *dims, const qmla_kv_cache *cache,
+                                        size_t *bytes);
+QMLA_API qmla_status qmla_decode_absorbed(const qmla_decode_dims *dims, const qmla_kv_cache *cache,
+                                 qmla_dtype q_dtype, const void *q_latent, const void *q_rope,
+                                 double scale, float *out_latent, float *out_lse,
+                                 void *workspace, size_t workspace_bytes, qmla_stream stream);
+/* Same, with the number of token splits fixed by the caller (>= 1): used by
+ * the split-invariance tests and for tuning.  0 means automatic. */
+QMLA_API qmla_status qmla_decode_absorbed_splits(const qmla_decode_dims *dims, const qmla_kv_cache *cache,
+                                        qmla_dtype q_dtype, const void *q_latent,
+                                        const void *q_rope, double scale, float *out_latent,
+                                        float *out_lse, int32_t num_splits, void *workspace,
+                                        size_t workspace_bytes, qmla_stream stream);
+QMLA_API qmla_status qmla_decode_workspace_bytes_splits(const qmla_decode_dims *dims,
+                                               const qmla_kv_cache *cache, int32_t num_splits,
+                                               size_t *bytes);
+
+/* --------------------------------------------- MLA layer (model.rs) -----
+ * MlaAttention, src/model.rs:107-307, with device-resident weights.
+ * Weights are given as host f32 arrays in the reference's Linear layout
+ * ([out, in] weight, [out] bias), copied to the device at creation:
+ *   wq [H(dn+dr), hidden]   bq    q_proj              src/model.rs:126-130
+ *   wkva [r+dr, hidden]     bkva  kv_a_proj_with_mqa  src/model.rs:131-135
+ *   ln_w, ln_b [r]                kv_a_layernorm      src/model.rs:136
+ *   wkvb [H(dn+dv), r]      bkvb  kv_b_proj           src/model.rs:137-141
+ *   wo [hidden, H dv]       bo    o_proj              src/model.rs:142-146
+ * Any bias pointer may be NULL (treated as zero).                        */
+typedef struct {
+  int32_t hidden, heads, qk_nope, qk_rope, v_dim, kv_lora_rank;
+  double rope_mscale;   /* src/model.rs:160-165 (1.0857263992...)   */
+  double softmax_scale; /* src/model.rs:166-173 (0.1147213868 at 192) */
+  double ln_eps;        /* 1e-6, src/model.rs:136                     */
+} qmla_layer_config;
+
+typedef struct qmla_layer qmla_layer;
+
+/* Fills rope_mscale / softmax_scale / ln_eps from the reference's
+ * constructor (YaRN factor 40, mscale 1.0, mscale_all_dim 0.707). */
+QMLA_API qmla_status qmla_layer_default_scales(qmla_layer_config *cfg);
+QMLA_API qmla_status qmla_layer_create(const qmla_layer_config *cfg, const float *wq, const float *bq,
+                              const float *wkva, const float *bkva, const float *ln_w,
+                              const float *ln_b, const float *wkvb, const float *bkvb,
+                              const float *wo, const float *bo, qmla_layer **out);
+QMLA_API qmla_status qmla_layer_destroy(qmla_layer *layer);
+/* Device scratch needed by the two forward calls for (batch, seq) tokens
+ * attending at most max_ctx cached+new tokens. */
+QMLA_API qmla_status qmla_layer_workspace_bytes(const qmla_layer *layer, const qmla_kv_cache *cache,
+                                       int32_t batch, int32_t seq, size_t *bytes);
+/* MlaAttention::forward_with_cache, src/model.rs:256-307, over the latent
+ * cache: xs [batch, seq, hidden] f32 device, out [batch, seq, hidden] f32.
+ * Appends the seq new latent rows of sequences 0..batch-1 to the cache
+ * (positions continue from each sequence's current length, which must be
+ * equal across the batch as in the reference's uniform KVCache), then
+ * attends all cached + new tokens without a mask (as :297-302). */
+QMLA_API qmla_status qmla_layer_forward_with_cache(const qmla_layer *layer, const float *xs, int32_t batch,
+                                          int32_t seq, qmla_kv_cache *cache, float *out,
+                                          void *workspace, size_t workspace_bytes,
+                                          qmla_stream stream);
+/* MlaAttention::forward_prefill, src/model.rs:193-253: causal attention
+ * over the seq tokens, which are appended to the (empty) cache sequences
+ * 0..batch-1 -- the latent replacement of the KVCache it returns (:250). */
+QMLA_API qmla_status qmla_layer_forward_prefill(const qmla_layer *layer, const float *xs, int32_t batch,
+                                       int32_t seq, qmla_kv_cache *cache, float *out,
+                                       void *workspace, size_t workspace_bytes,
+                                       qmla_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QMLA_H */

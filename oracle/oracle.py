@@ -1,0 +1,399 @@
+"""ctypes binding of the CPU oracle (oracle/mla_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() and
+by bench.py's cpu_baseline leg, as the checker.  The product library
+(qmoe-rs_amd/) never imports this module.
+
+Every wrapper takes and returns numpy arrays in the layouts documented in
+mla_oracle.h; the C function it calls cites the reference file:line.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from dataclasses import dataclass
+
+import numpy as np
+
+_DIR = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_DIR, "liboracle.so")
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_i64p = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so with the committed Makefile."""
+    args = ["make", "-C", _DIR] + (["-B"] if force else [])
+    subprocess.run(args, check=True, stdout=subprocess.DEVNULL)
+    return _LIB_PATH
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = C.CDLL(_LIB_PATH)
+        sig = {
+            "orc_splitmix64_at": (C.c_uint64, [C.c_uint64, C.c_uint64]),
+            "orc_fill_normal": (None, [_f32p, C.c_size_t, C.c_uint64, C.c_double, C.c_double]),
+            "orc_fill_uniform_int": (None, [_i32p, C.c_size_t, C.c_uint64, C.c_int32, C.c_int32]),
+            "orc_f32_to_bf16": (C.c_uint16, [C.c_float]),
+            "orc_bf16_to_f32": (C.c_float, [C.c_uint16]),
+            "orc_to_bf16": (None, [_f32p, _u16p, C.c_size_t]),
+            "orc_round_bf16": (None, [_f32p, _f32p, C.c_size_t]),
+            "orc_yarn_get_mscale": (C.c_double, [C.c_double, C.c_double]),
+            "orc_mla_scales": (None, [C.c_int, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+            "orc_tile_size": (C.c_int, [C.c_int]),
+            "orc_rope_table": (None, [C.c_int, C.c_int, C.c_int, C.c_double, _f32p]),
+            "orc_apply_rope": (None, [_f32p, _f32p, C.c_int, C.c_int, C.c_int, _f32p]),
+            "orc_linear": (None, [_f32p, C.c_int, C.c_int, _f32p, C.c_void_p, C.c_int, _f32p]),
+            "orc_layer_norm": (None, [_f32p, C.c_int, C.c_int, _f32p, C.c_void_p, C.c_double, _f32p]),
+            "orc_softmax_rows": (None, [_f32p, C.c_long, C.c_int]),
+            "orc_reference_eager_attn": (None, [_f32p, _f32p, _f32p] + [C.c_int] * 5 + [C.c_double, C.c_int, _f32p]),
+            "orc_fused_prefill_attn": (None, [_f32p] * 5 + [C.c_int] * 9 + [C.c_double, C.c_int, _f32p]),
+            "orc_prefill_attn_f64": (None, [_f32p] * 5 + [C.c_int] * 9 + [C.c_double, C.c_int, _f64p]),
+            "orc_decode_absorbed": (None, [_f32p, _f32p, _f32p, _i64p, _i32p, C.c_int, C.c_int, C.c_int,
+                                           C.c_int, C.c_double, _f32p, C.c_void_p]),
+            "orc_decode_absorbed_f64": (None, [_f32p, _f32p, _f32p, _i64p, _i32p, C.c_int, C.c_int, C.c_int,
+                                               C.c_int, C.c_double, _f64p, C.c_void_p]),
+            "orc_num_threads": (C.c_int, []),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        vp, i_, lp = C.c_void_p, C.c_int, C.c_long
+        layer_sig = {
+            "orc_compute_kv": [vp, vp, lp, vp, vp],
+            "orc_mla_latent_rows": [vp, vp, i_, i_, i_, vp],
+            "orc_decompress_cache": [vp, vp, i_, i_, vp, vp, vp],
+            "orc_mla_forward_with_cache": [vp, vp, i_, i_, vp, vp, vp, i_, vp, vp, vp, vp],
+            "orc_mla_forward_prefill": [vp, vp, i_, i_, vp, vp, vp, vp],
+            "orc_absorb_q": [vp, vp, lp, vp],
+            "orc_unabsorb_out": [vp, vp, lp, vp],
+            "orc_mla_forward_with_latent": [vp, vp, i_, i_, vp, i_, vp, vp],
+        }
+        for name, args in layer_sig.items():
+            fn = getattr(L, name)
+            fn.restype = None
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _c(a, dtype=np.float32):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+# ------------------------------------------------------------------ RNG ----
+
+def splitmix64_at(seed: int, i: int) -> int:
+    return lib().orc_splitmix64_at(seed, i)
+
+
+def normal(shape, seed: int, std: float = 1.0, mean: float = 0.0) -> np.ndarray:
+    """SplitMix64 -> Box-Muller (fp64) -> f32, element i depends on (seed, i)."""
+    n = int(np.prod(shape)) if len(shape) else 1
+    out = np.empty(n, np.float32)
+    lib().orc_fill_normal(out, n, seed, mean, std)
+    return out.reshape(shape)
+
+
+def uniform_int(n: int, seed: int, lo: int, hi: int) -> np.ndarray:
+    out = np.empty(n, np.int32)
+    lib().orc_fill_uniform_int(out, n, seed, lo, hi)
+    return out
+
+
+def to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    x = _c(x)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_to_bf16(x.reshape(-1), out.reshape(-1), x.size)
+    return out
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    x = _c(x)
+    out = np.empty_like(x)
+    lib().orc_round_bf16(x.reshape(-1), out.reshape(-1), x.size)
+    return out
+
+
+# --------------------------------------------------------------- scalars ----
+
+def yarn_get_mscale(scale: float, mscale: float) -> float:
+    return lib().orc_yarn_get_mscale(scale, mscale)
+
+
+def mla_scales(qk_nope: int, qk_rope: int):
+    a, b = C.c_double(), C.c_double()
+    lib().orc_mla_scales(qk_nope, qk_rope, C.byref(a), C.byref(b))
+    return a.value, b.value
+
+
+def tile_size(s: int) -> int:
+    return lib().orc_tile_size(s)
+
+
+def rope_table(pos0: int, n: int, d: int, mscale: float) -> np.ndarray:
+    out = np.empty((n, d), np.float32)
+    lib().orc_rope_table(pos0, n, d, mscale, out)
+    return out
+
+
+def apply_rope(x: np.ndarray, table: np.ndarray) -> np.ndarray:
+    """x [..., s, d], table [s, d]."""
+    x = _c(x)
+    s, d = x.shape[-2], x.shape[-1]
+    outer = x.size // (s * d)
+    out = np.empty_like(x)
+    lib().orc_apply_rope(x, out, outer, s, d, _c(table))
+    return out
+
+
+def linear(x: np.ndarray, W: np.ndarray, b: np.ndarray | None) -> np.ndarray:
+    x = _c(x)
+    W = _c(W)
+    rows, n_in = x.reshape(-1, x.shape[-1]).shape
+    n_out = W.shape[0]
+    y = np.empty((rows, n_out), np.float32)
+    bb = _c(b) if b is not None else None
+    lib().orc_linear(x, rows, n_in, W, bb.ctypes.data if bb is not None else None, n_out, y)
+    return y.reshape(x.shape[:-1] + (n_out,))
+
+
+def layer_norm(x: np.ndarray, w: np.ndarray, b: np.ndarray | None, eps: float = 1e-6) -> np.ndarray:
+    x = _c(x)
+    n = x.shape[-1]
+    rows = x.size // n
+    y = np.empty_like(x)
+    bb = _c(b) if b is not None else None
+    lib().orc_layer_norm(x, rows, n, _c(w), bb.ctypes.data if bb is not None else None, eps, y)
+    return y
+
+
+def softmax_rows(x: np.ndarray) -> np.ndarray:
+    y = _c(x).copy()
+    lib().orc_softmax_rows(y, y.size // y.shape[-1], y.shape[-1])
+    return y
+
+
+# ------------------------------------------------------------- attention ----
+
+def reference_eager_attn(q, k, v, scale: float, causal: bool) -> np.ndarray:
+    q, k, v = _c(q), _c(k), _c(v)
+    b, h, s, d = q.shape
+    dv = v.shape[-1]
+    out = np.empty((b, h, s, dv), np.float32)
+    lib().orc_reference_eager_attn(q, k, v, b, h, s, d, dv, scale, int(causal), out)
+    return out
+
+
+def _prefill_args(q_nope, q_rope, k, k_rope, v):
+    q_nope, q_rope, k, k_rope, v = map(_c, (q_nope, q_rope, k, k_rope, v))
+    b, h, sq, dn = q_nope.shape
+    dr = q_rope.shape[-1]
+    sk = k.shape[2]
+    dv = v.shape[-1]
+    krh = k_rope.shape[1]
+    assert krh in (1, h)
+    return (q_nope, q_rope, k, k_rope, v), (b, h, sq, sk, dn, dr, dv, krh)
+
+
+def fused_prefill_attn(q_nope, q_rope, k, k_rope, v, scale: float, causal: bool, q_offset: int = 0):
+    arrs, (b, h, sq, sk, dn, dr, dv, krh) = _prefill_args(q_nope, q_rope, k, k_rope, v)
+    out = np.empty((b, h, sq, dv), np.float32)
+    lib().orc_fused_prefill_attn(*arrs, b, h, sq, sk, dn, dr, dv, krh, q_offset, scale, int(causal), out)
+    return out
+
+
+def prefill_attn_f64(q_nope, q_rope, k, k_rope, v, scale: float, causal: bool, q_offset: int = 0):
+    arrs, (b, h, sq, sk, dn, dr, dv, krh) = _prefill_args(q_nope, q_rope, k, k_rope, v)
+    out = np.empty((b, h, sq, dv), np.float64)
+    lib().orc_prefill_attn_f64(*arrs, b, h, sq, sk, dn, dr, dv, krh, q_offset, scale, int(causal), out)
+    return out
+
+
+def decode_absorbed(q_lat, q_rope, cache, offsets, lens, scale: float, f64: bool = False):
+    """q_lat [nseq, M, r], q_rope [nseq, M, dr], cache [rows, r+dr];
+    returns (out [nseq, M, r], lse [nseq, M])."""
+    q_lat, q_rope, cache = _c(q_lat), _c(q_rope), _c(cache)
+    offsets = np.ascontiguousarray(offsets, np.int64)
+    lens = np.ascontiguousarray(lens, np.int32)
+    nseq, M, r = q_lat.shape
+    dr = q_rope.shape[-1]
+    assert cache.shape[-1] == r + dr and r <= 1024
+    dt = np.float64 if f64 else np.float32
+    out = np.empty((nseq, M, r), dt)
+    lse = np.empty((nseq, M), dt)
+    fn = lib().orc_decode_absorbed_f64 if f64 else lib().orc_decode_absorbed
+    fn(q_lat, q_rope, cache.reshape(-1, r + dr), offsets, lens, nseq, M, r, dr, scale, out,
+       lse.ctypes.data)
+    return out, lse
+
+
+def num_threads() -> int:
+    return lib().orc_num_threads()
+
+
+# ----------------------------------------------------------- MLA layer ----
+
+class _Layer(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("hidden", "heads", "dn", "dr", "dv", "r")] + [
+        (n, C.c_void_p) for n in ("wq", "bq", "wkva", "bkva", "ln_w", "ln_b", "wkvb", "bkvb", "wo", "bo")
+    ] + [("rope_mscale", C.c_double), ("softmax_scale", C.c_double), ("ln_eps", C.c_double)]
+
+
+@dataclass
+class MlaWeights:
+    """Weights of one MlaAttention (src/model.rs:107-175), numpy f32."""
+    hidden: int
+    heads: int
+    dn: int
+    dr: int
+    dv: int
+    r: int
+    wq: np.ndarray
+    bq: np.ndarray
+    wkva: np.ndarray
+    bkva: np.ndarray
+    ln_w: np.ndarray
+    ln_b: np.ndarray
+    wkvb: np.ndarray
+    bkvb: np.ndarray
+    wo: np.ndarray
+    bo: np.ndarray
+    rope_mscale: float
+    softmax_scale: float
+    ln_eps: float = 1e-6
+
+    @staticmethod
+    def random(hidden, heads, dn, dr, dv, r, seed=1000, std=0.02, scale=None):
+        """Seeded N(0, std^2) weights and biases; LayerNorm weight 1 + N(0, std^2)."""
+        H = heads
+        rm, ss = mla_scales(dn, dr)
+        shapes = dict(wq=(H * (dn + dr), hidden), bq=(H * (dn + dr),), wkva=(r + dr, hidden),
+                      bkva=(r + dr,), ln_w=(r,), ln_b=(r,), wkvb=(H * (dn + dv), r),
+                      bkvb=(H * (dn + dv),), wo=(hidden, H * dv), bo=(hidden,))
+        arrs = {}
+        for i, (k, shp) in enumerate(shapes.items()):
+            arrs[k] = normal(shp, seed + i, std)
+        arrs["ln_w"] = (arrs["ln_w"] + 1.0).astype(np.float32)
+        return MlaWeights(hidden, heads, dn, dr, dv, r, rope_mscale=rm,
+                          softmax_scale=ss if scale is None else scale, **arrs)
+
+    def _struct(self):
+        keep = {k: _c(getattr(self, k)) for k in
+                ("wq", "bq", "wkva", "bkva", "ln_w", "ln_b", "wkvb", "bkvb", "wo", "bo")}
+        s = _Layer(self.hidden, self.heads, self.dn, self.dr, self.dv, self.r,
+                   *[keep[k].ctypes.data for k in ("wq", "bq", "wkva", "bkva", "ln_w", "ln_b",
+                                                   "wkvb", "bkvb", "wo", "bo")],
+                   self.rope_mscale, self.softmax_scale, self.ln_eps)
+        return s, keep
+
+
+def compute_kv(L: MlaWeights, c: np.ndarray):
+    c = _c(c)
+    n = c.shape[0]
+    k = np.empty((n, L.heads, L.dn), np.float32)
+    v = np.empty((n, L.heads, L.dv), np.float32)
+    s, keep = L._struct()
+    lib().orc_compute_kv(C.byref(s), c.ctypes.data, C.c_long(n), k.ctypes.data, v.ctypes.data)
+    return k, v
+
+
+def latent_rows(L: MlaWeights, xs: np.ndarray, pos0: int) -> np.ndarray:
+    xs = _c(xs)
+    b, s, _ = xs.shape
+    rows = np.empty((b, s, L.r + L.dr), np.float32)
+    st, keep = L._struct()
+    lib().orc_mla_latent_rows(C.byref(st), xs.ctypes.data, b, s, pos0, rows.ctypes.data)
+    return rows
+
+
+def decompress_cache(L: MlaWeights, latent: np.ndarray):
+    latent = _c(latent)
+    b, T, _ = latent.shape
+    H = L.heads
+    k = np.empty((b, H, T, L.dn), np.float32)
+    v = np.empty((b, H, T, L.dv), np.float32)
+    kr = np.empty((b, H, T, L.dr), np.float32)
+    st, keep = L._struct()
+    lib().orc_decompress_cache(C.byref(st), latent.ctypes.data, b, T, k.ctypes.data, v.ctypes.data,
+                               kr.ctypes.data)
+    return k, v, kr
+
+
+def mla_forward_with_cache(L: MlaWeights, xs, k, v, k_rope, return_cache=False):
+    xs, k, v, k_rope = map(_c, (xs, k, v, k_rope))
+    b, s, _ = xs.shape
+    Tc = k.shape[2]
+    H, T = L.heads, Tc + s
+    out = np.empty((b, s, L.hidden), np.float32)
+    nk = np.empty((b, H, T, L.dn), np.float32) if return_cache else None
+    nv = np.empty((b, H, T, L.dv), np.float32) if return_cache else None
+    nkr = np.empty((b, H, T, L.dr), np.float32) if return_cache else None
+    st, keep = L._struct()
+    ptr = lambda a: a.ctypes.data if a is not None else None  # noqa: E731
+    lib().orc_mla_forward_with_cache(C.byref(st), xs.ctypes.data, b, s, k.ctypes.data, v.ctypes.data,
+                                     k_rope.ctypes.data, Tc, out.ctypes.data, ptr(nk), ptr(nv), ptr(nkr))
+    return (out, (nk, nv, nkr)) if return_cache else out
+
+
+def mla_forward_prefill(L: MlaWeights, xs):
+    xs = _c(xs)
+    b, s, _ = xs.shape
+    H = L.heads
+    out = np.empty((b, s, L.hidden), np.float32)
+    k = np.empty((b, H, s, L.dn), np.float32)
+    v = np.empty((b, H, s, L.dv), np.float32)
+    kr = np.empty((b, H, s, L.dr), np.float32)
+    st, keep = L._struct()
+    lib().orc_mla_forward_prefill(C.byref(st), xs.ctypes.data, b, s, out.ctypes.data, k.ctypes.data,
+                                  v.ctypes.data, kr.ctypes.data)
+    return out, (k, v, kr)
+
+
+def absorb_q(L: MlaWeights, q_nope: np.ndarray) -> np.ndarray:
+    """q_nope [n, H, dn] -> [n, H, r]"""
+    q_nope = _c(q_nope)
+    n = q_nope.shape[0]
+    out = np.empty((n, L.heads, L.r), np.float32)
+    st, keep = L._struct()
+    lib().orc_absorb_q(C.byref(st), q_nope.ctypes.data, C.c_long(n), out.ctypes.data)
+    return out
+
+
+def unabsorb_out(L: MlaWeights, o_lat: np.ndarray) -> np.ndarray:
+    o_lat = _c(o_lat)
+    n = o_lat.shape[0]
+    out = np.empty((n, L.heads, L.dv), np.float32)
+    st, keep = L._struct()
+    lib().orc_unabsorb_out(C.byref(st), o_lat.ctypes.data, C.c_long(n), out.ctypes.data)
+    return out
+
+
+def mla_forward_with_latent(L: MlaWeights, xs, latent):
+    xs, latent = _c(xs), _c(latent)
+    b, s, _ = xs.shape
+    Tc = latent.shape[1]
+    out = np.empty((b, s, L.hidden), np.float32)
+    rows = np.empty((b, s, L.r + L.dr), np.float32)
+    st, keep = L._struct()
+    lib().orc_mla_forward_with_latent(C.byref(st), xs.ctypes.data, b, s, latent.ctypes.data, Tc,
+                                      out.ctypes.data, rows.ctypes.data)
+    return out, rows

@@ -1,0 +1,115 @@
+// internal.hpp -- objects shared between the translation units of libqmla.
+#pragma once
+
+#include <vector>
+
+#include "common.hpp"
+
+// Latent KV cache: one row [c_kv | k_pe] per token, sequence i owning rows
+// [offsets[i], offsets[i] + capacity[i]) of a single HBM pool.  Lengths are
+// kept on the device (read by kernels) and mirrored on the host (validation
+// without a device sync).
+struct qmla_kv_cache {
+  int device = 0;
+  int32_t num_seqs = 0;
+  int32_t r = 0;
+  int32_t dr = 0;
+  qmla_dtype dtype = QMLA_F32;
+  int64_t row_elems = 0;
+  int64_t total_rows = 0;
+  void *rows = nullptr;          // device [total_rows, row_elems]
+  int64_t *d_offsets = nullptr;  // device [num_seqs]
+  int32_t *d_lens = nullptr;     // device [num_seqs]
+  int32_t *d_cap = nullptr;      // device [num_seqs]
+  std::vector<int64_t> h_offsets;
+  std::vector<int32_t> h_lens;
+  std::vector<int32_t> h_cap;
+
+  size_t elem_bytes() const { return dtype == QMLA_BF16 ? 2 : 4; }
+  size_t row_bytes() const { return (size_t)row_elems * elem_bytes(); }
+};
+
+namespace qmla {
+
+inline bool valid_dtype(qmla_dtype d) { return d == QMLA_F32 || d == QMLA_BF16; }
+inline size_t dtype_bytes(qmla_dtype d) { return d == QMLA_BF16 ? 2 : 4; }
+
+// ------------------------------------------------------------ decode plan
+// The token range of sequences 0..batch-1 (concatenated, N tokens) is cut
+// into `blocks` contiguous pieces of `chunk` tokens (the last one takes the
+// remainder).  A piece may cover parts of several sequences; each (piece,
+// sequence) overlap is a segment with its own partial-result slot.
+struct DecodeSegment {
+  int32_t seq;
+  int32_t t0;    // first token (sequence-relative)
+  int32_t t1;    // one past the last token
+  int32_t slot;  // partial slot, or -1 when the segment is its sequence's only one
+};
+
+struct DecodePlanView {
+  int32_t *seg_start;      // [blocks + 1] first segment of each piece
+  DecodeSegment *segs;     // [blocks + batch]
+  int32_t *seq_slot_base;  // [batch]
+  int32_t *seq_nslots;     // [batch] 0 (empty), 1 (written directly), >= 2 (merge)
+};
+
+// Workspace layout for a decode call with `blocks` pieces:
+//   plan (seg_start, segs, seq tables), then slots x rows x r f32 partial
+//   outputs and slots x rows f32 partial log-sum-exp.
+struct DecodeWorkspace {
+  size_t plan_bytes = 0;
+  size_t part_o_off = 0;
+  size_t part_lse_off = 0;
+  size_t total = 0;
+  int32_t slots = 0;
+};
+
+DecodeWorkspace decode_workspace_layout(int32_t batch, int32_t rows, int32_t r, int32_t blocks);
+DecodePlanView decode_plan_view(void *ws, int32_t batch, int32_t blocks);
+
+qmla_status launch_decode_plan(const qmla_kv_cache *cache, int32_t batch, int32_t blocks,
+                               int32_t chunk, DecodePlanView plan, hipStream_t stream);
+qmla_status launch_decode_merge(int32_t batch, int32_t rows, int32_t r, DecodePlanView plan,
+                                const float *part_o, const float *part_lse, float *out,
+                                float *out_lse, hipStream_t stream);
+
+// Attention cores (decode_f32.hip / decode_mfma.hip).
+struct DecodeArgs {
+  const qmla_kv_cache *cache;
+  int32_t batch, rows, r, dr;
+  const void *q_lat;  // [batch, rows, r]  f32 or bf16 (q_dtype)
+  const void *q_rope; // [batch, rows, dr]
+  qmla_dtype q_dtype;
+  float scale;
+  float *out;         // [batch, rows, r]
+  float *out_lse;     // [batch, rows] or null
+  DecodePlanView plan;
+  float *part_o;
+  float *part_lse;
+  int32_t blocks;
+};
+qmla_status launch_decode_f32(const DecodeArgs &a, hipStream_t stream);
+qmla_status launch_decode_mfma(const DecodeArgs &a, hipStream_t stream);
+bool decode_mfma_supported(int32_t rows, int32_t r, int32_t dr);
+// Pieces per compute unit the MFMA decode kernel runs concurrently.
+int decode_mfma_blocks_per_cu(int32_t rows);
+
+// Prefill attention (prefill_*.hip).
+qmla_status launch_prefill_f32(const qmla_prefill_dims &d, const float *q_nope,
+                               const float *q_rope, const float *k, const float *k_rope,
+                               const float *v, float scale, int causal, float *out,
+                               hipStream_t stream);
+qmla_status launch_prefill_bf16(const qmla_prefill_dims &d, const uint16_t *q_nope,
+                                const uint16_t *q_rope, const uint16_t *k,
+                                const uint16_t *k_rope, const uint16_t *v, float scale,
+                                int causal, uint16_t *out, hipStream_t stream);
+
+// Cache row writer shared by the cache API and the layer: copies/converts
+// n_seqs x n_new rows (row-major [n_seqs, n_new, row_elems]) into sequences
+// seq0 .. seq0 + n_seqs - 1 at their current device lengths, then advances
+// those lengths by n_new.
+qmla_status launch_cache_append(qmla_kv_cache *cache, const void *rows, qmla_dtype rows_dtype,
+                                int32_t seq0, int32_t n_seqs, int32_t n_new, hipStream_t stream);
+qmla_status check_append(const qmla_kv_cache *cache, int32_t seq0, int32_t n_seqs, int32_t n_new);
+
+}  // namespace qmla

@@ -1,0 +1,518 @@
+// layer.hip -- MlaAttention (src/model.rs:107-307) with device-resident
+// weights, in f32.
+//
+// forward_with_cache (src/model.rs:256-307) runs in absorbed form over the
+// latent cache:
+//   q = xs Wq^T + bq; q_rope roped at positions len + i       (:263-267)
+//   kv_a = xs Wkva^T + bkva; c = LayerNorm(kv_a[:r]);
+//   k_pe = rope(kv_a[r:])                                      (:270-288)
+//   append [c | k_pe] to the latent cache                      (:291)
+//   q_lat[h] = W_UK^h^T q_nope[h]       (W_UK^h = kv_b rows [h(dn+dv), +dn))
+//   o_lat = absorbed attention core (decode.hip)               (:294-303)
+//   o[h] = W_UV^h o_lat[h] + b_V^h ; out = o Wo^T + bo         (:303-306)
+// The b_K part of kv_b's bias adds q_nope . b_K^h to every score of a row,
+// a constant that softmax removes, so it never enters the absorbed form.
+//
+// forward_prefill (src/model.rs:193-253) decompresses K and V for the new
+// tokens (compute_kv, :178-190) and runs the causal prefill kernel with the
+// rope key stored once (k_rope_heads = 1) instead of broadcast per head.
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "internal.hpp"
+
+struct qmla_layer {
+  qmla_layer_config cfg{};
+  float *wq = nullptr, *bq = nullptr, *wkva = nullptr, *bkva = nullptr, *ln_w = nullptr,
+        *ln_b = nullptr, *wkvb = nullptr, *bkvb = nullptr, *wo = nullptr, *bo = nullptr;
+  float *inv_freq = nullptr;  // [dr / 2], src/model.rs:56-58
+  std::vector<void *> allocs;
+};
+
+namespace qmla {
+
+namespace {
+
+// ------------------------------------------------------------ f32 GEMM
+// C[z][m][n] = sum_k A[z][m][k] * B[z][k][n] (+ bias[z][n]); B is read as
+// B[k][n] = Bt[n][k] when TRANS_B (the Linear layout W[out][in]).
+// 64x64 tiles, 256 threads, 4x4 outputs per thread.
+struct GemmArgs {
+  const float *A;
+  const float *B;
+  const float *bias;
+  float *C;
+  int M, N, K;
+  int64_t lda, ldb, ldc;
+  int64_t sA, sB, sC, sBias;  // per-z strides
+};
+
+template <bool TRANS_B>
+__global__ __launch_bounds__(256) void k_gemm_f32(GemmArgs g) {
+  __shared__ float As[16][64 + 4];
+  __shared__ float Bs[16][64 + 4];
+  const int z = blockIdx.z;
+  const float *A = g.A + z * g.sA;
+  const float *B = g.B + z * g.sB;
+  float *C = g.C + z * g.sC;
+  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < g.K; k0 += 16) {
+    for (int e = tid; e < 16 * 64; e += 256) {
+      const int kk = e & 15, mm = e >> 4;
+      const int m = m0 + mm, k = k0 + kk;
+      As[kk][mm] = (m < g.M && k < g.K) ? A[m * g.lda + k] : 0.f;
+    }
+    for (int e = tid; e < 16 * 64; e += 256) {
+      float x;
+      int kk, nn;
+      if (TRANS_B) {
+        kk = e & 15;
+        nn = e >> 4;
+      } else {
+        nn = e & 63;
+        kk = e >> 6;
+      }
+      const int n = n0 + nn, k = k0 + kk;
+      if (n < g.N && k < g.K)
+        x = TRANS_B ? B[n * g.ldb + k] : B[k * g.ldb + n];
+      else
+        x = 0.f;
+      Bs[kk][nn] = x;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = As[kk][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+  const float *bias = g.bias ? g.bias + z * g.sBias : nullptr;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + ty * 4 + i;
+    if (m >= g.M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + tx * 4 + j;
+      if (n < g.N) C[m * g.ldc + n] = acc[i][j] + (bias ? bias[n] : 0.f);
+    }
+  }
+}
+
+qmla_status gemm(const GemmArgs &g, int batch, bool trans_b, hipStream_t s) {
+  if (g.M == 0 || g.N == 0) return QMLA_OK;
+  dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, batch), block(256);
+  QMLA_REQUIRE(grid.y <= 65535 && batch <= 65535, QMLA_ERR_SHAPE, "GEMM too large");
+  if (trans_b)
+    k_gemm_f32<true><<<grid, block, 0, s>>>(g);
+  else
+    k_gemm_f32<false><<<grid, block, 0, s>>>(g);
+  QMLA_LAUNCH_CHECK("k_gemm_f32");
+  return QMLA_OK;
+}
+
+// y = x W^T + b for x [M, K], W [N, K] (candle_nn::Linear)
+qmla_status linear(const float *x, int M, int K, const float *W, const float *b, int N, float *y,
+                   hipStream_t s) {
+  GemmArgs g{x, W, b, y, M, N, K, K, K, N, 0, 0, 0, 0};
+  return gemm(g, 1, true, s);
+}
+
+__device__ inline float block_sum(float v, float *red) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  __syncthreads();
+  if (l == 0) red[w] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) t += red[i];
+  return t;
+}
+
+// Latent rows of new tokens: one block per token (b, i).
+//   rows[b,i] = [LayerNorm(kva[b,i,:r]) | rope(kva[b,i,r:], pos0 + i)]
+// LayerNorm as candle_nn::LayerNorm (src/model.rs:136): mean, biased
+// variance of the centred values, divide by sqrt(var + eps), weight, bias.
+__global__ __launch_bounds__(256) void k_latent_rows(const float *__restrict__ kva, int s, int r,
+                                                     int dr, const float *__restrict__ ln_w,
+                                                     const float *__restrict__ ln_b, float eps,
+                                                     const float *__restrict__ inv_freq,
+                                                     float mscale, int pos0,
+                                                     float *__restrict__ rows) {
+  __shared__ float red[8];
+  const int tok = blockIdx.x, i = tok % s;
+  const float *x = kva + (int64_t)tok * (r + dr);
+  float *y = rows + (int64_t)tok * (r + dr);
+  float sum = 0.f;
+  for (int c = threadIdx.x; c < r; c += blockDim.x) sum += x[c];
+  const float mean = block_sum(sum, red) / (float)r;
+  float sq = 0.f;
+  for (int c = threadIdx.x; c < r; c += blockDim.x) {
+    const float d = x[c] - mean;
+    sq += d * d;
+  }
+  const float var = block_sum(sq, red) / (float)r;
+  const float den = sqrtf(var + eps);
+  for (int c = threadIdx.x; c < r; c += blockDim.x) {
+    const float t = (x[c] - mean) / den * ln_w[c];
+    y[c] = ln_b ? t + ln_b[c] : t;
+  }
+  const float pos = (float)(pos0 + i);
+  for (int p = threadIdx.x; p < dr / 2; p += blockDim.x) {
+    const float ang = pos * inv_freq[p];
+    const float cs = cosf(ang) * mscale, sn = sinf(ang) * mscale;
+    const float e = x[r + 2 * p], o = x[r + 2 * p + 1];
+    y[r + 2 * p] = e * cs - o * sn;
+    y[r + 2 * p + 1] = o * cs + e * sn;
+  }
+}
+
+// Split q [b*s, H, dn+dr] into q_nope and roped q_rope (src/model.rs:263-267
+// and :199-203).  Output layouts are selected by `bhs`:
+//   bhs = 0: q_nope [b, s, H, dn], q_rope [b, s, H, dr]  (decode rows i*H + h)
+//   bhs = 1: q_nope [b, H, s, dn], q_rope [b, H, s, dr]  (prefill layout)
+__global__ __launch_bounds__(64) void k_split_rope_q(const float *__restrict__ q, int s, int H,
+                                                      int dn, int dr,
+                                                      const float *__restrict__ inv_freq,
+                                                      float mscale, int pos0, int bhs,
+                                                      float *__restrict__ q_nope,
+                                                      float *__restrict__ q_rope) {
+  const int tok = blockIdx.x, h = blockIdx.y;
+  const int b = tok / s, i = tok % s;
+  const float *src = q + ((int64_t)tok * H + h) * (dn + dr);
+  const int64_t o = bhs ? ((int64_t)b * H + h) * s + i : (int64_t)tok * H + h;
+  for (int c = threadIdx.x; c < dn; c += blockDim.x) q_nope[o * dn + c] = src[c];
+  const float pos = (float)(pos0 + i);
+  for (int p = threadIdx.x; p < dr / 2; p += blockDim.x) {
+    const float ang = pos * inv_freq[p];
+    const float cs = cosf(ang) * mscale, sn = sinf(ang) * mscale;
+    const float e = src[dn + 2 * p], od = src[dn + 2 * p + 1];
+    q_rope[o * dr + 2 * p] = e * cs - od * sn;
+    q_rope[o * dr + 2 * p + 1] = od * cs + e * sn;
+  }
+}
+
+// kvb [b*s, H, dn+dv] -> k [b, H, s, dn], v [b, H, s, dv]  (compute_kv's
+// reshape + transpose, src/model.rs:181-188 and :213-215)
+__global__ __launch_bounds__(128) void k_split_kv(const float *__restrict__ kvb, int s, int H,
+                                                   int dn, int dv, float *__restrict__ k,
+                                                   float *__restrict__ v) {
+  const int tok = blockIdx.x, h = blockIdx.y;
+  const int b = tok / s, i = tok % s;
+  const float *src = kvb + ((int64_t)tok * H + h) * (dn + dv);
+  const int64_t o = ((int64_t)b * H + h) * s + i;
+  for (int c = threadIdx.x; c < dn; c += blockDim.x) k[o * dn + c] = src[c];
+  for (int c = threadIdx.x; c < dv; c += blockDim.x) v[o * dv + c] = src[dn + c];
+}
+
+// rows [b*s, r+dr] -> k_rope [b, 1, s, dr]
+__global__ __launch_bounds__(64) void k_rows_rope(const float *__restrict__ rows, int r, int dr,
+                                                   float *__restrict__ k_rope) {
+  const int tok = blockIdx.x;
+  for (int c = threadIdx.x; c < dr; c += blockDim.x)
+    k_rope[(int64_t)tok * dr + c] = rows[(int64_t)tok * (r + dr) + r + c];
+}
+
+// ctx [b, H, s, dv] -> [b, s, H*dv]  (src/model.rs:248)
+__global__ __launch_bounds__(128) void k_merge_heads(const float *__restrict__ ctx, int s, int H,
+                                                      int dv, float *__restrict__ o) {
+  const int tok = blockIdx.x, h = blockIdx.y;
+  const int b = tok / s, i = tok % s;
+  const float *src = ctx + (((int64_t)b * H + h) * s + i) * dv;
+  float *dst = o + ((int64_t)tok * H + h) * dv;
+  for (int c = threadIdx.x; c < dv; c += blockDim.x) dst[c] = src[c];
+}
+
+inline size_t al(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct LayerWs {
+  size_t q, kva, rows, qn, qr, qlat, olat, o, dec, kvb, k, v, kr, ctx, total;
+};
+
+// Scratch carve-up shared by the size query and the two forward calls.
+LayerWs layer_ws(const qmla_layer *L, const qmla_kv_cache *c, int32_t batch, int32_t seq,
+                 size_t dec_bytes) {
+  const auto &g = L->cfg;
+  const size_t n = (size_t)batch * seq, H = g.heads;
+  LayerWs w{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t o = off;
+    off += al(bytes);
+    return o;
+  };
+  w.q = take(sizeof(float) * n * H * (g.qk_nope + g.qk_rope));
+  w.kva = take(sizeof(float) * n * (g.kv_lora_rank + g.qk_rope));
+  w.rows = take(sizeof(float) * n * (g.kv_lora_rank + g.qk_rope));
+  w.qn = take(sizeof(float) * n * H * g.qk_nope);
+  w.qr = take(sizeof(float) * n * H * g.qk_rope + 4);
+  w.qlat = take(sizeof(float) * n * H * g.kv_lora_rank);
+  w.olat = take(sizeof(float) * n * H * g.kv_lora_rank);
+  w.o = take(sizeof(float) * n * H * g.v_dim);
+  w.dec = take(dec_bytes);
+  w.kvb = take(sizeof(float) * n * H * (g.qk_nope + g.v_dim));
+  w.k = take(sizeof(float) * n * H * g.qk_nope);
+  w.v = take(sizeof(float) * n * H * g.v_dim);
+  w.kr = take(sizeof(float) * n * g.qk_rope + 4);
+  w.ctx = take(sizeof(float) * n * H * g.v_dim);
+  w.total = off;
+  (void)c;
+  return w;
+}
+
+qmla_status check_layer_call(const qmla_layer *L, const float *xs, int32_t batch, int32_t seq,
+                             const qmla_kv_cache *c, const float *out) {
+  QMLA_REQUIRE(L && c, QMLA_ERR_INVALID_ARG, "NULL layer or cache");
+  QMLA_REQUIRE(batch > 0 && seq > 0, QMLA_ERR_SHAPE, "batch and seq must be > 0");
+  QMLA_REQUIRE(xs && out, QMLA_ERR_INVALID_ARG, "NULL xs or out");
+  QMLA_REQUIRE(batch <= c->num_seqs, QMLA_ERR_SHAPE, "batch %d > cache sequences %d", batch,
+               c->num_seqs);
+  QMLA_REQUIRE(c->r == L->cfg.kv_lora_rank && c->dr == L->cfg.qk_rope, QMLA_ERR_SHAPE,
+               "cache latent dims (%d, %d) differ from the layer's (%d, %d)", c->r, c->dr,
+               L->cfg.kv_lora_rank, L->cfg.qk_rope);
+  for (int32_t i = 1; i < batch; ++i)
+    QMLA_REQUIRE(c->h_lens[i] == c->h_lens[0], QMLA_ERR_SHAPE,
+                 "sequence lengths differ (%d vs %d): the layer API takes a uniform batch",
+                 c->h_lens[i], c->h_lens[0]);
+  return QMLA_OK;
+}
+
+size_t decode_bytes_for(const qmla_layer *L, const qmla_kv_cache *c, int32_t batch,
+                        int32_t seq) {
+  // Pieces are chosen from the lengths after the append; the decode call in
+  // forward_with_cache sees exactly these lengths.
+  int64_t total = 0;
+  for (int32_t i = 0; i < batch; ++i) total += c->h_lens[i] + seq;
+  int cus = device_cu_count();
+  if (cus <= 0) cus = 256;
+  int64_t blocks = std::max<int64_t>(1, std::min<int64_t>((int64_t)cus * 4, (total + 255) / 256));
+  (void)L;
+  return decode_workspace_layout(batch, seq * L->cfg.heads, L->cfg.kv_lora_rank, (int32_t)blocks)
+      .total;
+}
+
+}  // namespace
+}  // namespace qmla
+
+using namespace qmla;
+
+extern "C" {
+
+qmla_status qmla_layer_default_scales(qmla_layer_config *cfg) {
+  QMLA_REQUIRE(cfg, QMLA_ERR_INVALID_ARG, "cfg is NULL");
+  // src/model.rs:46-52 and :160-173
+  auto mscale = [](double scale, double m) { return scale <= 1.0 ? 1.0 : 0.1 * m * std::log(scale) + 1.0; };
+  const double factor = 40.0;
+  cfg->rope_mscale = mscale(factor, 1.0) / mscale(factor, 0.707);
+  const double m = mscale(factor, 0.707);
+  cfg->softmax_scale = std::pow((double)(cfg->qk_nope + cfg->qk_rope), -0.5) * m * m;
+  cfg->ln_eps = 1e-6;
+  return QMLA_OK;
+}
+
+qmla_status qmla_layer_create(const qmla_layer_config *cfg, const float *wq, const float *bq,
+                              const float *wkva, const float *bkva, const float *ln_w,
+                              const float *ln_b, const float *wkvb, const float *bkvb,
+                              const float *wo, const float *bo, qmla_layer **out) {
+  QMLA_REQUIRE(cfg && out, QMLA_ERR_INVALID_ARG, "NULL cfg or out");
+  *out = nullptr;
+  QMLA_REQUIRE(wq && wkva && ln_w && wkvb && wo, QMLA_ERR_INVALID_ARG, "NULL weight");
+  const auto &g = *cfg;
+  QMLA_REQUIRE(g.hidden > 0 && g.heads > 0 && g.qk_nope > 0 && g.qk_rope >= 0 && g.v_dim > 0 &&
+                   g.kv_lora_rank > 0,
+               QMLA_ERR_SHAPE, "bad layer dims");
+  QMLA_REQUIRE(g.qk_rope % 2 == 0, QMLA_ERR_SHAPE, "qk_rope must be even");
+  QMLA_REQUIRE((g.kv_lora_rank + g.qk_rope) % 8 == 0, QMLA_ERR_UNSUPPORTED,
+               "kv_lora_rank + qk_rope must be a multiple of 8");
+  qmla_layer *L = new (std::nothrow) qmla_layer();
+  QMLA_REQUIRE(L, QMLA_ERR_OOM, "host allocation failed");
+  L->cfg = g;
+  const int H = g.heads;
+  struct W {
+    float **dst;
+    const float *src;
+    size_t n;
+  } ws[] = {
+      {&L->wq, wq, (size_t)H * (g.qk_nope + g.qk_rope) * g.hidden},
+      {&L->bq, bq, (size_t)H * (g.qk_nope + g.qk_rope)},
+      {&L->wkva, wkva, (size_t)(g.kv_lora_rank + g.qk_rope) * g.hidden},
+      {&L->bkva, bkva, (size_t)(g.kv_lora_rank + g.qk_rope)},
+      {&L->ln_w, ln_w, (size_t)g.kv_lora_rank},
+      {&L->ln_b, ln_b, (size_t)g.kv_lora_rank},
+      {&L->wkvb, wkvb, (size_t)H * (g.qk_nope + g.v_dim) * g.kv_lora_rank},
+      {&L->bkvb, bkvb, (size_t)H * (g.qk_nope + g.v_dim)},
+      {&L->wo, wo, (size_t)g.hidden * H * g.v_dim},
+      {&L->bo, bo, (size_t)g.hidden},
+  };
+  qmla_status st = QMLA_OK;
+  for (auto &w : ws) {
+    if (!w.src) continue;  // optional bias
+    void *p = nullptr;
+    if (hipMalloc(&p, w.n * sizeof(float)) != hipSuccess) {
+      st = fail(QMLA_ERR_OOM, "weight allocation failed");
+      break;
+    }
+    L->allocs.push_back(p);
+    *w.dst = static_cast<float *>(p);
+    if (hipMemcpy(p, w.src, w.n * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
+      st = fail(QMLA_ERR_HIP, "weight upload failed");
+      break;
+    }
+  }
+  if (st == QMLA_OK && g.qk_rope > 0) {
+    // inv_freq[i] = 1.0f / (float)10000^(2i/d)  (src/model.rs:56-58)
+    std::vector<float> inv(g.qk_rope / 2);
+    for (int i = 0; i < g.qk_rope / 2; ++i)
+      inv[i] = 1.0f / (float)std::pow(10000.0, 2.0 * i / (double)g.qk_rope);
+    void *p = nullptr;
+    if (hipMalloc(&p, inv.size() * sizeof(float)) != hipSuccess ||
+        hipMemcpy(p, inv.data(), inv.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
+      st = fail(QMLA_ERR_HIP, "inv_freq upload failed");
+    if (p) L->allocs.push_back(p);
+    L->inv_freq = static_cast<float *>(p);
+  }
+  if (st != QMLA_OK) {
+    for (void *p : L->allocs) (void)hipFree(p);
+    delete L;
+    return st;
+  }
+  *out = L;
+  return QMLA_OK;
+}
+
+qmla_status qmla_layer_destroy(qmla_layer *layer) {
+  if (!layer) return QMLA_OK;
+  for (void *p : layer->allocs) (void)hipFree(p);
+  delete layer;
+  return QMLA_OK;
+}
+
+qmla_status qmla_layer_workspace_bytes(const qmla_layer *layer, const qmla_kv_cache *cache,
+                                       int32_t batch, int32_t seq, size_t *bytes) {
+  QMLA_REQUIRE(layer && cache && bytes, QMLA_ERR_INVALID_ARG, "NULL pointer");
+  QMLA_REQUIRE(batch > 0 && seq > 0 && batch <= cache->num_seqs, QMLA_ERR_SHAPE,
+               "bad batch/seq");
+  *bytes = layer_ws(layer, cache, batch, seq, decode_bytes_for(layer, cache, batch, seq)).total;
+  return QMLA_OK;
+}
+
+qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, int32_t batch,
+                                          int32_t seq, qmla_kv_cache *cache, float *out,
+                                          void *workspace, size_t workspace_bytes,
+                                          qmla_stream stream) {
+  QMLA_TRY(check_layer_call(L, xs, batch, seq, cache, out));
+  QMLA_REQUIRE(cache->dtype == QMLA_F32, QMLA_ERR_UNSUPPORTED,
+               "the f32 layer needs an f32 latent cache");
+  QMLA_TRY(check_append(cache, 0, batch, seq));
+  const auto &g = L->cfg;
+  const int H = g.heads, dn = g.qk_nope, dr = g.qk_rope, dv = g.v_dim, r = g.kv_lora_rank;
+  const size_t dec_bytes = decode_bytes_for(L, cache, batch, seq);
+  const LayerWs w = layer_ws(L, cache, batch, seq, dec_bytes);
+  QMLA_REQUIRE(workspace && workspace_bytes >= w.total, QMLA_ERR_WORKSPACE,
+               "workspace of %zu bytes < required %zu", workspace_bytes, w.total);
+  char *ws = static_cast<char *>(workspace);
+  float *q = (float *)(ws + w.q), *kva = (float *)(ws + w.kva), *rows = (float *)(ws + w.rows);
+  float *qn = (float *)(ws + w.qn), *qr = (float *)(ws + w.qr), *qlat = (float *)(ws + w.qlat);
+  float *olat = (float *)(ws + w.olat), *o = (float *)(ws + w.o);
+  hipStream_t s = as_stream(stream);
+  const int n = batch * seq;
+  const int pos0 = cache->h_lens[0];
+
+  QMLA_TRY(linear(xs, n, g.hidden, L->wq, L->bq, H * (dn + dr), q, s));
+  QMLA_TRY(linear(xs, n, g.hidden, L->wkva, L->bkva, r + dr, kva, s));
+  k_latent_rows<<<dim3(n), dim3(256), 0, s>>>(kva, seq, r, dr, L->ln_w, L->ln_b, (float)g.ln_eps,
+                                              L->inv_freq, (float)g.rope_mscale, pos0, rows);
+  QMLA_LAUNCH_CHECK("k_latent_rows");
+  k_split_rope_q<<<dim3(n, H), dim3(64), 0, s>>>(q, seq, H, dn, dr, L->inv_freq,
+                                                (float)g.rope_mscale, pos0, 0, qn, qr);
+  QMLA_LAUNCH_CHECK("k_split_rope_q");
+  // q_lat[t, h, :] = q_nope[t, h, :] W_UK^h   (batched over heads)
+  {
+    GemmArgs a{qn, L->wkvb, nullptr, qlat, n, r, dn, (int64_t)H * dn, r, (int64_t)H * r,
+               dn, (int64_t)(dn + dv) * r, r, 0};
+    QMLA_TRY(gemm(a, H, false, s));
+  }
+  QMLA_TRY(launch_cache_append(cache, rows, QMLA_F32, 0, batch, seq, s));
+  qmla_decode_dims dd{batch, seq * H, r, dr};
+  QMLA_TRY(qmla_decode_absorbed(&dd, cache, QMLA_F32, qlat, qr, g.softmax_scale, olat, nullptr,
+                                ws + w.dec, dec_bytes, stream));
+  // o[t, h, :] = W_UV^h o_lat[t, h, :] + b_V^h
+  {
+    GemmArgs a{olat, L->wkvb + (size_t)dn * r, L->bkvb ? L->bkvb + dn : nullptr, o, n, dv, r,
+               (int64_t)H * r, r, (int64_t)H * dv, r, (int64_t)(dn + dv) * r, dv,
+               (int64_t)(dn + dv)};
+    QMLA_TRY(gemm(a, H, true, s));
+  }
+  QMLA_TRY(linear(o, n, H * dv, L->wo, L->bo, g.hidden, out, s));
+  return QMLA_OK;
+}
+
+qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int32_t batch,
+                                       int32_t seq, qmla_kv_cache *cache, float *out,
+                                       void *workspace, size_t workspace_bytes,
+                                       qmla_stream stream) {
+  QMLA_TRY(check_layer_call(L, xs, batch, seq, cache, out));
+  QMLA_REQUIRE(cache->dtype == QMLA_F32 || cache->dtype == QMLA_BF16, QMLA_ERR_UNSUPPORTED,
+               "bad cache dtype");
+  QMLA_REQUIRE(cache->h_lens[0] == 0, QMLA_ERR_SHAPE,
+               "forward_prefill starts a sequence: cache lengths must be 0 (got %d)",
+               cache->h_lens[0]);
+  QMLA_TRY(check_append(cache, 0, batch, seq));
+  const auto &g = L->cfg;
+  const int H = g.heads, dn = g.qk_nope, dr = g.qk_rope, dv = g.v_dim, r = g.kv_lora_rank;
+  const LayerWs w = layer_ws(L, cache, batch, seq, decode_bytes_for(L, cache, batch, seq));
+  QMLA_REQUIRE(workspace && workspace_bytes >= w.total, QMLA_ERR_WORKSPACE,
+               "workspace of %zu bytes < required %zu", workspace_bytes, w.total);
+  char *ws = static_cast<char *>(workspace);
+  float *q = (float *)(ws + w.q), *kva = (float *)(ws + w.kva), *rows = (float *)(ws + w.rows);
+  float *qn = (float *)(ws + w.qn), *qr = (float *)(ws + w.qr), *kvb = (float *)(ws + w.kvb);
+  float *k = (float *)(ws + w.k), *v = (float *)(ws + w.v), *kr = (float *)(ws + w.kr);
+  float *ctx = (float *)(ws + w.ctx), *o = (float *)(ws + w.o);
+  hipStream_t s = as_stream(stream);
+  const int n = batch * seq;
+
+  QMLA_TRY(linear(xs, n, g.hidden, L->wq, L->bq, H * (dn + dr), q, s));
+  QMLA_TRY(linear(xs, n, g.hidden, L->wkva, L->bkva, r + dr, kva, s));
+  k_latent_rows<<<dim3(n), dim3(256), 0, s>>>(kva, seq, r, dr, L->ln_w, L->ln_b, (float)g.ln_eps,
+                                              L->inv_freq, (float)g.rope_mscale, 0, rows);
+  QMLA_LAUNCH_CHECK("k_latent_rows");
+  k_split_rope_q<<<dim3(n, H), dim3(64), 0, s>>>(q, seq, H, dn, dr, L->inv_freq,
+                                                (float)g.rope_mscale, 0, 1, qn, qr);
+  QMLA_LAUNCH_CHECK("k_split_rope_q");
+  // compute_kv on the LayerNorm'd latent (src/model.rs:178-190)
+  {
+    GemmArgs a{rows, L->wkvb, L->bkvb, kvb, n, H * (dn + dv), r, r + dr, r, (int64_t)H * (dn + dv),
+               0, 0, 0, 0};
+    QMLA_TRY(gemm(a, 1, true, s));
+  }
+  k_split_kv<<<dim3(n, H), dim3(128), 0, s>>>(kvb, seq, H, dn, dv, k, v);
+  QMLA_LAUNCH_CHECK("k_split_kv");
+  if (dr > 0) {
+    k_rows_rope<<<dim3(n), dim3(64), 0, s>>>(rows, r, dr, kr);
+    QMLA_LAUNCH_CHECK("k_rows_rope");
+  }
+  qmla_prefill_dims pd{batch, H, seq, seq, dn, dr, dv, 1, 0};
+  QMLA_TRY(launch_prefill_f32(pd, qn, qr, k, kr, v, (float)g.softmax_scale, 1, ctx, s));
+  k_merge_heads<<<dim3(n, H), dim3(128), 0, s>>>(ctx, seq, H, dv, o);
+  QMLA_LAUNCH_CHECK("k_merge_heads");
+  QMLA_TRY(linear(o, n, H * dv, L->wo, L->bo, g.hidden, out, s));
+  // the latent replacement of the KVCache returned at src/model.rs:250
+  QMLA_TRY(launch_cache_append(cache, rows, QMLA_F32, 0, batch, seq, s));
+  return QMLA_OK;
+}
+
+}  // extern "C"

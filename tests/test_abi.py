@@ -1,0 +1,69 @@
+"""CPU checks of the C ABI boundary: the library loads, exports exactly what
+include/qmla.h declares, and validates arguments before touching a device.
+No compute call is made here (there is no GPU on the build host)."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import pytest
+
+import qmla
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "qmla.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"QMLA_API\s+[\w\s\*]*?\b(qmla_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    syms = header_symbols()
+    for required in ("qmla_fused_prefill_attn", "qmla_reference_eager_attn", "qmla_eager_prefill_attn",
+                     "qmla_cache_create", "qmla_cache_append", "qmla_cache_clone", "qmla_cache_lengths",
+                     "qmla_decode_absorbed", "qmla_decode_workspace_bytes", "qmla_layer_forward_with_cache",
+                     "qmla_layer_forward_prefill", "qmla_last_error"):
+        assert required in syms
+
+
+def test_library_exports_every_declared_symbol():
+    if not os.path.exists(qmla.LIB_PATH):
+        pytest.fail("libqmla.so is not built (run __graft_entry__.build())")
+    out = subprocess.run(["nm", "-D", "--defined-only", qmla.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\bT (qmla_\w+)$", out, re.M))
+    declared = set(header_symbols())
+    assert declared - exported == set(), f"declared but not exported: {declared - exported}"
+    assert exported - declared == set(), f"exported but not declared: {exported - declared}"
+    # and the Python binding knows every one of them
+    assert declared == set(qmla.SIGNATURES)
+
+
+def test_library_loads_and_reports_errors_without_a_device():
+    L = qmla.lib()
+    assert L.qmla_version() == 100
+    assert L.qmla_status_string(6) == b"QMLA_ERR_CAPACITY"
+    # argument validation happens before any HIP call
+    assert L.qmla_fused_prefill_attn(None, 0, None, None, None, None, None, 1.0, 1, None, None) == 1
+    assert b"dims is NULL" in L.qmla_last_error()
+    dims = qmla.PrefillDims(1, 2, 4, 4, 16, 8, 16, 3, 0)  # k_rope_heads 3 is neither 1 nor heads
+    st = L.qmla_fused_prefill_attn(C.byref(dims), 0, 1, 1, 1, 1, 1, 1.0, 1, 1, None)
+    assert st == 2 and b"k_rope_heads" in L.qmla_last_error()
+    dims = qmla.PrefillDims(1, 2, 4, 4, 16, 8, 16, 1, -3)
+    assert L.qmla_fused_prefill_attn(C.byref(dims), 0, 1, 1, 1, 1, 1, 1.0, 1, 1, None) == 2
+    dims = qmla.PrefillDims(1, 2, 4, 4, 16, 8, 16, 1, 0)
+    assert L.qmla_fused_prefill_attn(C.byref(dims), 7, 1, 1, 1, 1, 1, 1.0, 1, 1, None) == 1
+    assert L.qmla_fused_prefill_attn(C.byref(dims), 0, 1, 1, 1, 1, 1, float("nan"), 1, 1, None) == 1
+    assert L.qmla_cache_create(0, None, 512, 64, 1, None) == 1
+    h = C.c_void_p()
+    caps = (C.c_int32 * 2)(4, 4)
+    assert L.qmla_cache_create(2, caps, 500, 64, 1, C.byref(h)) == 3  # 564 % 8 != 0
+    assert L.qmla_decode_absorbed(None, None, 0, None, None, 1.0, None, None, None, 0, None) == 1
+
+
+def test_oracle_library_builds_and_loads():
+    import oracle
+    oracle.build(force=False)
+    assert oracle.lib().orc_tile_size(2049) == 16

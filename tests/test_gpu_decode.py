@@ -1,0 +1,176 @@
+"""GPU parity tests of the absorbed-latent decode core (qmla_decode_absorbed),
+the attention core of MlaAttention::forward_with_cache (src/model.rs:294-303)
+rewritten over the latent cache.
+
+Tolerances (max |gpu - ref| / max |ref|): 1e-4 for the f32 cache, 2e-2 for
+the bf16 cache (bf16 MFMA, f32 accumulate), as the north-star contract
+states.  The reference side is the CPU oracle (oracle/mla_oracle.c) on the
+same inputs (the bf16 cache values exactly, q unrounded)."""
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import bf16_bits, bf16_to_f32, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32, TOL_BF16 = 1e-4, 2e-2
+
+
+def make_cache(q, lens, r, dr, dtype, seed, cap_extra=0):
+    """Cache whose sequence i holds lens[i] N(0,1) rows (host generated)."""
+    lens = np.asarray(lens, np.int32)
+    cache = q.KVCache(lens + cap_extra, r, dr, dtype)
+    total = int((lens + cap_extra).sum())
+    rows = O.normal((total, r + dr), seed)
+    if dtype == q.BF16:
+        bits = bf16_bits(rows)
+        cache.write_pool(bits)
+        rows = bf16_to_f32(bits)
+    else:
+        cache.write_pool(rows)
+    cache.set_lengths(lens)
+    offs = np.concatenate([[0], np.cumsum(lens + cap_extra)[:-1]]).astype(np.int64)
+    return cache, rows, offs
+
+
+def run(q, cache, ql, qr, scale, splits=0, q_dtype=None):
+    q_dtype = q.F32 if q_dtype is None else q_dtype
+    if q_dtype == q.BF16:
+        ql, qr = bf16_bits(ql), bf16_bits(qr)
+    return q.decode_numpy(cache, ql, qr, scale, splits=splits, q_dtype=q_dtype)
+
+
+def test_decode_f32_ragged_golden(qmla_gpu, golden):
+    q = qmla_gpu
+    cache, rows, offs = make_cache(q, [5, 17, 40], 64, 16, q.F32, 31)
+    ql, qr = O.normal((3, 4, 64), 32), O.normal((3, 4, 16), 33)
+    out, lse = run(q, cache, ql, qr, 0.1)
+    assert rel_err(out, golden["ragged_out"]) < TOL_F32
+    np.testing.assert_allclose(lse, golden["ragged_lse"], rtol=1e-5)
+
+
+@pytest.mark.parametrize("rows_m", [4, 16, 40, 96, 128])
+def test_decode_bf16_small_latent(qmla_gpu, rows_m):
+    q = qmla_gpu
+    lens = [5, 17, 40, 1, 100]
+    cache, rows, offs = make_cache(q, lens, 64, 16, q.BF16, 41)
+    ql, qr = O.normal((5, rows_m, 64), 42), O.normal((5, rows_m, 16), 43)
+    out, lse = run(q, cache, ql, qr, 0.125)
+    ref, rlse = O.decode_absorbed(ql, qr, rows, offs, lens, 0.125)
+    err = rel_err(out, ref)
+    print(f"rows={rows_m} rel_err={err:.2e}")
+    assert err < TOL_BF16
+    np.testing.assert_allclose(lse, rlse, atol=2e-2)
+
+
+def test_decode_f32_v2lite_subset(qmla_gpu):
+    """C2 shapes (H16, r512, rope64, T=4096+1) with an f32 cache: 1e-4."""
+    q = qmla_gpu
+    lens = [4097] * 4
+    cache, rows, offs = make_cache(q, lens, 512, 64, q.F32, 51)
+    ql, qr = O.normal((4, 16, 512), 52), O.normal((4, 16, 64), 53)
+    s = 192 ** -0.5
+    out, lse = run(q, cache, ql, qr, s)
+    ref, rlse = O.decode_absorbed(ql, qr, rows, offs, lens, s)
+    assert rel_err(out, ref) < TOL_F32
+    np.testing.assert_allclose(lse, rlse, rtol=1e-5)
+
+
+def test_decode_bf16_v2lite_full(qmla_gpu):
+    """C2: batch 32, 16 heads, 4096 cached + 1, bf16 cache, scale 1/sqrt(192)."""
+    q = qmla_gpu
+    lens = [4097] * 32
+    cache, rows, offs = make_cache(q, lens, 512, 64, q.BF16, 61)
+    ql, qr = O.normal((32, 16, 512), 62), O.normal((32, 16, 64), 63)
+    s = 192 ** -0.5
+    out, lse = run(q, cache, ql, qr, s)
+    ref, rlse = O.decode_absorbed(ql, qr, rows, offs, lens, s)
+    err = rel_err(out, ref)
+    print(f"C2 bf16 rel_err={err:.2e}")
+    assert err < TOL_BF16
+    np.testing.assert_allclose(lse, rlse, atol=2e-2)
+    # q given as bf16 or as f32 (rounded on the device) must agree exactly
+    out_b, _ = run(q, cache, ql, qr, s, q_dtype=q.BF16)
+    np.testing.assert_array_equal(out_b, out)
+
+
+def test_decode_bf16_v3_ragged_full_size(qmla_gpu):
+    """C4: batch 64, 128 heads, contexts U[1024, 32768] + 1 (seeded), bf16.
+    Full-size run; the oracle checks the shortest, the longest and one middle
+    sequence; split-count invariance covers the rest."""
+    q = qmla_gpu
+    lens = (O.uniform_int(64, 4, 1024, 32768) + 1).astype(np.int32)
+    print(f"C4 tokens={int(lens.sum())} min={lens.min()} max={lens.max()}", flush=True)
+    cache = q.KVCache(lens, 512, 64, q.BF16)
+    d = cache.describe()
+    total = int(lens.sum())
+    tmp = q.DeviceBuffer(total * 576 * 4)
+    q.check(q.lib().qmla_fill_normal_f32(tmp.ptr, total * 576, 77, 0.0, 1.0, None))
+    q.check(q.lib().qmla_f32_to_bf16(tmp.ptr, d.rows, total * 576, None))
+    tmp.free()
+    cache.set_lengths(lens)
+    ql, qr = O.normal((64, 128, 512), 72), O.normal((64, 128, 64), 73)
+    s = 192 ** -0.5
+    out, lse = run(q, cache, ql, qr, s)
+    assert np.isfinite(out).all() and np.isfinite(lse).all()
+    pool = cache.read_rows()
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+    pick = [int(np.argmin(lens)), int(np.argmax(lens)), 17]
+    for b in pick:
+        rows = bf16_to_f32(pool[offs[b]:offs[b] + lens[b]])
+        ref, rlse = O.decode_absorbed(ql[b:b + 1], qr[b:b + 1], rows, np.zeros(1, np.int64), lens[b:b + 1], s)
+        err = rel_err(out[b], ref[0])
+        print(f"C4 seq {b} T={lens[b]} rel_err={err:.2e}", flush=True)
+        assert err < TOL_BF16
+        np.testing.assert_allclose(lse[b], rlse[0], atol=2e-2)
+    out2, lse2 = run(q, cache, ql, qr, s, splits=97)
+    assert rel_err(out2, out) < 5e-3
+    np.testing.assert_allclose(lse2, lse, atol=5e-3)
+
+
+def test_decode_rows_beyond_one_pass(qmla_gpu):
+    """256 query rows (128 heads x 2 new tokens) run as two row passes."""
+    q = qmla_gpu
+    lens = [300, 65]
+    cache, rows, offs = make_cache(q, lens, 512, 64, q.BF16, 81)
+    ql, qr = O.normal((2, 256, 512), 82), O.normal((2, 256, 64), 83)
+    out, _ = run(q, cache, ql, qr, 0.07)
+    ref, _ = O.decode_absorbed(ql, qr, rows, offs, lens, 0.07)
+    assert rel_err(out, ref) < TOL_BF16
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_decode_empty_sequence_and_splits(qmla_gpu, dtype):
+    q = qmla_gpu
+    dt = q.F32 if dtype == "f32" else q.BF16
+    lens = [0, 33, 1, 700]
+    cache, rows, offs = make_cache(q, lens, 512, 64, dt, 91, cap_extra=3)
+    ql, qr = O.normal((4, 32, 512), 92), O.normal((4, 32, 64), 93)
+    ref, rlse = O.decode_absorbed(ql, qr, rows, offs, lens, 0.09)
+    tol = TOL_F32 if dtype == "f32" else TOL_BF16
+    for splits in (0, 1, 5, 64):
+        out, lse = run(q, cache, ql, qr, 0.09, splits=splits)
+        np.testing.assert_array_equal(out[0], 0.0)
+        assert np.all(np.isneginf(lse[0]))
+        assert rel_err(out[1:], ref[1:]) < tol
+        np.testing.assert_allclose(lse[1:], rlse[1:], atol=tol)
+
+
+def test_decode_argument_errors(qmla_gpu):
+    q = qmla_gpu
+    cache, _, _ = make_cache(q, [10, 10], 512, 64, q.BF16, 5)
+    ql = q.DeviceBuffer(2 * 16 * 512 * 4)
+    qr = q.DeviceBuffer(2 * 16 * 64 * 4)
+    out = q.DeviceBuffer(2 * 16 * 512 * 4)
+    need = q.decode_workspace_bytes(cache, 2, 16)
+    ws = q.DeviceBuffer(need)
+    with pytest.raises(q.QmlaError) as e:
+        q.decode_absorbed(cache, 2, 16, ql, qr, 0.1, out, workspace=ws, workspace_bytes=need - 1)
+    assert e.value.status == 7
+    with pytest.raises(q.QmlaError) as e:
+        q.decode_absorbed(cache, 3, 16, ql, qr, 0.1, out, workspace=ws, workspace_bytes=need)
+    assert e.value.status == 2
+    with pytest.raises(q.QmlaError) as e:
+        q.decode_absorbed(cache, 2, 16, ql, qr, float("inf"), out, workspace=ws, workspace_bytes=need)
+    assert e.value.status == 1
