@@ -1,0 +1,271 @@
+#!/usr/bin/env python3
+"""bench.py -- MI355X benchmark of the MLA attention hot path.
+
+Headline workload (one step = one absorbed-latent decode over the batch's
+latent cache, i.e. one attention layer's decode kernels):
+  128 heads, kv_lora_rank 512, rope 64, batch 64, ragged contexts
+  U[1024, 32768] + 1 (seeded), bf16 latent cache, scale 1/sqrt(192).
+value = decode tokens/s (batch / step time); the roofline is HBM bytes of
+the latent cache (sum_b T_b * 1152 B) per step against 8 TB/s.
+
+Secondary lines (same JSON object, "secondary"): 16-head V2-Lite decode
+(batch 32, 4096 + 1 tokens), causal prefill (batch 4, 2048 tokens, 16 heads)
+and chunked prefill (batch 8, 8192 cached + 512 new, 128 heads), the
+prefills reported in TFLOP/s of unmasked attention work (MHA form,
+dqk 192 + dv 128) against the 2.5 PFLOP/s bf16 dense peak.
+
+Inputs are generated on the device (seeded) before the timed region.  The
+decode caches rotate over replicas totalling >= 2 GB so consecutive steps
+never re-read a cache that could still sit in the 256 MB Infinity Cache.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "qmoe-rs_amd"))
+
+import numpy as np  # noqa: E402
+
+import qmla  # noqa: E402
+from qmla import synth  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+ROW_ELEMS = 576            # kv_lora_rank 512 + rope 64
+ROW_BYTES = ROW_ELEMS * 2  # bf16
+SCALE = 192 ** -0.5
+METRIC = "MLA decode tok/s + HBM GB/s (% of peak); prefill TFLOP/s (% MFMA peak)"
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def fill_bf16(dst_ptr: int, n: int, seed: int, tmp: qmla.DeviceBuffer, stream):
+    """dst (bf16, n elements) <- N(0,1) via an f32 staging buffer."""
+    done = 0
+    cap = tmp.nbytes // 4
+    while done < n:
+        m = min(cap, n - done)
+        qmla.check(qmla.lib().qmla_fill_normal_f32(tmp.ptr, m, seed + done, 0.0, 1.0, qmla._sh(stream)))
+        qmla.check(qmla.lib().qmla_f32_to_bf16(tmp.ptr, dst_ptr + 2 * done, m, qmla._sh(stream)))
+        done += m
+
+
+def time_steps(step, steps: int, warmup: int, stream):
+    """Runs warmup + timed steps; returns (wall ms per step, per-step event ms)."""
+    for i in range(warmup):
+        step(i)
+    stream.sync()
+    evs = [(qmla.Event(), qmla.Event()) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        evs[i][0].record(stream)
+        step(warmup + i)
+        evs[i][1].record(stream)
+    stream.sync()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    ev = np.array([a.elapsed_ms(b) for a, b in evs])
+    return wall, ev
+
+
+class DecodeBench:
+    """Absorbed decode over a bf16 latent cache, rotating cache replicas."""
+
+    def __init__(self, lens, heads, stream, seed, min_rotation_bytes=2 << 30):
+        self.lens = np.asarray(lens, np.int32)
+        self.batch, self.heads, self.stream = len(self.lens), heads, stream
+        self.tokens = int(self.lens.sum())
+        self.cache_bytes = self.tokens * ROW_BYTES
+        self.replicas = max(2, math.ceil(min_rotation_bytes / self.cache_bytes))
+        tmp = qmla.DeviceBuffer(min(self.tokens * ROW_ELEMS, 256 << 20) * 4)
+        self.caches = []
+        for r in range(self.replicas):
+            c = qmla.KVCache(self.lens, 512, 64, qmla.BF16)
+            fill_bf16(c.describe().rows, self.tokens * ROW_ELEMS, seed + 1000003 * r, tmp, stream)
+            c.set_lengths(self.lens, stream)
+            self.caches.append(c)
+        nq = self.batch * heads
+        self.q_lat = qmla.DeviceBuffer(nq * 512 * 2)
+        self.q_rope = qmla.DeviceBuffer(nq * 64 * 2)
+        fill_bf16(self.q_lat.ptr, nq * 512, seed + 7, tmp, stream)
+        fill_bf16(self.q_rope.ptr, nq * 64, seed + 8, tmp, stream)
+        self.out = qmla.DeviceBuffer(nq * 512 * 4)
+        self.lse = qmla.DeviceBuffer(nq * 4)
+        self.ws_bytes = qmla.decode_workspace_bytes(self.caches[0], self.batch, heads)
+        self.ws = qmla.DeviceBuffer(self.ws_bytes)
+        stream.sync()
+        tmp.free()
+
+    def step(self, i):
+        qmla.decode_absorbed(self.caches[i % self.replicas], self.batch, self.heads, self.q_lat, self.q_rope,
+                             SCALE, self.out, self.lse, qmla.BF16, self.ws, self.ws_bytes, stream=self.stream)
+
+    def run(self, steps, warmup):
+        wall, ev = time_steps(self.step, steps, warmup, self.stream)
+        t = float(np.median(ev)) * 1e-3
+        gbs = self.cache_bytes / t / 1e9
+        flops = self.tokens * self.heads * (2 * ROW_ELEMS + 2 * 512)
+        return {
+            "tok_s": self.batch / (wall * 1e-3),
+            "ms_per_step": wall,
+            "event_ms_median": float(np.median(ev)),
+            "event_ms_p10": float(np.percentile(ev, 10)),
+            "event_ms_p90": float(np.percentile(ev, 90)),
+            "hbm_gbs": gbs,
+            "hbm_frac": gbs / HBM_PEAK_GBS,
+            "mfma_tflops": flops / t / 1e12,
+            "bytes_per_step": self.cache_bytes,
+            "tokens": self.tokens,
+            "replicas": self.replicas,
+        }
+
+
+class PrefillBench:
+    """bf16 causal prefill (optionally after a cached prefix)."""
+
+    def __init__(self, b, h, sq, sk, q_offset, stream, seed):
+        self.dims = qmla.PrefillDims(b, h, sq, sk, 128, 64, 128, 1, q_offset)
+        self.stream = stream
+        shapes = [b * h * sq * 128, b * h * sq * 64, b * h * sk * 128, b * sk * 64, b * h * sk * 128]
+        tmp = qmla.DeviceBuffer(min(max(shapes), 256 << 20) * 4)
+        self.bufs = []
+        for i, n in enumerate(shapes):
+            buf = qmla.DeviceBuffer(n * 2)
+            fill_bf16(buf.ptr, n, seed + 31 * i, tmp, stream)
+            self.bufs.append(buf)
+        self.out = qmla.DeviceBuffer(b * h * sq * 128 * 2)
+        stream.sync()
+        tmp.free()
+        C, P = sq, q_offset
+        pairs = C * P + C * (C + 1) // 2  # unmasked (query, key) pairs per (b, h)
+        self.flops = b * h * pairs * 2 * (192 + 128)
+
+    def step(self, i):
+        qmla.fused_prefill_attn(*self.bufs, SCALE, True, dims=self.dims, dtype=qmla.BF16, out=self.out,
+                                stream=self.stream)
+
+    def run(self, steps, warmup):
+        wall, ev = time_steps(self.step, steps, warmup, self.stream)
+        t = float(np.median(ev)) * 1e-3
+        tf = self.flops / t / 1e12
+        return {"tflops": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS, "ms_per_step": wall,
+                "event_ms_median": float(np.median(ev)), "gflop_per_step": self.flops / 1e9}
+
+
+def cpu_baseline(lens, heads, sample_seqs):
+    """The oracle's absorbed-latent decode (the CPU restatement of the
+    reference path), timed on a sample of the same workload."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O  # checker library, used here only as the CPU baseline
+    sample = np.asarray(lens[:sample_seqs], np.int32)
+    rows = O.normal((int(sample.sum()), ROW_ELEMS), 4242)
+    ql = O.normal((len(sample), heads, 512), 4243)
+    qr = O.normal((len(sample), heads, 64), 4244)
+    offs = np.concatenate([[0], np.cumsum(sample)[:-1]]).astype(np.int64)
+    t0 = time.perf_counter()
+    O.decode_absorbed(ql, qr, rows, offs, sample, SCALE)
+    dt = time.perf_counter() - t0
+    full_time = dt * float(np.sum(lens)) / float(sample.sum())
+    return {"value": len(lens) / full_time, "unit": "tok/s", "cores": O.num_threads(), "kind": "port",
+            "sample": f"first {len(sample)} of {len(lens)} sequences ({int(sample.sum())} of {int(np.sum(lens))} "
+                      f"tokens, {heads} heads) in {dt:.1f} s; scaled by token count to the full batch; "
+                      f"absorbed-latent f32 C restatement (oracle/mla_oracle.c), OpenMP over (sequence, row block)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-seqs", type=int, default=32)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the decode path shards by batch "
+              f"with no exchange, so N GPUs scale the one-GPU number (see DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+
+    dev, cus, arch = qmla.device_info()
+    log(f"device {dev} {arch} with {cus} CUs")
+    stream = qmla.Stream()
+
+    lens = synth.v3_decode_lengths()
+    log(f"v3 decode: batch {len(lens)}, {int(lens.sum())} tokens, {int(lens.sum()) * ROW_BYTES / 1e9:.3f} GB latent")
+    dec = DecodeBench(lens, 128, stream, seed=11)
+    log(f"replicas {dec.replicas}, workspace {dec.ws_bytes / 1e6:.1f} MB")
+    main_res = dec.run(args.steps, args.warmup)
+    log("v3 decode", json.dumps(main_res))
+    del dec
+
+    secondary = {}
+    if not args.no_secondary:
+        d2 = DecodeBench(np.full(32, 4097, np.int32), 16, stream, seed=21)
+        secondary["v2lite_decode"] = {"workload": "16 heads, batch 32, 4096 cached + 1, bf16 latent", **d2.run(args.steps, args.warmup)}
+        log("v2lite decode", json.dumps(secondary["v2lite_decode"]))
+        del d2
+        p3 = PrefillBench(4, 16, 2048, 2048, 0, stream, seed=31)
+        secondary["causal_prefill"] = {"workload": "batch 4, 2048 tokens, 16 heads, dn 128 dr 64 dv 128, bf16, causal",
+                                       **p3.run(args.steps, args.warmup)}
+        log("causal prefill", json.dumps(secondary["causal_prefill"]))
+        del p3
+        p5 = PrefillBench(8, 128, 512, 8704, 8192, stream, seed=41)
+        secondary["chunked_prefill"] = {"workload": "batch 8, 8192 cached + 512 new, 128 heads, bf16, causal in chunk",
+                                        **p5.run(max(3, args.steps // 4), max(1, args.warmup // 2))}
+        log("chunked prefill", json.dumps(secondary["chunked_prefill"]))
+        del p5
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(lens, 128, args.cpu_sample_seqs)
+        log("cpu baseline", json.dumps(cpu))
+
+    line = {
+        "metric": METRIC,
+        "value": main_res["tok_s"],
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": main_res["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) latent cache and absorbed queries generated on device; no checkpoint",
+        "config": {
+            "workload": "v3 absorbed MLA decode: 128 heads, kv_lora_rank 512, rope 64, batch 64, ragged contexts "
+                        "U[1024,32768]+1 (seed 4), bf16 latent cache, f32 accumulate, one step = one layer's "
+                        "decode attention over the batch",
+            "batch": int(len(lens)), "heads": 128, "kv_lora_rank": 512, "rope_dim": 64,
+            "tokens": main_res["tokens"], "cache_replicas": main_res["replicas"],
+        },
+        "hbm_gbs": main_res["hbm_gbs"],
+        "hbm_frac": main_res["hbm_frac"],
+        "roofline": {
+            "bound": "hbm",
+            "achieved": main_res["hbm_gbs"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": main_res["hbm_frac"],
+            "traffic": None,
+            "kernel": "decode step (plan + k_decode_mfma + merge), median of HIP events on the launch stream",
+            "bytes_per_launch": main_res["bytes_per_step"],
+        },
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -27,18 +27,50 @@ namespace qmla {
 
 namespace {
 
-constexpr int kTok = 32;  // tokens per tile
+constexpr int kTok = 32;      // tokens per tile
+constexpr int kPrefetch = 3;  // LDS operand reads issued ahead of their MFMA
 
+// LDS stage layout for one 32-token tile:
+//  * c_kv region: token rows of R bf16 (2R bytes).  Each DMA instruction
+//    (64 lanes x 16 B) fills one 1 KB group of 1024 / 2R rows; groups are
+//    padded by 16 B (1040 B stride for R = 512) so the S^T operand reads
+//    (16 rows x 16 B per quarter-wave) fall in distinct bank groups.
+//  * rope region: 32 rows x DR bf16, chunk positions XOR-swizzled by row.
 template <int R, int DR>
 struct DecodeShape {
-  static constexpr int W = R + DR;                  // latent row width
-  static constexpr int KSTEPS = W / 16;             // S k-steps
-  static constexpr int CB = R / 32;                 // PV column blocks
-  static constexpr int CHUNKS = W / 8;              // 16-byte chunks per row
-  static constexpr int RS = CHUNKS + 1;             // padded LDS row stride (chunks)
-  static constexpr int INSTR = (kTok * RS + 63) / 64;  // DMA instructions per tile
-  static constexpr int SLOTS = INSTR * 64;          // 16-byte slots per stage
-  static_assert(R % 32 == 0 && W % 16 == 0, "unsupported latent shape");
+  static constexpr int W = R + DR;                    // latent row width
+  static constexpr int KSTEPS = W / 16;               // S k-steps (16 dims each)
+  static constexpr int KV_STEPS = R / 16;             // ... of which over c_kv
+  static constexpr int CB = R / 32;                   // PV column blocks
+  static constexpr int ROW_B = R * 2;                 // c_kv bytes per token
+  static constexpr int RPG = 1024 / ROW_B;            // c_kv rows per DMA group
+  static constexpr int GS = 1024 + 16;                // padded group stride
+  static constexpr int KV_INSTR = kTok / RPG;         // DMA instructions for c_kv
+  static constexpr int KV_BYTES = KV_INSTR * GS;
+  static constexpr int RCH = DR / 8;                  // rope chunks per token
+  static constexpr int ROPE_INSTR = kTok * DR * 2 / 1024;
+  static constexpr int INSTR = KV_INSTR + ROPE_INSTR;
+  static constexpr int STAGE_BYTES = KV_BYTES + ROPE_INSTR * 1024;
+  static_assert(R == 64 || R == 128 || R == 256 || R == 512, "kv_lora_rank");
+  static_assert(DR == 16 || DR == 32 || DR == 64, "rope dim");
+  // Token t of a tile lives in c_kv row slot pi(t) (for one row per group):
+  // pi(t) = (t & 16) | (t & 3) << 2 | (t >> 2) & 3.  With the 1040-byte row
+  // stride this makes both LDS read patterns conflict-free on the 64-bank
+  // LDS: the S^T operand reads (16 consecutive tokens, same 16-byte chunk)
+  // hit 16 distinct row offsets mod 256 B, and the transposed V^T reads
+  // (4 consecutive tokens x 64 contiguous bytes per 32 lanes) hit rows whose
+  // offsets are 64 B apart mod 256 B.  pi(t + 8) = pi(t) + 2 for t % 16 < 8.
+  static __device__ __forceinline__ int slot(int t) {
+    return RPG == 1 ? ((t & 16) | ((t & 3) << 2) | ((t >> 2) & 3)) : t;
+  }
+  // byte offset of token row t in the c_kv region
+  static __device__ __forceinline__ int kv_row(int t) {
+    const int r = slot(t);
+    return (r / RPG) * GS + (r % RPG) * ROW_B;
+  }
+  // row-offset (bytes) between tokens t + 8 and t (t % 16 < 8), and t + 16 and t
+  static constexpr int HI8 = RPG == 1 ? 2 * GS : (8 / RPG) * GS;
+  static constexpr int HI16 = RPG == 1 ? 16 * GS : (16 / RPG) * GS;
 };
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
@@ -50,7 +82,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 __device__ __forceinline__ void wait_vmcnt_dyn(int n) {
-  // n is wave-uniform; dispatch to an immediate.
+  // n is wave-uniform (scalar); dispatch to an immediate.
   switch (n) {
 #define QMLA_W(k) case k: wait_vmcnt<k>(); break;
     QMLA_W(0) QMLA_W(1) QMLA_W(2) QMLA_W(3) QMLA_W(4) QMLA_W(5) QMLA_W(6) QMLA_W(7)
@@ -66,31 +98,48 @@ __device__ __forceinline__ void wait_vmcnt_dyn(int n) {
   }
 }
 
+// Waits until at most k tiles of this wave's DMA are outstanding.  With an
+// even split (every wave issues INSTR / NW instructions per tile) the count
+// is a compile-time multiple; otherwise dispatch on the runtime count.
+template <class SH, int NW>
+__device__ __forceinline__ void wait_tiles(int k, int my_instr) {
+  if constexpr (SH::INSTR % NW == 0) {
+    constexpr int MI = SH::INSTR / NW;
+    if (k <= 0)
+      wait_vmcnt<0>();
+    else if (k == 1)
+      wait_vmcnt<MI>();
+    else
+      wait_vmcnt<(2 * MI < 63 ? 2 * MI : 63)>();
+  } else {
+    wait_vmcnt_dyn(k * my_instr);
+  }
+}
+
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) char lds_char;
 typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4;
 typedef __attribute__((address_space(3))) bf16x8_t lds_bf16x8;
 
-// o *= alpha for a 16-float MFMA accumulator.  Done through inline asm with
-// AGPR operands, one value at a time through a VGPR, so the 256 accumulator
-// registers of a wave stay in AGPRs (a VALU multiply on them would make the
-// register allocator move them to arch VGPRs, which do not have room).
-__device__ __forceinline__ void agpr_scale16(floatx16_t &o, float alpha) {
-  float e[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) e[i] = o[i];
-  float tmp;
-#define QMLA_S1(i) "v_accvgpr_read_b32 %16, %" #i "\n v_mul_f32 %16, %16, %17\n v_accvgpr_write_b32 %" #i ", %16\n"
-  asm volatile(QMLA_S1(0) QMLA_S1(1) QMLA_S1(2) QMLA_S1(3) QMLA_S1(4) QMLA_S1(5) QMLA_S1(6)
-                   QMLA_S1(7) QMLA_S1(8) QMLA_S1(9) QMLA_S1(10) QMLA_S1(11) QMLA_S1(12)
-                       QMLA_S1(13) QMLA_S1(14) QMLA_S1(15)
-               : "+a"(e[0]), "+a"(e[1]), "+a"(e[2]), "+a"(e[3]), "+a"(e[4]), "+a"(e[5]),
-                 "+a"(e[6]), "+a"(e[7]), "+a"(e[8]), "+a"(e[9]), "+a"(e[10]), "+a"(e[11]),
-                 "+a"(e[12]), "+a"(e[13]), "+a"(e[14]), "+a"(e[15]), "=&v"(tmp)
-               : "v"(alpha));
-#undef QMLA_S1
-#pragma unroll
-  for (int i = 0; i < 16; ++i) o[i] = e[i];
+// S^T accumulation chain in arch VGPRs.  Any AGPR operand in a function makes
+// the compiler pick the AGPR form for every MFMA builtin, which would put
+// this 16-register accumulator next to the 256 O^T accumulators in the AGPR
+// file and spill Q; issuing the S^T MFMAs through inline asm with "v"
+// constraints keeps it in VGPRs.  Hazards: the first MFMA of a chain takes
+// srcC = 0 (no VALU -> MFMA srcC dependence); each following one reads the
+// previous result as srcC with exactly the same registers (forwarded, no
+// wait states); VALU reads of the result are preceded by s_nop padding
+// (mfma_s_drain) longer than the MFMA's 8 passes.
+__device__ __forceinline__ floatx16_t mfma_s_first(const bf16x8_t &a, const bf16x8_t &b) {
+  floatx16_t d;
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+  return d;
+}
+__device__ __forceinline__ void mfma_s_acc(floatx16_t &d, const bf16x8_t &a, const bf16x8_t &b) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma_s_drain(floatx16_t &d) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(d));
 }
 
 __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
@@ -101,30 +150,38 @@ __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// Issue this wave's share of the DMA instructions for one tile.  Slot s of
-// the stage holds chunk (s % RS) of tile row (s / RS); pad slots and rows
-// past the segment end re-load a valid chunk (never read back).
+// Issue this wave's share of the DMA instructions for one tile.  Tokens past
+// the segment end re-load the segment's last row (masked later, never used).
 template <class SH, int NW>
 __device__ __forceinline__ void issue_tile(const uint8_t *__restrict__ seq_base, int tile_t0,
                                            int seg_t1, lds_char *stage, int wave, int lane) {
-  for (int ins = wave; ins < SH::INSTR; ins += NW) {
-    const int s = ins * 64 + lane;
-    int t = s / SH::RS, c = s - t * SH::RS;
-    if (t >= kTok || c >= SH::CHUNKS) {
-      t = 0;
-      c = 0;
+  // With NW dividing both instruction counts, whether instruction ins0+wave
+  // exists and which region it fills is known per unrolled step.
+  constexpr bool EVEN = SH::INSTR % NW == 0 && SH::KV_INSTR % NW == 0;
+#pragma unroll
+  for (int ins0 = 0; ins0 < SH::INSTR; ins0 += NW) {
+    const int ins = ins0 + wave;
+    if (EVEN || ins < SH::INSTR) {
+      int t, c, base_b;
+      lds_char *dst;
+      if (EVEN ? ins0 < SH::KV_INSTR : ins < SH::KV_INSTR) {
+        t = ins * SH::RPG + lane / (SH::ROW_B / 16);
+        c = lane % (SH::ROW_B / 16);
+        base_b = 0;
+        dst = stage + (SH::RPG == 1 ? SH::kv_row(ins) : ins * SH::GS);
+      } else {
+        const int q = ins - SH::KV_INSTR;
+        t = q * (64 / SH::RCH) + lane / SH::RCH;
+        c = (lane % SH::RCH) ^ (t & (SH::RCH - 1));
+        base_b = SH::ROW_B;
+        dst = stage + SH::KV_BYTES + q * 1024;
+      }
+      int tok = tile_t0 + t;
+      tok = tok < seg_t1 ? tok : seg_t1 - 1;
+      const uint8_t *src = seq_base + (int64_t)tok * (SH::W * 2) + base_b + c * 16;
+      __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)dst, 16, 0, 0);
     }
-    int tok = tile_t0 + t;
-    tok = tok < seg_t1 ? tok : seg_t1 - 1;
-    const uint8_t *src = seq_base + (int64_t)tok * (SH::W * 2) + c * 16;
-    __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(stage + ins * 1024), 16, 0,
-                                     0);
   }
-}
-
-template <class SH, int NW>
-__device__ __forceinline__ constexpr int instr_of_wave(int wave) {
-  return (SH::INSTR - wave + NW - 1) / NW;
 }
 
 template <int R, int DR, typename QT>
@@ -145,6 +202,119 @@ __device__ __forceinline__ bf16x8_t load_q8(const QT *__restrict__ q_lat,
   }
 }
 
+// Per-lane LDS read addressing (see DecodeShape).
+template <class SH>
+struct LaneAddr {
+  int a_base;     // S^T operand, c_kv part: + kk*32
+  int rope_row;   // S^T operand, rope part: row base inside the rope region
+  int rope_mask;  // row & (RCH - 1): XOR swizzle of rope chunks
+  int half;
+  int v_base;     // V^T operand: + ks-block and cb offsets
+
+  __device__ __forceinline__ bf16x8_t s_read(const lds_char *st, int kk) const {
+    if (kk < SH::KV_STEPS)
+      return *reinterpret_cast<const lds_bf16x8 *>(st + a_base + kk * 32);
+    const int c = (2 * (kk - SH::KV_STEPS) + half) ^ rope_mask;
+    return *reinterpret_cast<const lds_bf16x8 *>(st + SH::KV_BYTES + rope_row + c * 16);
+  }
+  // PV operand i = ks * CB + cb: tokens 16 ks + {tok_a, tok_a + 8}, 32 columns
+  __device__ __forceinline__ bf16x8_t pv_read(const lds_char *st, int i) const {
+    const int ks = i / SH::CB, cb = i % SH::CB;
+    const lds_char *p = st + v_base + ks * SH::HI16 + cb * 64;
+    const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4 *)p);
+    const bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4 *)(p + SH::HI8));
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  }
+};
+
+// One pipelined body: S^T of the next tile (DO_S) interleaved with O^T +=
+// V^T P^T of the current tile (DO_PV).  Operand reads run two MFMAs ahead.
+template <class SH, bool DO_S, bool DO_PV>
+__device__ __forceinline__ void body(const LaneAddr<SH> &la, const lds_char *st_s,
+                                     const lds_char *st_pv, const bf16x8_t (&qf)[SH::KSTEPS],
+                                     floatx16_t &s, const bf16x8_t (&pb)[2],
+                                     floatx16_t (&o)[SH::CB]) {
+  constexpr int NS = DO_S ? SH::KSTEPS : 0;
+  constexpr int NP = DO_PV ? 2 * SH::CB : 0;
+  constexpr int N = NS > NP ? NS : NP;
+  constexpr int D = kPrefetch;
+  bf16x8_t sa[D + 1], pa[D + 1];
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+    if (i < NS) sa[i] = la.s_read(st_s, i);
+    if (i < NP) pa[i] = la.pv_read(st_pv, i);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    if (i < NS) {
+      if (i + D < NS) sa[(i + D) % (D + 1)] = la.s_read(st_s, i + D);
+      if (i == 0)
+        s = mfma_s_first(sa[0], qf[0]);
+      else
+        mfma_s_acc(s, sa[i % (D + 1)], qf[i]);
+    }
+    if (i < NP) {
+      if (i + D < NP) pa[(i + D) % (D + 1)] = la.pv_read(st_pv, i + D);
+      o[i % SH::CB] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[i % (D + 1)], pb[i / SH::CB],
+                                                              o[i % SH::CB], 0, 0, 0);
+    }
+  }
+  if constexpr (DO_S) mfma_s_drain(s);
+}
+
+// Online softmax of one tile's S^T (lane = head, 16 tokens) in the log2
+// domain.  The running reference m is set by the first tile (or given by a
+// restart) and then kept: probabilities are exp2(s - m) <= 2^16 as long as no
+// row's maximum exceeds m by more than kRefSlack.  When one does (rare), the
+// function returns true and the block restarts the segment with the larger
+// reference (see the kernel).  The O^T accumulators are therefore only ever
+// MFMA-accumulated, read at the end or zeroed at a segment start -- never
+// rescaled in registers, which keeps all 256 of them in AGPRs.
+constexpr float kRefSlack = 16.f;
+
+template <class SH>
+__device__ __forceinline__ bool softmax_tile(floatx16_t &s, float scale_log2, int tile_t0, int T,
+                                             int half, float &m_run, float &l_run,
+                                             bf16x8_t (&pb)[2], float &mt_out) {
+  float mt = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int tok = tile_t0 + 8 * (j >> 2) + 4 * half + (j & 3);
+    const float x = tok < T ? s[j] * scale_log2 : -INFINITY;
+    s[j] = x;
+    mt = fmaxf(mt, x);
+  }
+  mt = xor32_max(mt);
+  mt_out = mt;
+  if (m_run == -INFINITY) {
+    m_run = mt;  // first tile of the segment (or after a flush): o and l are zero
+  } else if (__ballot(mt > m_run + kRefSlack) != 0) {
+    return true;
+  }
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    u32x4_t pk;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p0 = exp2f(s[ks * 8 + 2 * i] - m_run);
+      const float p1 = exp2f(s[ks * 8 + 2 * i + 1] - m_run);
+      l_run += p0 + p1;
+      pk[i] = pack2_bf16(p0, p1);
+    }
+    pb[ks] = __builtin_bit_cast(bf16x8_t, pk);
+  }
+  return false;
+}
+
+// True when any wave of the block raised its reference-overflow flag.
+template <int NW>
+__device__ __forceinline__ bool any_flag(const volatile int *flags) {
+  int v = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) v |= flags[w];
+  return v != 0;
+}
+
 template <int R, int DR, int NW, int NSTAGE, typename QT>
 __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
     const uint8_t *__restrict__ pool, const int64_t *__restrict__ offsets,
@@ -152,29 +322,32 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
     float scale_log2, DecodePlanView plan, float *__restrict__ out, float *__restrict__ out_lse,
     float *__restrict__ part_o, float *__restrict__ part_lse) {
   using SH = DecodeShape<R, DR>;
-  constexpr int STAGE_BYTES = SH::SLOTS * 16;
-  constexpr int ROW_BYTES = SH::RS * 16;
+  static_assert(NSTAGE >= 3, "the pipelined loop keeps two stages resident");
   extern __shared__ __attribute__((aligned(16))) char ring_raw[];
+  __shared__ int ovf_flag[NW];
   lds_char *ring = (lds_char *)ring_raw;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   const int n = lane & 31;     // head (query row) within the wave = MFMA column
   const int half = lane >> 5;  // which 8-wide k half of an MFMA operand
   const int row = blockIdx.y * (NW * 32) + wave * 32 + n;  // query row
   const bool row_ok = row < rows;
   const int row_c = row_ok ? row : rows - 1;
   const int piece = blockIdx.x;
-  const int my_instr = instr_of_wave<SH, NW>(wave);
+  const int my_instr = (SH::INSTR - wave + NW - 1) / NW;
 
-  // Per-lane LDS byte offsets inside a stage.
-  //  S^T A operand (tokens x dims): row n, chunk 2*kk + half -> + kk*32.
-  const int a_off = (n * SH::RS + half) * 16;
-  //  V^T A operand via ds_read_b64_tr_b16: 16-lane group g reads 4 tokens x
-  //  16 columns; lane sl supplies token tok_a + ..., columns col_in..+3.
-  const int g = lane >> 4, sl = lane & 15;
-  const int tok_a = (g >= 2 ? 4 : 0) + (sl >> 2);
-  const int col_in = (g & 1) * 16 + 4 * (sl & 3);
-  const int v_off = tok_a * ROW_BYTES + (col_in >> 3) * 16 + (col_in & 7) * 2;
+  LaneAddr<SH> la;
+  la.a_base = SH::kv_row(n) + half * 16;
+  la.rope_row = n * (DR * 2);
+  la.rope_mask = n & (SH::RCH - 1);
+  la.half = half;
+  {
+    const int g = lane >> 4, sl = lane & 15;
+    const int tok_a = (g >= 2 ? 4 : 0) + (sl >> 2);
+    const int col_in = (g & 1) * 16 + 4 * (sl & 3);
+    la.v_base = SH::kv_row(tok_a) + (col_in >> 3) * 16 + (col_in & 7) * 2;
+  }
 
   const int32_t s0 = plan.seg_start[piece], s1 = plan.seg_start[piece + 1];
   for (int32_t si = s0; si < s1; ++si) {
@@ -187,8 +360,8 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
     bf16x8_t qf[SH::KSTEPS];
 #pragma unroll
     for (int kk = 0; kk < SH::KSTEPS; ++kk) {
-      bf16x8_t v = load_q8<R, DR, QT>(q_lat, q_rope, qrow_c, kk * 16 + half * 8);
-      u32x4_t u = __builtin_bit_cast(u32x4_t, v);
+      u32x4_t u = __builtin_bit_cast(u32x4_t, load_q8<R, DR, QT>(q_lat, q_rope, qrow_c,
+                                                                  kk * 16 + half * 8));
       const uint32_t keep = row_ok ? 0xffffffffu : 0u;
       u[0] &= keep;
       u[1] &= keep;
@@ -197,116 +370,74 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
       qf[kk] = __builtin_bit_cast(bf16x8_t, u);
     }
 
-    floatx16_t o[SH::CB];
-#pragma unroll
-    for (int cb = 0; cb < SH::CB; ++cb)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) o[cb][j] = 0.f;
-    float m_run = -INFINITY, l_run = 0.f;
-
     const int T = sg.t1 - sg.t0;
     const int ntiles = (T + kTok - 1) / kTok;
-    const int seg_end = sg.t1;
-#pragma unroll
-    for (int p = 0; p < NSTAGE - 1; ++p)
-      if (p < ntiles)
-        issue_tile<SH, NW>(seq_base, sg.t0 + p * kTok, seg_end, ring + p * STAGE_BYTES, wave,
-                           lane);
+    auto stage = [&](int t) { return ring + (t % NSTAGE) * SH::STAGE_BYTES; };
 
-    for (int it = 0; it < ntiles; ++it) {
-      const int nxt = it + NSTAGE - 1;
-      if (nxt < ntiles)
-        issue_tile<SH, NW>(seq_base, sg.t0 + nxt * kTok, seg_end,
-                           ring + (nxt % NSTAGE) * STAGE_BYTES, wave, lane);
-      // Tiles it+1 .. min(nxt, ntiles-1) may stay in flight.
-      const int ahead = (nxt < ntiles ? nxt : ntiles - 1) - it;
-      wait_vmcnt_dyn(ahead * my_instr);
+    floatx16_t o[SH::CB];
+    floatx16_t s;
+    bf16x8_t pb[2];
+    float m_run, l_run;
+    float m_init = -INFINITY;  // reference to (re)start the segment with
+    for (;;) {
+#pragma unroll
+      for (int cb = 0; cb < SH::CB; ++cb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) o[cb][j] = 0.f;
+      m_run = m_init;
+      l_run = 0.f;
+      if (lane == 0) ovf_flag[wave] = 0;
+
+      // prologue: NSTAGE-1 tiles in flight, then S and softmax of tile 0
+#pragma unroll
+      for (int p = 0; p < NSTAGE - 1; ++p)
+        if (p < ntiles) issue_tile<SH, NW>(seq_base, sg.t0 + p * kTok, sg.t1, stage(p), wave, lane);
+      wait_tiles<SH, NW>(min(NSTAGE - 2, ntiles - 1), my_instr);
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
+      body<SH, true, false>(la, stage(0), stage(0), qf, s, pb, o);
+      float mt;
+      // tile 0 never overflows: m_init is -inf or covers every tile's max
+      (void)softmax_tile<SH>(s, scale_log2, 0, T, half, m_run, l_run, pb, mt);
+      float m_cand = fmaxf(m_run, mt);  // max over all tiles of the segment
 
-      const lds_char *stage = ring + (it % NSTAGE) * STAGE_BYTES;
-      const lds_char *pa = stage + a_off;
-      const lds_char *pv = stage + v_off;
-      // ---- S^T = C Q^T over the 32 tokens of this tile
-      floatx16_t s;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) s[j] = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < SH::KSTEPS; ++kk) {
-        const bf16x8_t a = *reinterpret_cast<const lds_bf16x8 *>(pa + kk * 32);
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], s, 0, 0, 0);
+      // steady state: S^T of tile it+1 interleaved with P.V of tile it.  A
+      // reference overflow only raises a flag (the tile's P is left stale and
+      // the segment is redone below): the loop keeps a single exit.
+      for (int it = 0; it + 1 < ntiles; ++it) {
+        // tile it+1 must be complete; tile it+2 (if issued) may stay in flight
+        wait_tiles<SH, NW>(min(NSTAGE - 3, ntiles - 2 - it), my_instr);
+        // All waves are past iteration it-1: stage (it-1) % NSTAGE is free and
+        // tile it+1 is visible to every wave.
+        __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        const int nxt = it + NSTAGE - 1;
+        if (nxt < ntiles)
+          issue_tile<SH, NW>(seq_base, sg.t0 + nxt * kTok, sg.t1, stage(nxt), wave, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        body<SH, true, true>(la, stage(it + 1), stage(it), qf, s, pb, o);
+        __builtin_amdgcn_sched_barrier(0);
+        if (softmax_tile<SH>(s, scale_log2, (it + 1) * kTok, T, half, m_run, l_run, pb, mt) &&
+            lane == 0)
+          ovf_flag[wave] = 1;
+        m_cand = fmaxf(m_cand, mt);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      // Keep 4 operand reads in flight ahead of the MFMA chain.
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-      for (int kk = 0; kk < SH::KSTEPS - 4; ++kk) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-      __builtin_amdgcn_sched_barrier(0);
-      // ---- online softmax (log2 domain); lane holds 16 tokens of head n
-      const int tile_t0 = it * kTok;  // relative to the segment
-      float mt = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int tok = tile_t0 + 8 * (j >> 2) + 4 * half + (j & 3);
-        const float x = tok < T ? s[j] * scale_log2 : -INFINITY;
-        s[j] = x;
-        mt = fmaxf(mt, x);
-      }
-      mt = xor32_max(mt);
-      // Lazy rescaling: keep the running reference unless the tile max
-      // exceeds it by more than 8 (a factor 256); p stays <= 256.
-      if (m_run == -INFINITY || mt > m_run + 8.f) {
-        const float m_new = fmaxf(mt, m_run);
-        const float alpha = m_run == -INFINITY ? 0.f : exp2f(m_run - m_new);
-        m_run = m_new;
-        l_run *= alpha;
-#pragma unroll
-        for (int cb = 0; cb < SH::CB; ++cb) agpr_scale16(o[cb], alpha);
-      }
-      u32x4_t pk[2];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p0 = exp2f(s[ks * 8 + 2 * i] - m_run);
-          const float p1 = exp2f(s[ks * 8 + 2 * i + 1] - m_run);
-          l_run += p0 + p1;
-          pk[ks][i] = pack2_bf16(p0, p1);
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      // ---- O^T += V^T P^T
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const bf16x8_t pb = __builtin_bit_cast(bf16x8_t, pk[ks]);
-#pragma unroll
-        for (int cb = 0; cb < SH::CB; ++cb) {
-          const lds_char *p1 = pv + ks * 16 * ROW_BYTES + cb * 64;
-          const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4 *)p1);
-          const bf16x4_t hi =
-              __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4 *)(p1 + 8 * ROW_BYTES));
-          const bf16x8_t a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-          o[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, o[cb], 0, 0, 0);
-        }
-      }
-      // Keep 3 MFMAs' worth of transposed reads in flight.
-      __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
-#pragma unroll
-      for (int i = 0; i < 2 * SH::CB - 3; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
-      __builtin_amdgcn_sched_barrier(0);
-      // Every wave must be done reading this stage before it is refilled.
+      // P.V of the last tile
+      body<SH, false, true>(la, stage(ntiles - 1), stage(ntiles - 1), qf, s, pb, o);
+      // Every wave is done with the stages (the next segment's or attempt's
+      // prologue refills them) and every overflow flag is visible.
       __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
       __builtin_amdgcn_s_barrier();
+      if (!any_flag<NW>(ovf_flag)) break;
+      // Rare: some row's maximum outgrew the reference.  Redo the segment
+      // with a reference covering every tile's maximum (cannot overflow).
+      __builtin_amdgcn_s_barrier();  // all waves have read the flags
+      m_init = m_cand;
     }
 
-    // ---- finalise: combine the two half-waves' denominators
+    // ---- finalise: combine the two half-waves' denominators and write
     l_run = xor32_sum(l_run);
     const float inv = 1.f / l_run;
     const float lse = (m_run + log2f(l_run)) * 0.69314718055994531f;
@@ -336,7 +467,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
 template <int R, int DR, int NW, int NSTAGE>
 qmla_status launch_shape(const DecodeArgs &a, hipStream_t stream) {
   using SH = DecodeShape<R, DR>;
-  const size_t lds = (size_t)NSTAGE * SH::SLOTS * 16;
+  const size_t lds = (size_t)NSTAGE * SH::STAGE_BYTES;
   const int passes = (a.rows + NW * 32 - 1) / (NW * 32);
   dim3 grid(a.blocks, passes), block(NW * 64);
   const float sl2 = a.scale * 1.4426950408889634f;
@@ -362,8 +493,8 @@ qmla_status launch_shape(const DecodeArgs &a, hipStream_t stream) {
 
 template <int R, int DR>
 qmla_status launch_dims(const DecodeArgs &a, hipStream_t stream) {
-  if (a.rows <= 32) return launch_shape<R, DR, 1, 2>(a, stream);
-  if (a.rows <= 64) return launch_shape<R, DR, 2, 2>(a, stream);
+  if (a.rows <= 32) return launch_shape<R, DR, 1, 3>(a, stream);
+  if (a.rows <= 64) return launch_shape<R, DR, 2, 4>(a, stream);
   return launch_shape<R, DR, 4, 4>(a, stream);
 }
 
