@@ -20,6 +20,8 @@
 // quarter-wave) free of bank conflicts.
 
 #include <cmath>
+#include <type_traits>
+#include <utility>
 
 #include "internal.hpp"
 
@@ -28,7 +30,7 @@ namespace qmla {
 namespace {
 
 constexpr int kTok = 32;      // tokens per tile
-constexpr int kPrefetch = 3;  // LDS operand reads issued ahead of their MFMA
+constexpr int kPrefetch = 8;  // S^T operand reads issued ahead of their MFMA
 
 // LDS stage layout for one 32-token tile:
 //  * c_kv region: token rows of R bf16 (2R bytes).  Each DMA instruction
@@ -150,40 +152,6 @@ __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// Issue this wave's share of the DMA instructions for one tile.  Tokens past
-// the segment end re-load the segment's last row (masked later, never used).
-template <class SH, int NW>
-__device__ __forceinline__ void issue_tile(const uint8_t *__restrict__ seq_base, int tile_t0,
-                                           int seg_t1, lds_char *stage, int wave, int lane) {
-  // With NW dividing both instruction counts, whether instruction ins0+wave
-  // exists and which region it fills is known per unrolled step.
-  constexpr bool EVEN = SH::INSTR % NW == 0 && SH::KV_INSTR % NW == 0;
-#pragma unroll
-  for (int ins0 = 0; ins0 < SH::INSTR; ins0 += NW) {
-    const int ins = ins0 + wave;
-    if (EVEN || ins < SH::INSTR) {
-      int t, c, base_b;
-      lds_char *dst;
-      if (EVEN ? ins0 < SH::KV_INSTR : ins < SH::KV_INSTR) {
-        t = ins * SH::RPG + lane / (SH::ROW_B / 16);
-        c = lane % (SH::ROW_B / 16);
-        base_b = 0;
-        dst = stage + (SH::RPG == 1 ? SH::kv_row(ins) : ins * SH::GS);
-      } else {
-        const int q = ins - SH::KV_INSTR;
-        t = q * (64 / SH::RCH) + lane / SH::RCH;
-        c = (lane % SH::RCH) ^ (t & (SH::RCH - 1));
-        base_b = SH::ROW_B;
-        dst = stage + SH::KV_BYTES + q * 1024;
-      }
-      int tok = tile_t0 + t;
-      tok = tok < seg_t1 ? tok : seg_t1 - 1;
-      const uint8_t *src = seq_base + (int64_t)tok * (SH::W * 2) + base_b + c * 16;
-      __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)dst, 16, 0, 0);
-    }
-  }
-}
-
 template <int R, int DR, typename QT>
 __device__ __forceinline__ bf16x8_t load_q8(const QT *__restrict__ q_lat,
                                             const QT *__restrict__ q_rope, int64_t qrow, int d0) {
@@ -202,117 +170,409 @@ __device__ __forceinline__ bf16x8_t load_q8(const QT *__restrict__ q_lat,
   }
 }
 
-// Per-lane LDS read addressing (see DecodeShape).
+// LDS traffic of the hot loop is issued through inline asm with explicit
+// lgkmcnt waits.  The compiler cannot tell the tile reads from the
+// direct-to-LDS DMA writes still in flight into other stages, so for
+// ordinary loads it drains the vector-memory counter (vmcnt(0): every tile
+// in flight) and the LDS counter before each group of reads, which
+// serialises the pipeline.  Ordering is explicit instead: a stage is read
+// only after wait_tiles + barrier, and each operand after the lgkmcnt wait
+// that covers it (LDS operations complete in issue order; any other
+// counted operation only makes a wait stricter).
+__device__ __forceinline__ uint32_t lds_u32(const lds_char *p) {
+  return (uint32_t)(uintptr_t)p;
+}
+template <int OFF>
+__device__ __forceinline__ bf16x8_t ds_b128(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset");
+  bf16x8_t r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+  return r;
+}
+// V^T operand: two transposing 8-byte reads (tokens t and t + 8)
+template <int OFF, int HI>
+__device__ __forceinline__ bf16x8_t ds_tr2(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF + HI < 65536, "ds offset");
+  u32x2_t lo, hi;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(lo) : "v"(addr), "n"(OFF));
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(hi) : "v"(addr), "n"(OFF + HI));
+  return __builtin_bit_cast(bf16x8_t, (u32x4_t){lo[0], lo[1], hi[0], hi[1]});
+}
+template <int OFF>
+__device__ __forceinline__ void ds_w128(uint32_t addr, const bf16x8_t &v) {
+  asm volatile("ds_write_b128 %0, %1 offset:%2" : : "v"(addr), "v"(v), "n"(OFF));
+}
+template <int N>
+__device__ __forceinline__ void wait_lgkm() {
+  static_assert(N >= 0 && N <= 15, "lgkmcnt");
+  asm volatile("s_waitcnt lgkmcnt(%0)" : : "n"(N) : "memory");
+}
+// Marks x as produced here: placed right after the wait that covers the
+// asm read of x, it keeps every use of x (compiler MFMAs, copies) after
+// that wait.  Emits no code.
+__device__ __forceinline__ void arrived(bf16x8_t &x) { asm volatile("" : "+v"(x)); }
+
+// Per-lane LDS byte offsets of the MFMA operands (see DecodeShape).
 template <class SH>
 struct LaneAddr {
-  int a_base;     // S^T operand, c_kv part: + kk*32
-  int rope_row;   // S^T operand, rope part: row base inside the rope region
-  int rope_mask;  // row & (RCH - 1): XOR swizzle of rope chunks
+  static constexpr int ROPE_STEPS = SH::KSTEPS - SH::KV_STEPS;
+  uint32_t s_kv;                  // S^T operand, c_kv part: + kk*32
+  uint32_t s_rope[ROPE_STEPS];    // S^T operand, rope k-steps (XOR-swizzled chunks)
+  uint32_t v;                     // V^T operand: + ks/cb offsets
+  uint32_t p_rd, p_wr;            // P^T rows: read (row group) / write (own rows)
   int half;
-  int v_base;     // V^T operand: + ks-block and cb offsets
-
-  __device__ __forceinline__ bf16x8_t s_read(const lds_char *st, int kk) const {
-    if (kk < SH::KV_STEPS)
-      return *reinterpret_cast<const lds_bf16x8 *>(st + a_base + kk * 32);
-    const int c = (2 * (kk - SH::KV_STEPS) + half) ^ rope_mask;
-    return *reinterpret_cast<const lds_bf16x8 *>(st + SH::KV_BYTES + rope_row + c * 16);
-  }
-  // PV operand i = ks * CB + cb: tokens 16 ks + {tok_a, tok_a + 8}, 32 columns
-  __device__ __forceinline__ bf16x8_t pv_read(const lds_char *st, int i) const {
-    const int ks = i / SH::CB, cb = i % SH::CB;
-    const lds_char *p = st + v_base + ks * SH::HI16 + cb * 64;
-    const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4 *)p);
-    const bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4 *)(p + SH::HI8));
-    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-  }
 };
 
-// One pipelined body: S^T of the next tile (DO_S) interleaved with O^T +=
-// V^T P^T of the current tile (DO_PV).  Operand reads run two MFMAs ahead.
-template <class SH, bool DO_S, bool DO_PV>
-__device__ __forceinline__ void body(const LaneAddr<SH> &la, const lds_char *st_s,
-                                     const lds_char *st_pv, const bf16x8_t (&qf)[SH::KSTEPS],
-                                     floatx16_t &s, const bf16x8_t (&pb)[2],
-                                     floatx16_t (&o)[SH::CB]) {
-  constexpr int NS = DO_S ? SH::KSTEPS : 0;
-  constexpr int NP = DO_PV ? 2 * SH::CB : 0;
-  constexpr int N = NS > NP ? NS : NP;
-  constexpr int D = kPrefetch;
-  bf16x8_t sa[D + 1], pa[D + 1];
-#pragma unroll
-  for (int i = 0; i < D; ++i) {
-    if (i < NS) sa[i] = la.s_read(st_s, i);
-    if (i < NP) pa[i] = la.pv_read(st_pv, i);
-  }
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    if (i < NS) {
-      if (i + D < NS) sa[(i + D) % (D + 1)] = la.s_read(st_s, i + D);
-      if (i == 0)
-        s = mfma_s_first(sa[0], qf[0]);
-      else
-        mfma_s_acc(s, sa[i % (D + 1)], qf[i]);
-    }
-    if (i < NP) {
-      if (i + D < NP) pa[(i + D) % (D + 1)] = la.pv_read(st_pv, i + D);
-      o[i % SH::CB] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[i % (D + 1)], pb[i / SH::CB],
-                                                              o[i % SH::CB], 0, 0, 0);
-    }
-  }
-  if constexpr (DO_S) mfma_s_drain(s);
+template <class SH, int KK>
+__device__ __forceinline__ bf16x8_t s_read(const LaneAddr<SH> &la, uint32_t st_kv,
+                                           uint32_t st_base) {
+  if constexpr (KK < SH::KV_STEPS)
+    return ds_b128<KK * 32>(st_kv);
+  else
+    return ds_b128<0>(st_base + la.s_rope[KK - SH::KV_STEPS]);
 }
 
-// Online softmax of one tile's S^T (lane = head, 16 tokens) in the log2
-// domain.  The running reference m is set by the first tile (or given by a
-// restart) and then kept: probabilities are exp2(s - m) <= 2^16 as long as no
-// row's maximum exceeds m by more than kRefSlack.  When one does (rare), the
-// function returns true and the block restarts the segment with the larger
-// reference (see the kernel).  The O^T accumulators are therefore only ever
-// MFMA-accumulated, read at the end or zeroed at a segment start -- never
-// rescaled in registers, which keeps all 256 of them in AGPRs.
-constexpr float kRefSlack = 16.f;
+// One direct-to-LDS DMA instruction: 64 lanes x 16 B from sbase + voff
+// (uniform base, 32-bit per-lane offset) to LDS address lds + 16 * lane.
+// Issued through asm in the SGPR-base form, so no 64-bit per-lane address
+// is formed; M0 (the LDS destination) is saved and restored around it, and
+// the wait states after the M0 write are covered by the s_nop.  The compiler
+// does not track this load: vmcnt is waited on explicitly (wait_tiles).
+__device__ __forceinline__ void dma16(const uint8_t *sbase, uint32_t voff, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(sbase), "s"(lds)
+      : "memory");
+}
+
+// DMA of a full tile (all 32 tokens inside the segment), issued in
+// per-wave instruction slots: a uniform tile base plus per-lane offsets
+// that are the same for every tile, so no per-tile vector address math.
+// Per-wave uniform parts of the DMA addresses.  Instruction ins = k*NW +
+// wave of a tile splits into a compile-time part (slot k) and these wave
+// terms: for one row per group, pi(k*NW + wave) = pi(k*NW) + 4*wave because
+// NW <= 4 only touches the low two bits of the token.
+struct WaveDma {
+  int src_kv, src_rope;  // source byte offsets (row terms)
+  int dst_kv, dst_rope;  // LDS byte offsets inside a stage
+};
+
+template <class SH, int NW>
+__device__ __forceinline__ WaveDma wave_dma(int wave) {
+  static_assert(NW == 1 || NW == 2 || NW == 4, "wave count");
+  WaveDma w;
+  w.src_kv = wave * SH::RPG * (SH::W * 2);
+  w.src_rope = wave * (64 / SH::RCH) * (SH::W * 2);
+  w.dst_kv = SH::RPG == 1 ? 4 * wave * SH::GS : wave * SH::GS;
+  w.dst_rope = wave * 1024;
+  return w;
+}
+
+struct FullTileDma {
+  const uint8_t *tile_base;
+  lds_char *stage;
+  int wave;
+  uint32_t v_kv, v_rope;
+  WaveDma w;
+};
+
+template <class SH, int NW>
+struct DmaSlots {
+  static constexpr int MI = (SH::INSTR + NW - 1) / NW;  // slots per wave
+  static constexpr bool EVEN = SH::INSTR % NW == 0 && SH::KV_INSTR % NW == 0;
+};
+
+// Hides a uniform value from loop-invariant code motion: addresses derived
+// from it are formed right where they are used instead of being hoisted
+// (dozens of per-instruction DMA addresses would otherwise occupy SGPRs).
+template <class T>
+__device__ __forceinline__ T fresh(T x) {
+  asm volatile("" : "+s"(x));
+  return x;
+}
+
+// Slot k of this wave: DMA instruction k * NW + wave of the tile.
+template <class SH, int NW>
+__device__ __forceinline__ void issue_full_one(const FullTileDma &d, int k) {
+  constexpr bool EVEN = DmaSlots<SH, NW>::EVEN;
+  const int ins0 = k * NW, ins = ins0 + d.wave;
+  if (EVEN || ins < SH::INSTR) {
+    const uint8_t *tb = fresh(d.tile_base);
+    const uint32_t st = fresh(lds_u32(d.stage));
+    if (EVEN ? ins0 < SH::KV_INSTR : ins < SH::KV_INSTR) {
+      // rows ins*RPG .. +RPG-1, lane covers row ins*RPG + lane/(ROW_B/16)
+      dma16(tb + (ins0 * SH::RPG * (SH::W * 2) + d.w.src_kv), d.v_kv,
+            st + (uint32_t)((SH::RPG == 1 ? SH::kv_row(ins0) : ins0 * SH::GS) + d.w.dst_kv));
+    } else {
+      // q0 = rope instruction index of wave 0 (negative for a wave whose
+      // first rope instruction follows wave 0's last c_kv one)
+      const int q0 = ins0 - SH::KV_INSTR;
+      dma16(tb + (q0 * (64 / SH::RCH) * (SH::W * 2) + d.w.src_rope), d.v_rope,
+            st + (uint32_t)(SH::KV_BYTES + q0 * 1024 + d.w.dst_rope));
+    }
+  }
+}
+
+// S^T of one tile: KSTEPS dependent MFMAs into the VGPR accumulator s,
+// operands read kPrefetch steps ahead (LDS latency is ~3-4 MFMAs).  With
+// DMA, this wave's instruction slots for the tile in `d` are spread evenly
+// over the MFMAs so the vector-memory issue hides under them.
+template <class SH, int NW, bool DMA>
+__device__ __forceinline__ void s_phase(const LaneAddr<SH> &la, const lds_char *st,
+                                        const bf16x8_t (&qf)[SH::KSTEPS], floatx16_t &s,
+                                        const FullTileDma &d) {
+  constexpr int D = kPrefetch < SH::KSTEPS ? kPrefetch : SH::KSTEPS;
+  constexpr int MI = DmaSlots<SH, NW>::MI;
+  const uint32_t st_base = lds_u32(st);
+  const uint32_t st_kv = st_base + la.s_kv;
+  bf16x8_t a[D + 1];
+  [&]<int... K>(std::integer_sequence<int, K...>) {
+    ([&] { if constexpr (K < D) a[K] = s_read<SH, K>(la, st_kv, st_base); }(), ...);
+    ([&] {
+      constexpr int kk = K;
+      // reads issued after read kk
+      constexpr int after = (kk + D - 1 < SH::KSTEPS - 1 ? D - 1 : SH::KSTEPS - 1 - kk);
+      wait_lgkm<after>();
+      arrived(a[kk % (D + 1)]);
+      if constexpr (kk == 0)
+        s = mfma_s_first(a[0], qf[0]);
+      else
+        mfma_s_acc(s, a[kk % (D + 1)], qf[kk]);
+      if constexpr (DMA) {
+#pragma unroll
+        for (int k = 0; k < MI; ++k)
+          if ((k * SH::KSTEPS) / MI == kk) issue_full_one<SH, NW>(d, k);
+      }
+      if constexpr (kk + D < SH::KSTEPS) a[(kk + D) % (D + 1)] = s_read<SH, kk + D>(la, st_kv, st_base);
+    }(), ...);
+  }(std::make_integer_sequence<int, SH::KSTEPS>{});
+  mfma_s_drain(s);
+}
+
+// Split of the O^T accumulation over the block's waves.  Every wave owns
+// the S^T / softmax of its 32 query rows; the P.V product is split by
+// (row block, column block) instead, so that each wave reads only its share
+// of V^T from LDS and takes P^T for all rows from a small LDS buffer.  With
+// CW column groups and RW = NW / CW row groups, wave w accumulates column
+// blocks w % CW + i * CW (i < NCB) for row blocks w / CW + r * RW (r < NRB).
+template <int R, int NW>
+struct PvSplit {
+  static constexpr int CB = R / 32;
+  static constexpr int CW = CB < NW ? CB : NW;
+  static constexpr int RW = NW / CW;
+  static constexpr int NCB = CB / CW;
+  static constexpr int NRB = NW / RW;
+  static_assert(NCB * NRB == CB, "accumulator count");
+};
+
+// P^T staging: one 80-byte row per query row holding the four 16-byte
+// B-operand chunks (k-step ks, half h) at ks*32 + h*16.  The 16-byte pad
+// spreads 16 consecutive rows over distinct LDS bank groups.
+constexpr int kPRow = 80;
 
 template <class SH>
-__device__ __forceinline__ bool softmax_tile(floatx16_t &s, float scale_log2, int tile_t0, int T,
-                                             int half, float &m_run, float &l_run,
-                                             bf16x8_t (&pb)[2], float &mt_out) {
-  float mt = -INFINITY;
+__device__ __forceinline__ void p_write(const LaneAddr<SH> &la, uint32_t pbuf,
+                                        const bf16x8_t (&pn)[2]) {
+  ds_w128<0>(pbuf + la.p_wr, pn[0]);
+  ds_w128<32>(pbuf + la.p_wr, pn[1]);
+}
+
+// O^T += V^T P^T for this wave's share of one tile: NCB x NRB x 2 MFMAs
+// into the AGPR accumulators.  P^T fragments of both k-steps are loaded
+// first, then the V^T fragments stream kPvAhead ahead of their MFMAs.
+constexpr int kPvAhead = 3;
+
+template <class SH, class PS, int J>
+__device__ __forceinline__ bf16x8_t v_frag(uint32_t vb) {
+  constexpr int ks = J / PS::NCB, i = J % PS::NCB;
+  return ds_tr2<ks * SH::HI16 + i * PS::CW * 64, SH::HI8>(vb);
+}
+
+template <class SH, class PS>
+__device__ __forceinline__ void pv_phase(const LaneAddr<SH> &la, const lds_char *st,
+                                         uint32_t pbuf, int cw,
+                                         floatx16_t (&o)[PS::NCB][PS::NRB]) {
+  constexpr int NA = 2 * PS::NCB;  // V^T fragments (k-step, column block)
+  constexpr int DA = kPvAhead < NA ? kPvAhead : NA;
+  const uint32_t vb = lds_u32(st) + la.v + cw * 64;
+  const uint32_t pb = pbuf + la.p_rd;
+  bf16x8_t b[2][PS::NRB], a[DA + 1];
+  [&]<int... R>(std::integer_sequence<int, R...>) {
+    ((b[0][R] = ds_b128<R * PS::RW * 32 * kPRow>(pb)), ...);
+    ((b[1][R] = ds_b128<R * PS::RW * 32 * kPRow + 32>(pb)), ...);
+  }(std::make_integer_sequence<int, PS::NRB>{});
+  [&]<int... J>(std::integer_sequence<int, J...>) {
+    ([&] { if constexpr (J < DA) a[J] = v_frag<SH, PS, J>(vb); }(), ...);
+    ([&] {
+      constexpr int j = J;
+      // two reads per V^T fragment issued after fragment j
+      constexpr int after = 2 * (j + DA - 1 < NA - 1 ? DA - 1 : NA - 1 - j);
+      wait_lgkm<after>();
+      arrived(a[j % (DA + 1)]);
+      if constexpr (j == 0) {  // the P^T fragments were read before V^T fragment 0
+#pragma unroll
+        for (int r = 0; r < PS::NRB; ++r) {
+          arrived(b[0][r]);
+          arrived(b[1][r]);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < PS::NRB; ++r)
+        o[j % PS::NCB][r] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            a[j % (DA + 1)], b[j / PS::NCB][r], o[j % PS::NCB][r], 0, 0, 0);
+      if constexpr (j + DA < NA) a[(j + DA) % (DA + 1)] = v_frag<SH, PS, j + DA>(vb);
+    }(), ...);
+  }(std::make_integer_sequence<int, NA>{});
+}
+
+// Online softmax in the log2 domain with a lazy fixed reference.  The
+// reference m (scaled units) is the first tile's row maximum, or the one a
+// restart hands in, and then stays fixed: p = exp2(s * scale_log2 - m) <=
+// 2^kRefSlack as long as no later score exceeds m by more than kRefSlack.
+// Each lane tracks the raw maximum of every tile it sees; after the segment
+// the block checks it, and in the rare case of an overflow redoes the
+// segment with the true maximum as reference (see the kernel).  The O^T
+// accumulators are therefore only ever MFMA-accumulated, zeroed at a
+// segment start or read at the end -- never rescaled in registers, which
+// keeps all 256 of them in AGPRs -- and the per-tile softmax has no branch,
+// so the scheduler can spread it over the P.V MFMAs.
+constexpr float kRefSlack = 16.f;
+
+// Token (within the tile) of S^T accumulator element j of this lane.
+__device__ __forceinline__ int tile_tok(int j, int half) {
+  return 8 * (j >> 2) + 4 * half + (j & 3);
+}
+
+// Raw (unscaled) maximum of this lane's 16 scores; with MASK, tokens at or
+// past `valid` are ignored.
+template <bool MASK>
+__device__ __forceinline__ float tile_max(const floatx16_t &s, int valid, int half) {
+  float x[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) x[j] = (!MASK || tile_tok(j, half) < valid) ? s[j] : -INFINITY;
+  float m01 = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+  float m23 = fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7]));
+  float m45 = fmaxf(fmaxf(x[8], x[9]), fmaxf(x[10], x[11]));
+  float m67 = fmaxf(fmaxf(x[12], x[13]), fmaxf(x[14], x[15]));
+  return fmaxf(fmaxf(m01, m23), fmaxf(m45, m67));
+}
+
+// p = exp2(s * sl2 - m) packed into the two bf16 B-operand fragments of
+// P^T; adds the tile's probability mass to l.  sl2 >= 0.
+template <bool MASK>
+__device__ __forceinline__ void tile_p(const floatx16_t &s, float sl2, float m, int valid,
+                                       int half, float &l, bf16x8_t (&pb)[2]) {
+  float p[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    const int tok = tile_t0 + 8 * (j >> 2) + 4 * half + (j & 3);
-    const float x = tok < T ? s[j] * scale_log2 : -INFINITY;
-    s[j] = x;
-    mt = fmaxf(mt, x);
+    p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j], sl2, -m));
+    if (MASK) p[j] = tile_tok(j, half) < valid ? p[j] : 0.f;
   }
-  mt = xor32_max(mt);
-  mt_out = mt;
-  if (m_run == -INFINITY) {
-    m_run = mt;  // first tile of the segment (or after a flush): o and l are zero
-  } else if (__ballot(mt > m_run + kRefSlack) != 0) {
-    return true;
-  }
+  float q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[i] = p[2 * i] + p[2 * i + 1];
+  l += ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     u32x4_t pk;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float p0 = exp2f(s[ks * 8 + 2 * i] - m_run);
-      const float p1 = exp2f(s[ks * 8 + 2 * i + 1] - m_run);
-      l_run += p0 + p1;
-      pk[i] = pack2_bf16(p0, p1);
-    }
+    for (int i = 0; i < 4; ++i) pk[i] = pack2_bf16(p[ks * 8 + 2 * i], p[ks * 8 + 2 * i + 1]);
     pb[ks] = __builtin_bit_cast(bf16x8_t, pk);
   }
-  return false;
 }
 
-// True when any wave of the block raised its reference-overflow flag.
-template <int NW>
-__device__ __forceinline__ bool any_flag(const volatile int *flags) {
-  int v = 0;
+template <class SH, int NW>
+__device__ __forceinline__ void issue_full_tile(const FullTileDma &d) {
 #pragma unroll
-  for (int w = 0; w < NW; ++w) v |= flags[w];
-  return v != 0;
+  for (int k = 0; k < DmaSlots<SH, NW>::MI; ++k) issue_full_one<SH, NW>(d, k);
+}
+
+// DMA of the segment's last, partial tile: tokens past `last` (the last
+// valid token, relative to the tile) re-load that token's row, which the
+// softmax masks.  Sources are the uniform tile base plus 32-bit per-lane
+// offsets; the LDS position (and rope swizzle) stays that of the unclamped
+// token.
+template <class SH, int NW>
+__device__ __forceinline__ void issue_clamped_tile(const uint8_t *__restrict__ tile_base,
+                                                   lds_char *stage, int wave, int lane, int last,
+                                                   const WaveDma &w) {
+  constexpr bool EVEN = DmaSlots<SH, NW>::EVEN;
+#pragma unroll
+  for (int ins0 = 0; ins0 < SH::INSTR; ins0 += NW) {
+    const int ins = ins0 + wave;
+    if (EVEN || ins < SH::INSTR) {
+      int t, c, base_b, dst;
+      if (EVEN ? ins0 < SH::KV_INSTR : ins < SH::KV_INSTR) {
+        t = ins * SH::RPG + lane / (SH::ROW_B / 16);
+        c = lane % (SH::ROW_B / 16);
+        base_b = 0;
+        dst = (SH::RPG == 1 ? SH::kv_row(ins0) : ins0 * SH::GS) + w.dst_kv;
+      } else {
+        const int q = ins - SH::KV_INSTR;
+        t = q * (64 / SH::RCH) + lane / SH::RCH;
+        c = (lane % SH::RCH) ^ (t & (SH::RCH - 1));
+        base_b = SH::ROW_B;
+        dst = SH::KV_BYTES + (ins0 - SH::KV_INSTR) * 1024 + w.dst_rope;
+      }
+      dma16(fresh(tile_base), (uint32_t)(min(t, last) * (SH::W * 2) + base_b + c * 16),
+            fresh(lds_u32(stage)) + (uint32_t)dst);
+    }
+  }
+}
+
+template <class SH, int NW>
+__device__ __forceinline__ void issue_any_tile(const uint8_t *__restrict__ seq_base, int tile_t0,
+                                               int seg_t1, lds_char *stage, int wave, int lane,
+                                               uint32_t v_kv, uint32_t v_rope, const WaveDma &w) {
+  const uint8_t *tile_base = seq_base + (int64_t)tile_t0 * (SH::W * 2);
+  if (tile_t0 + kTok <= seg_t1)
+    issue_full_tile<SH, NW>(FullTileDma{tile_base, stage, wave, v_kv, v_rope, w});
+  else
+    issue_clamped_tile<SH, NW>(tile_base, stage, wave, lane, seg_t1 - 1 - tile_t0, w);
+}
+
+// Block-wide flags and per-row floats in LDS, accessed through asm like
+// the rest of the kernel's LDS traffic.
+__device__ __forceinline__ void ds_w32(uint32_t addr, uint32_t v) {
+  asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v));
+}
+__device__ __forceinline__ uint32_t ds_r32(uint32_t addr) {
+  uint32_t r;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+__device__ __forceinline__ void arrived32(uint32_t &x) { asm volatile("" : "+v"(x)); }
+
+// True when any wave of the block raised its reference-overflow flag
+// (flags: NW words at LDS address `flags`; written before a barrier).
+template <int NW>
+__device__ __forceinline__ bool any_flag(uint32_t flags) {
+  uint32_t v[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) v[w] = ds_r32(flags + 4 * w);
+  wait_lgkm<0>();
+  uint32_t f = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    arrived32(v[w]);
+    f |= v[w];
+  }
+  return __builtin_amdgcn_readfirstlane(f) != 0;
+}
+
+// Dynamic LDS of one block: the NSTAGE tile ring, the P^T staging rows,
+// the per-row softmax denominators exchanged at the end of a segment and
+// the per-wave reference-overflow flags.
+template <int R, int DR, int NW, int NSTAGE>
+constexpr size_t decode_lds_bytes() {
+  return (size_t)NSTAGE * DecodeShape<R, DR>::STAGE_BYTES + NW * 32 * kPRow + NW * 32 * 4 +
+         NW * 4;
 }
 
 template <int R, int DR, int NW, int NSTAGE, typename QT>
@@ -322,51 +582,66 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
     float scale_log2, DecodePlanView plan, float *__restrict__ out, float *__restrict__ out_lse,
     float *__restrict__ part_o, float *__restrict__ part_lse) {
   using SH = DecodeShape<R, DR>;
+  using PS = PvSplit<R, NW>;
   static_assert(NSTAGE >= 3, "the pipelined loop keeps two stages resident");
   extern __shared__ __attribute__((aligned(16))) char ring_raw[];
-  __shared__ int ovf_flag[NW];
   lds_char *ring = (lds_char *)ring_raw;
+  lds_char *pbuf = ring + NSTAGE * SH::STAGE_BYTES;
+  const uint32_t l_rows = lds_u32(pbuf + NW * 32 * kPRow);  // NW*32 floats
+  const uint32_t ovf_flags = l_rows + NW * 32 * 4;         // NW words
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
-  const int n = lane & 31;     // head (query row) within the wave = MFMA column
+  const int n = lane & 31;     // row within a 32-row block = MFMA column
   const int half = lane >> 5;  // which 8-wide k half of an MFMA operand
-  const int row = blockIdx.y * (NW * 32) + wave * 32 + n;  // query row
+  const int row0 = blockIdx.y * (NW * 32);  // first query row of this block
+  const int row = row0 + wave * 32 + n;     // this lane's softmax row
   const bool row_ok = row < rows;
   const int row_c = row_ok ? row : rows - 1;
+  const int cw = wave % PS::CW, rg = wave / PS::CW;  // P.V share of this wave
   const int piece = blockIdx.x;
   const int my_instr = (SH::INSTR - wave + NW - 1) / NW;
+  // A negative scale is applied as |scale| with the sign folded into q
+  // (exact in bf16), so the raw score maximum is also the scaled one.
+  const uint32_t q_sign = scale_log2 < 0.f ? 0x80008000u : 0u;
+  const float sl2 = fabsf(scale_log2);
 
   LaneAddr<SH> la;
-  la.a_base = SH::kv_row(n) + half * 16;
-  la.rope_row = n * (DR * 2);
-  la.rope_mask = n & (SH::RCH - 1);
-  la.half = half;
+  la.s_kv = SH::kv_row(n) + half * 16;
+#pragma unroll
+  for (int rk = 0; rk < LaneAddr<SH>::ROPE_STEPS; ++rk)
+    la.s_rope[rk] = SH::KV_BYTES + n * (DR * 2) + (((2 * rk + half) ^ (n & (SH::RCH - 1))) * 16);
   {
     const int g = lane >> 4, sl = lane & 15;
     const int tok_a = (g >= 2 ? 4 : 0) + (sl >> 2);
     const int col_in = (g & 1) * 16 + 4 * (sl & 3);
-    la.v_base = SH::kv_row(tok_a) + (col_in >> 3) * 16 + (col_in & 7) * 2;
+    la.v = SH::kv_row(tok_a) + (col_in >> 3) * 16 + (col_in & 7) * 2;
   }
+  la.p_rd = (32 * rg + n) * kPRow + half * 16;
+  la.p_wr = (32 * wave + n) * kPRow + half * 16;
+  la.half = half;
+  const uint32_t pbuf_u = lds_u32(pbuf);
+  // per-lane source offsets of a full tile's DMA (see issue_tile)
+  const uint32_t v_kv = (lane / (SH::ROW_B / 16)) * (SH::W * 2) + (lane % (SH::ROW_B / 16)) * 16;
+  const WaveDma wd = wave_dma<SH, NW>(wave);
+  const uint32_t v_rope = (lane / SH::RCH) * (SH::W * 2) + SH::ROW_B +
+                          ((lane % SH::RCH) ^ ((lane / SH::RCH) & (SH::RCH - 1))) * 16;
 
   const int32_t s0 = plan.seg_start[piece], s1 = plan.seg_start[piece + 1];
   for (int32_t si = s0; si < s1; ++si) {
     const DecodeSegment sg = plan.segs[si];
-    const int64_t qrow = (int64_t)sg.seq * rows + row;
     const int64_t qrow_c = (int64_t)sg.seq * rows + row_c;
     const uint8_t *seq_base = pool + offsets[sg.seq] * (int64_t)(SH::W * 2);
 
     // Q fragment = B operand of S^T: dims kk*16 + 8*half .. +7 of this row.
     bf16x8_t qf[SH::KSTEPS];
+    const uint32_t keep = row_ok ? 0xffffffffu : 0u;
 #pragma unroll
     for (int kk = 0; kk < SH::KSTEPS; ++kk) {
       u32x4_t u = __builtin_bit_cast(u32x4_t, load_q8<R, DR, QT>(q_lat, q_rope, qrow_c,
                                                                   kk * 16 + half * 8));
-      const uint32_t keep = row_ok ? 0xffffffffu : 0u;
-      u[0] &= keep;
-      u[1] &= keep;
-      u[2] &= keep;
-      u[3] &= keep;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) u[i] = (u[i] ^ q_sign) & keep;
       qf[kk] = __builtin_bit_cast(bf16x8_t, u);
     }
 
@@ -374,100 +649,155 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
     const int ntiles = (T + kTok - 1) / kTok;
     auto stage = [&](int t) { return ring + (t % NSTAGE) * SH::STAGE_BYTES; };
 
-    floatx16_t o[SH::CB];
+    floatx16_t o[PS::NCB][PS::NRB];
     floatx16_t s;
-    bf16x8_t pb[2];
-    float m_run, l_run;
+    bf16x8_t pn[2];
+    float m_run, l_run, m_raw;
     float m_init = -INFINITY;  // reference to (re)start the segment with
     for (;;) {
 #pragma unroll
-      for (int cb = 0; cb < SH::CB; ++cb)
+      for (int i = 0; i < PS::NCB; ++i)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) o[cb][j] = 0.f;
-      m_run = m_init;
+        for (int r = 0; r < PS::NRB; ++r)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) o[i][r][j] = 0.f;
       l_run = 0.f;
-      if (lane == 0) ovf_flag[wave] = 0;
+      if (lane == 0) ds_w32(ovf_flags + 4 * wave, 0u);
 
       // prologue: NSTAGE-1 tiles in flight, then S and softmax of tile 0
 #pragma unroll
       for (int p = 0; p < NSTAGE - 1; ++p)
-        if (p < ntiles) issue_tile<SH, NW>(seq_base, sg.t0 + p * kTok, sg.t1, stage(p), wave, lane);
+        if (p < ntiles)
+          issue_any_tile<SH, NW>(seq_base, sg.t0 + p * kTok, sg.t1, stage(p), wave, lane, v_kv,
+                                 v_rope, wd);
       wait_tiles<SH, NW>(min(NSTAGE - 2, ntiles - 1), my_instr);
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
-      body<SH, true, false>(la, stage(0), stage(0), qf, s, pb, o);
-      float mt;
-      // tile 0 never overflows: m_init is -inf or covers every tile's max
-      (void)softmax_tile<SH>(s, scale_log2, 0, T, half, m_run, l_run, pb, mt);
-      float m_cand = fmaxf(m_run, mt);  // max over all tiles of the segment
+      s_phase<SH, NW, false>(la, stage(0), qf, s, FullTileDma{});
+      m_raw = tile_max<true>(s, T, half);
+      m_run = m_init == -INFINITY ? xor32_max(m_raw) * sl2 : m_init;
+      tile_p<true>(s, sl2, m_run, T, half, l_run, pn);
+      __builtin_amdgcn_sched_barrier(0);
 
-      // steady state: S^T of tile it+1 interleaved with P.V of tile it.  A
-      // reference overflow only raises a flag (the tile's P is left stale and
-      // the segment is redone below): the loop keeps a single exit.
-      for (int it = 0; it + 1 < ntiles; ++it) {
+      // Steady state, iteration it: publish P of tile it, S^T of tile it+1,
+      // then P.V of tile it with the softmax of tile it+1 spread over its
+      // MFMAs.  FAST iterations (the prefetched tile it+NSTAGE-1 is a full
+      // tile and tile it+1 is not the last) spread their DMA over the S^T
+      // MFMAs and carry no mask; the at most NSTAGE-1 tail iterations issue
+      // their (possibly clamped) DMA up front and mask the scores.
+      auto step = [&](auto fast, int it) __attribute__((always_inline)) {
+        constexpr bool FAST = decltype(fast)::value;
         // tile it+1 must be complete; tile it+2 (if issued) may stay in flight
-        wait_tiles<SH, NW>(min(NSTAGE - 3, ntiles - 2 - it), my_instr);
-        // All waves are past iteration it-1: stage (it-1) % NSTAGE is free and
-        // tile it+1 is visible to every wave.
+        if constexpr (FAST)
+          wait_tiles<SH, NW>(NSTAGE - 3, my_instr);
+        else
+          wait_tiles<SH, NW>(min(NSTAGE - 3, ntiles - 2 - it), my_instr);
+        // Barrier A: every wave is past iteration it-1, so stage (it-1) %
+        // NSTAGE and the P^T rows are free, and tile it+1 is visible.
         __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         const int nxt = it + NSTAGE - 1;
-        if (nxt < ntiles)
-          issue_tile<SH, NW>(seq_base, sg.t0 + nxt * kTok, sg.t1, stage(nxt), wave, lane);
+        if (!FAST && nxt < ntiles)
+          issue_any_tile<SH, NW>(seq_base, sg.t0 + nxt * kTok, sg.t1, stage(nxt), wave, lane,
+                                 v_kv, v_rope, wd);
+        p_write(la, pbuf_u, pn);
         __builtin_amdgcn_sched_barrier(0);
-        body<SH, true, true>(la, stage(it + 1), stage(it), qf, s, pb, o);
+        s_phase<SH, NW, FAST>(
+            la, stage(it + 1), qf, s,
+            FullTileDma{seq_base + (int64_t)(sg.t0 + nxt * kTok) * (SH::W * 2), stage(nxt), wave,
+                        v_kv, v_rope, wd});
+        // Barrier B: P^T of tile it is complete in LDS.
+        __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
+        __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        if (softmax_tile<SH>(s, scale_log2, (it + 1) * kTok, T, half, m_run, l_run, pb, mt) &&
-            lane == 0)
-          ovf_flag[wave] = 1;
-        m_cand = fmaxf(m_cand, mt);
+        const int valid = T - (it + 1) * kTok;
+        m_raw = fmaxf(m_raw, tile_max<!FAST>(s, valid, half));
+        pv_phase<SH, PS>(la, stage(it), pbuf_u, cw, o);
+        tile_p<!FAST>(s, sl2, m_run, valid, half, l_run, pn);
         __builtin_amdgcn_sched_barrier(0);
-      }
+      };
+      int it = 0;
+      for (; it + NSTAGE + 1 <= ntiles; ++it) step(std::true_type{}, it);
+      for (; it + 1 < ntiles; ++it) step(std::false_type{}, it);
       // P.V of the last tile
-      body<SH, false, true>(la, stage(ntiles - 1), stage(ntiles - 1), qf, s, pb, o);
-      // Every wave is done with the stages (the next segment's or attempt's
-      // prologue refills them) and every overflow flag is visible.
       __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
       __builtin_amdgcn_s_barrier();
-      if (!any_flag<NW>(ovf_flag)) break;
+      p_write(la, pbuf_u, pn);
+      __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
+      __builtin_amdgcn_s_barrier();
+      pv_phase<SH, PS>(la, stage(ntiles - 1), pbuf_u, cw, o);
+
+      // Overflow check: the segment's scaled maximum against the reference.
+      const float m_seg = xor32_max(m_raw) * sl2;
+      const bool ovf = __ballot(m_seg > m_run + kRefSlack) != 0;  // every lane votes
+      if (ovf && lane == 0) ds_w32(ovf_flags + 4 * wave, 1u);
+      // Every wave is done with the stages and the P^T rows (the next
+      // segment's or attempt's prologue refills them) and every overflow
+      // flag is visible.
+      __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
+      __builtin_amdgcn_s_barrier();
+      if (!any_flag<NW>(ovf_flags)) break;
       // Rare: some row's maximum outgrew the reference.  Redo the segment
-      // with a reference covering every tile's maximum (cannot overflow).
+      // with its true maximum as reference (cannot overflow).
       __builtin_amdgcn_s_barrier();  // all waves have read the flags
-      m_init = m_cand;
+      m_init = m_seg;
     }
 
-    // ---- finalise: combine the two half-waves' denominators and write
+    // ---- finalise: denominators of this wave's rows, shared with the
+    // waves holding other parts of those rows' O^T
     l_run = xor32_sum(l_run);
-    const float inv = 1.f / l_run;
     const float lse = (m_run + log2f(l_run)) * 0.69314718055994531f;
-    if (row_ok) {
-      float *dst;
-      if (sg.slot < 0) {
-        dst = out + qrow * R;
-        if (out_lse && half == 0) out_lse[qrow] = lse;
+    if (half == 0) ds_w32(l_rows + 4 * (wave * 32 + n), __builtin_bit_cast(uint32_t, l_run));
+    const int slot = sg.slot;
+    if (row_ok && half == 0) {
+      if (slot < 0) {
+        if (out_lse) out_lse[(int64_t)sg.seq * rows + row] = lse;
       } else {
-        const int64_t prow = (int64_t)sg.slot * rows + row;
-        dst = part_o + prow * R;
-        if (half == 0) part_lse[prow] = lse;
+        part_lse[(int64_t)slot * rows + row] = lse;
       }
-#pragma unroll
-      for (int cb = 0; cb < SH::CB; ++cb)
-#pragma unroll
-        for (int jq = 0; jq < 4; ++jq) {
-          floatx4_t v;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) v[i] = o[cb][jq * 4 + i] * inv;
-          *reinterpret_cast<floatx4_t *>(dst + cb * 32 + 8 * jq + 4 * half) = v;
-        }
     }
+    __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
+    __builtin_amdgcn_s_barrier();
+    // every denominator first: no LDS access between the output stores
+    float inv[PS::NRB];
+    {
+      uint32_t lv[PS::NRB];
+#pragma unroll
+      for (int r = 0; r < PS::NRB; ++r) lv[r] = ds_r32(l_rows + 4 * (32 * (rg + r * PS::RW) + n));
+      wait_lgkm<0>();
+#pragma unroll
+      for (int r = 0; r < PS::NRB; ++r) {
+        arrived32(lv[r]);
+        inv[r] = 1.f / __builtin_bit_cast(float, lv[r]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < PS::NRB; ++r) {
+      const int orow = row0 + 32 * (rg + r * PS::RW) + n;
+      if (orow < rows) {
+        float *dst = slot < 0 ? out + ((int64_t)sg.seq * rows + orow) * R
+                              : part_o + ((int64_t)slot * rows + orow) * R;
+#pragma unroll
+        for (int i = 0; i < PS::NCB; ++i) {
+          const int cb = cw + i * PS::CW;
+#pragma unroll
+          for (int jq = 0; jq < 4; ++jq) {
+            floatx4_t v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = o[i][r][jq * 4 + e] * inv[r];
+            *reinterpret_cast<floatx4_t *>(dst + cb * 32 + 8 * jq + 4 * half) = v;
+          }
+        }
+      }
+    }
+    // l_rows is rewritten by the next segment only after its prologue barrier
   }
 }
 
 template <int R, int DR, int NW, int NSTAGE>
 qmla_status launch_shape(const DecodeArgs &a, hipStream_t stream) {
-  using SH = DecodeShape<R, DR>;
-  const size_t lds = (size_t)NSTAGE * SH::STAGE_BYTES;
+  const size_t lds = decode_lds_bytes<R, DR, NW, NSTAGE>();
   const int passes = (a.rows + NW * 32 - 1) / (NW * 32);
   dim3 grid(a.blocks, passes), block(NW * 64);
   const float sl2 = a.scale * 1.4426950408889634f;
