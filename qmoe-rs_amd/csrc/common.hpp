@@ -67,6 +67,10 @@ inline hipStream_t as_stream(qmla_stream s) { return reinterpret_cast<hipStream_
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
 
+// Raises the dynamic LDS limit of kernel `fn` on the current device to at
+// least `bytes`; the attribute call is made once per (kernel, device).
+qmla_status ensure_dynamic_lds(const void *fn, size_t bytes);
+
 // ------------------------------------------------------------- device side
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));

@@ -266,15 +266,19 @@ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 }  // namespace
 
-DecodeWorkspace decode_workspace_layout(int32_t batch, int32_t rows, int32_t r, int32_t blocks) {
+DecodeWorkspace decode_workspace_layout(int32_t batch, int32_t rows, int32_t r, int32_t blocks,
+                                        bool mfma) {
   DecodeWorkspace w;
   w.slots = blocks + batch;
-  size_t plan = sizeof(int32_t) * (blocks + 1) + sizeof(DecodeSegment) * (size_t)(blocks + batch) +
-                2 * sizeof(int32_t) * batch;
+  size_t plan = mfma ? sizeof(int2) * (size_t)batch
+                     : sizeof(int32_t) * (blocks + 1) +
+                           sizeof(DecodeSegment) * (size_t)(blocks + batch) +
+                           2 * sizeof(int32_t) * batch;
+  const size_t prow = mfma ? (size_t)((rows + 31) / 32) * 32 : (size_t)rows;
   w.plan_bytes = align256(plan);
   w.part_o_off = w.plan_bytes;
-  w.part_lse_off = w.part_o_off + align256(sizeof(float) * (size_t)w.slots * rows * r);
-  w.total = w.part_lse_off + align256(sizeof(float) * (size_t)w.slots * rows);
+  w.part_lse_off = w.part_o_off + align256(sizeof(float) * (size_t)w.slots * prow * r);
+  w.total = w.part_lse_off + align256(sizeof(float) * (size_t)w.slots * prow);
   return w;
 }
 
@@ -382,15 +386,23 @@ qmla_status decode_impl(const qmla_decode_dims *d, const qmla_kv_cache *c, qmla_
   QMLA_REQUIRE(splits >= 0, QMLA_ERR_INVALID_ARG, "negative split count");
   QMLA_REQUIRE(std::isfinite(scale), QMLA_ERR_INVALID_ARG, "non-finite scale");
   const int32_t blocks = choose_blocks(d, c, splits);
-  DecodeWorkspace lay = decode_workspace_layout(d->batch, d->rows, d->kv_lora_rank, blocks);
+  const bool mfma = c->dtype == QMLA_BF16;
+  if (mfma)
+    QMLA_REQUIRE(decode_mfma_supported(d->rows, d->kv_lora_rank, d->rope_dim),
+                 QMLA_ERR_UNSUPPORTED, "bf16 decode for kv_lora_rank %d, rope %d",
+                 d->kv_lora_rank, d->rope_dim);
+  DecodeWorkspace lay = decode_workspace_layout(d->batch, d->rows, d->kv_lora_rank, blocks, mfma);
   QMLA_REQUIRE(ws != nullptr && ws_bytes >= lay.total, QMLA_ERR_WORKSPACE,
                "workspace of %zu bytes < required %zu", ws_bytes, lay.total);
   hipStream_t s = as_stream(stream);
-  DecodePlanView plan = decode_plan_view(ws, d->batch, blocks);
-  int64_t total = 0;
-  for (int32_t i = 0; i < d->batch; ++i) total += c->h_lens[i];
-  int32_t chunk = (int32_t)std::max<int64_t>(1, (total + blocks - 1) / blocks);
-  QMLA_TRY(launch_decode_plan(c, d->batch, blocks, chunk, plan, s));
+  DecodePlanView plan{};
+  if (!mfma) {
+    plan = decode_plan_view(ws, d->batch, blocks);
+    int64_t total = 0;
+    for (int32_t i = 0; i < d->batch; ++i) total += c->h_lens[i];
+    int32_t chunk = (int32_t)std::max<int64_t>(1, (total + blocks - 1) / blocks);
+    QMLA_TRY(launch_decode_plan(c, d->batch, blocks, chunk, plan, s));
+  }
   DecodeArgs a;
   a.cache = c;
   a.batch = d->batch;
@@ -404,20 +416,14 @@ qmla_status decode_impl(const qmla_decode_dims *d, const qmla_kv_cache *c, qmla_
   a.out = out;
   a.out_lse = out_lse;
   a.plan = plan;
+  a.seq_info = reinterpret_cast<int2 *>(ws);
   a.part_o = reinterpret_cast<float *>(static_cast<char *>(ws) + lay.part_o_off);
   a.part_lse = reinterpret_cast<float *>(static_cast<char *>(ws) + lay.part_lse_off);
   a.blocks = blocks;
-  if (c->dtype == QMLA_F32) {
-    QMLA_TRY(launch_decode_f32(a, s));
-  } else {
-    QMLA_REQUIRE(decode_mfma_supported(d->rows, d->kv_lora_rank, d->rope_dim),
-                 QMLA_ERR_UNSUPPORTED,
-                 "bf16 decode needs kv_lora_rank %% 32 == 0 and (rank + rope) %% 16 == 0");
-    QMLA_TRY(launch_decode_mfma(a, s));
-  }
-  QMLA_TRY(launch_decode_merge(d->batch, d->rows, d->kv_lora_rank, plan, a.part_o, a.part_lse, out,
-                               out_lse, s));
-  return QMLA_OK;
+  if (mfma) return launch_decode_mfma(a, s);  // decode + merge
+  QMLA_TRY(launch_decode_f32(a, s));
+  return launch_decode_merge(d->batch, d->rows, d->kv_lora_rank, plan, a.part_o, a.part_lse, out,
+                             out_lse, s);
 }
 
 }  // namespace
@@ -431,7 +437,9 @@ qmla_status qmla_decode_workspace_bytes_splits(const qmla_decode_dims *dims,
   QMLA_TRY(validate_decode(dims, cache));
   QMLA_REQUIRE(num_splits >= 0, QMLA_ERR_INVALID_ARG, "negative split count");
   int32_t blocks = choose_blocks(dims, cache, num_splits);
-  *bytes = decode_workspace_layout(dims->batch, dims->rows, dims->kv_lora_rank, blocks).total;
+  *bytes = decode_workspace_layout(dims->batch, dims->rows, dims->kv_lora_rank, blocks,
+                                   cache->dtype == QMLA_BF16)
+               .total;
   return QMLA_OK;
 }
 

@@ -296,6 +296,12 @@ __device__ __forceinline__ T fresh(T x) {
   asm volatile("" : "+s"(x));
   return x;
 }
+// Per-lane counterpart: values derived from it after the hot loop are not
+// computed before the loop (and then kept, or spilled, across it).
+__device__ __forceinline__ int vfresh(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
 
 // Slot k of this wave: DMA instruction k * NW + wave of the tile.
 template <class SH, int NW>
@@ -500,9 +506,10 @@ __device__ __forceinline__ void issue_full_tile(const FullTileDma &d) {
 // token.
 template <class SH, int NW>
 __device__ __forceinline__ void issue_clamped_tile(const uint8_t *__restrict__ tile_base,
-                                                   lds_char *stage, int wave, int lane, int last,
-                                                   const WaveDma &w) {
+                                                   lds_char *stage, int wave, int lane_in,
+                                                   int last, const WaveDma &w) {
   constexpr bool EVEN = DmaSlots<SH, NW>::EVEN;
+  const int lane = vfresh(lane_in);
 #pragma unroll
   for (int ins0 = 0; ins0 < SH::INSTR; ins0 += NW) {
     const int ins = ins0 + wave;
@@ -566,20 +573,116 @@ __device__ __forceinline__ bool any_flag(uint32_t flags) {
   return __builtin_amdgcn_readfirstlane(f) != 0;
 }
 
+// ---- in-kernel split plan.  The concatenated tokens of the batch are cut
+// into gridDim.x pieces of `chunk` tokens; piece i covers [i*chunk,
+// (i+1)*chunk).  A (piece, sequence) overlap is a segment; every segment
+// writes a partial result to its own slot: sequence b owns slots
+// sb[b] .. sb[b] + ns[b] - 1 (ns[b] = pieces it touches), in piece order.
+// Each block derives its own segments (no separate planning launch): the
+// length prefix sums are rebuilt in the idle stage ring, and up to kSegCap
+// segment descriptors are kept in LDS; a block with more segments plans
+// again when its list runs out.  The block whose piece holds a sequence's
+// first token (blockIdx.y == 0) records {sb, ns} for the merge.
+constexpr int kSegCap = 64;
+
+struct SegDesc {
+  int32_t seq, t0, t1, slot;
+};
+
+// Exclusive scan of a[0..n) in LDS by NT threads; returns the total.
+template <int NT>
+__device__ int32_t lds_exscan(int32_t *a, int32_t n, int32_t *tmp) {
+  const int tid = threadIdx.x;
+  const int per = (n + NT - 1) / NT;
+  const int lo = min(n, tid * per), hi = min(n, lo + per);
+  int32_t local = 0;
+  for (int i = lo; i < hi; ++i) local += a[i];
+  tmp[tid] = local;
+  __syncthreads();
+  for (int off = 1; off < NT; off <<= 1) {
+    const int32_t v = tid >= off ? tmp[tid - off] : 0;
+    __syncthreads();
+    tmp[tid] += v;
+    __syncthreads();
+  }
+  int32_t run = tid > 0 ? tmp[tid - 1] : 0;
+  const int32_t total = tmp[NT - 1];
+  for (int i = lo; i < hi; ++i) {
+    const int32_t v = a[i];
+    a[i] = run;
+    run += v;
+  }
+  __syncthreads();
+  return total;
+}
+
+// One planning round: fills list[0..count) with this block's segments of
+// sequences >= from, sets *next to the first sequence not listed (batch
+// when done).  scratch: 2 * (batch + 1) + NT int32 of idle LDS.
+template <int NT>
+__device__ void plan_round(const int32_t *__restrict__ lens, int32_t batch, int32_t from,
+                           int32_t *scratch, SegDesc *list, int32_t *meta,
+                           int2 *__restrict__ seq_info) {
+  const int tid = threadIdx.x;
+  const int blocks = gridDim.x, piece = blockIdx.x;
+  int32_t *P = scratch, *SB = scratch + batch + 1, *tmp = SB + batch + 1;
+  for (int b = tid; b < batch; b += NT) P[b] = lens[b];
+  __syncthreads();
+  const int32_t N = lds_exscan<NT>(P, batch, tmp);
+  if (tid == 0) P[batch] = N;
+  const int32_t chunk = max(1, (N + blocks - 1) / blocks);
+  __syncthreads();
+  for (int b = tid; b < batch; b += NT) {
+    const int32_t p0 = P[b], p1 = P[b + 1];
+    SB[b] = p1 > p0 ? (p1 - 1) / chunk - p0 / chunk + 1 : 0;
+  }
+  __syncthreads();
+  (void)lds_exscan<NT>(SB, batch, tmp);
+  if (from == 0 && blockIdx.y == 0) {
+    for (int b = tid; b < batch; b += NT) {
+      const int32_t p0 = P[b], p1 = P[b + 1];
+      if (min(p0 / chunk, blocks - 1) == piece)
+        seq_info[b] = make_int2(SB[b], p1 > p0 ? (p1 - 1) / chunk - p0 / chunk + 1 : 0);
+    }
+  }
+  if (tid == 0) {
+    const int32_t start = min(piece * chunk, N), end = min(start + chunk, N);
+    // first sequence >= from whose tokens reach past start
+    int32_t lo = from, hi = batch;
+    while (lo < hi) {
+      const int32_t mid = (lo + hi) >> 1;
+      if (P[mid + 1] > start) hi = mid; else lo = mid + 1;
+    }
+    int32_t cnt = 0, b = lo;
+    for (; b < batch && P[b] < end && cnt < kSegCap; ++b) {
+      const int32_t p0 = P[b], p1 = P[b + 1];
+      if (p1 <= p0) continue;
+      list[cnt++] = SegDesc{b, max(start, p0) - p0, min(end, p1) - p0, SB[b] + (piece - p0 / chunk)};
+    }
+    meta[0] = cnt;
+    meta[1] = (b < batch && P[b] < end) ? b : batch;
+  }
+  __syncthreads();
+}
+
 // Dynamic LDS of one block: the NSTAGE tile ring, the P^T staging rows,
-// the per-row softmax denominators exchanged at the end of a segment and
-// the per-wave reference-overflow flags.
+// the per-row softmax denominators exchanged at the end of a segment, the
+// per-wave reference-overflow flags and the segment list (+ 2 words).
 template <int R, int DR, int NW, int NSTAGE>
 constexpr size_t decode_lds_bytes() {
   return (size_t)NSTAGE * DecodeShape<R, DR>::STAGE_BYTES + NW * 32 * kPRow + NW * 32 * 4 +
-         NW * 4;
+         NW * 4 + kSegCap * sizeof(SegDesc) + 16;
 }
 
+// Partial results: slot-major, then 32-row block, then 32-column block; a
+// block is 4 KB in the MFMA accumulator order [jq][lane][4] (element j of
+// lane l: row l % 32, column 8 (j / 4) + 4 (l / 32) + j % 4), so each store
+// instruction writes 1 KB contiguously.  part_lse: [slot][rows padded to 32].
 template <int R, int DR, int NW, int NSTAGE, typename QT>
 __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
     const uint8_t *__restrict__ pool, const int64_t *__restrict__ offsets,
-    const QT *__restrict__ q_lat, const QT *__restrict__ q_rope, int32_t rows,
-    float scale_log2, DecodePlanView plan, float *__restrict__ out, float *__restrict__ out_lse,
+    const int32_t *__restrict__ lens, int32_t batch, const QT *__restrict__ q_lat,
+    const QT *__restrict__ q_rope, int32_t rows, float scale_log2, int2 *__restrict__ seq_info,
     float *__restrict__ part_o, float *__restrict__ part_lse) {
   using SH = DecodeShape<R, DR>;
   using PS = PvSplit<R, NW>;
@@ -589,6 +692,10 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
   lds_char *pbuf = ring + NSTAGE * SH::STAGE_BYTES;
   const uint32_t l_rows = lds_u32(pbuf + NW * 32 * kPRow);  // NW*32 floats
   const uint32_t ovf_flags = l_rows + NW * 32 * 4;         // NW words
+  lds_char *seg_lds = pbuf + NW * 32 * kPRow + NW * 32 * 4 + NW * 4;
+  SegDesc *seg_list = (SegDesc *)seg_lds;                   // kSegCap entries
+  int32_t *seg_meta = (int32_t *)(seg_lds + kSegCap * sizeof(SegDesc));
+  const int row_blocks = (rows + 31) / 32;  // of the padded partial layout
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -599,7 +706,6 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
   const bool row_ok = row < rows;
   const int row_c = row_ok ? row : rows - 1;
   const int cw = wave % PS::CW, rg = wave / PS::CW;  // P.V share of this wave
-  const int piece = blockIdx.x;
   const int my_instr = (SH::INSTR - wave + NW - 1) / NW;
   // A negative scale is applied as |scale| with the sign folded into q
   // (exact in bf16), so the raw score maximum is also the scaled one.
@@ -627,9 +733,20 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
   const uint32_t v_rope = (lane / SH::RCH) * (SH::W * 2) + SH::ROW_B +
                           ((lane % SH::RCH) ^ ((lane / SH::RCH) & (SH::RCH - 1))) * 16;
 
-  const int32_t s0 = plan.seg_start[piece], s1 = plan.seg_start[piece + 1];
-  for (int32_t si = s0; si < s1; ++si) {
-    const DecodeSegment sg = plan.segs[si];
+  int32_t next_seq = 0;
+  do {
+  plan_round<NW * 64>(lens, batch, next_seq, (int32_t *)ring_raw, seg_list, seg_meta, seq_info);
+  const int32_t nseg = __builtin_amdgcn_readfirstlane(seg_meta[0]);
+  next_seq = __builtin_amdgcn_readfirstlane(seg_meta[1]);
+  for (int32_t si = 0; si < nseg; ++si) {
+    SegDesc sg;
+    {
+      const SegDesc d = seg_list[si];
+      sg.seq = __builtin_amdgcn_readfirstlane(d.seq);
+      sg.t0 = __builtin_amdgcn_readfirstlane(d.t0);
+      sg.t1 = __builtin_amdgcn_readfirstlane(d.t1);
+      sg.slot = __builtin_amdgcn_readfirstlane(d.slot);
+    }
     const int64_t qrow_c = (int64_t)sg.seq * rows + row_c;
     const uint8_t *seq_base = pool + offsets[sg.seq] * (int64_t)(SH::W * 2);
 
@@ -745,18 +862,16 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
     }
 
     // ---- finalise: denominators of this wave's rows, shared with the
-    // waves holding other parts of those rows' O^T
+    // waves holding other parts of those rows' O^T.  Lane-derived addresses
+    // are formed here from an opaque lane index (nothing kept across the
+    // loop for them).
+    const int fl = vfresh(lane), fn = fl & 31, fh = fl >> 5;
     l_run = xor32_sum(l_run);
     const float lse = (m_run + log2f(l_run)) * 0.69314718055994531f;
-    if (half == 0) ds_w32(l_rows + 4 * (wave * 32 + n), __builtin_bit_cast(uint32_t, l_run));
+    const int frow = row0 + wave * 32 + fn;
+    if (fh == 0) ds_w32(l_rows + 4 * (wave * 32 + fn), __builtin_bit_cast(uint32_t, l_run));
     const int slot = sg.slot;
-    if (row_ok && half == 0) {
-      if (slot < 0) {
-        if (out_lse) out_lse[(int64_t)sg.seq * rows + row] = lse;
-      } else {
-        part_lse[(int64_t)slot * rows + row] = lse;
-      }
-    }
+    if (fh == 0) part_lse[(int64_t)slot * (row_blocks * 32) + frow] = lse;
     __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
     __builtin_amdgcn_s_barrier();
     // every denominator first: no LDS access between the output stores
@@ -764,7 +879,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
     {
       uint32_t lv[PS::NRB];
 #pragma unroll
-      for (int r = 0; r < PS::NRB; ++r) lv[r] = ds_r32(l_rows + 4 * (32 * (rg + r * PS::RW) + n));
+      for (int r = 0; r < PS::NRB; ++r) lv[r] = ds_r32(l_rows + 4 * (32 * (rg + r * PS::RW) + fn));
       wait_lgkm<0>();
 #pragma unroll
       for (int r = 0; r < PS::NRB; ++r) {
@@ -774,24 +889,86 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
     }
 #pragma unroll
     for (int r = 0; r < PS::NRB; ++r) {
-      const int orow = row0 + 32 * (rg + r * PS::RW) + n;
-      if (orow < rows) {
-        float *dst = slot < 0 ? out + ((int64_t)sg.seq * rows + orow) * R
-                              : part_o + ((int64_t)slot * rows + orow) * R;
+      const int rb = blockIdx.y * NW + rg + r * PS::RW;  // 32-row block of the padded rows
+      float *blk = part_o + (((int64_t)slot * row_blocks + rb) * (R / 32)) * 1024 + fl * 4;
 #pragma unroll
-        for (int i = 0; i < PS::NCB; ++i) {
-          const int cb = cw + i * PS::CW;
+      for (int i = 0; i < PS::NCB; ++i) {
+        const int cb = cw + i * PS::CW;
 #pragma unroll
-          for (int jq = 0; jq < 4; ++jq) {
-            floatx4_t v;
+        for (int jq = 0; jq < 4; ++jq) {
+          floatx4_t v;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = o[i][r][jq * 4 + e] * inv[r];
-            *reinterpret_cast<floatx4_t *>(dst + cb * 32 + 8 * jq + 4 * half) = v;
-          }
+          for (int e = 0; e < 4; ++e) v[e] = o[i][r][jq * 4 + e] * inv[r];
+          *reinterpret_cast<floatx4_t *>(blk + cb * 1024 + jq * 256) = v;
         }
       }
     }
     // l_rows is rewritten by the next segment only after its prologue barrier
+  }
+  // the next planning round reuses the stage ring: every wave is done with it
+  __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
+  __builtin_amdgcn_s_barrier();
+  } while (next_seq < batch);
+}
+
+// Log-sum-exp merge of the partial slots into the row-major output.  One
+// wave per (sequence, 32-row block, 32-column block): per-row weights
+// exp(lse_s - max) from the slots' lse, the weighted sum of the slots' 4 KB
+// blocks, then an LDS transpose so the output is written as whole 128-byte
+// row segments.  Sequences without tokens get zeros and lse = -inf.
+template <int R>
+__global__ __launch_bounds__(256) void k_decode_merge_frag(
+    int32_t rows, int32_t row_blocks, const int2 *__restrict__ seq_info,
+    const float *__restrict__ part_o, const float *__restrict__ part_lse, float *__restrict__ out,
+    float *__restrict__ out_lse) {
+  constexpr int CB = R / 32;
+  __shared__ float tile[4][32][33];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int cb = blockIdx.y * 4 + wave;
+  if (cb >= CB) return;
+  const int b = blockIdx.x / row_blocks, rb = blockIdx.x % row_blocks;
+  const int n = lane & 31, half = lane >> 5;
+  const int row = rb * 32 + n;
+  const int2 si = seq_info[b];
+  const int32_t sb = si.x, ns = si.y;
+  const int rows_pad = row_blocks * 32;
+  float acc[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = 0.f;
+  float mx = -INFINITY, wsum = 0.f;
+  for (int k = 0; k < ns; ++k) mx = fmaxf(mx, part_lse[(int64_t)(sb + k) * rows_pad + row]);
+  for (int k = 0; k < ns; ++k) {
+    const float w = expf(part_lse[(int64_t)(sb + k) * rows_pad + row] - mx);
+    wsum += w;
+    const float *blk =
+        part_o + (((int64_t)(sb + k) * row_blocks + rb) * CB + cb) * 1024 + lane * 4;
+#pragma unroll
+    for (int jq = 0; jq < 4; ++jq) {
+      const floatx4_t v = *reinterpret_cast<const floatx4_t *>(blk + jq * 256);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[jq * 4 + e] += w * v[e];
+    }
+  }
+  const float inv = ns > 0 ? 1.f / wsum : 0.f;
+#pragma unroll
+  for (int jq = 0; jq < 4; ++jq)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tile[wave][n][8 * jq + 4 * half + e] = acc[jq * 4 + e] * inv;
+  if (cb == 0 && half == 0 && out_lse && row < rows)
+    out_lse[(int64_t)b * rows + row] = ns > 0 ? mx + logf(wsum) : -INFINITY;
+  __builtin_amdgcn_wave_barrier();
+  // lane l: rows l / 8 + 8 k, columns 4 (l % 8) .. + 3
+  const int c4 = (lane & 7) * 4;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int rl = (lane >> 3) + 8 * k;
+    const int orow = rb * 32 + rl;
+    if (orow < rows) {
+      floatx4_t v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = tile[wave][rl][c4 + e];
+      *reinterpret_cast<floatx4_t *>(out + ((int64_t)b * rows + orow) * R + cb * 32 + c4) = v;
+    }
   }
 }
 
@@ -804,20 +981,23 @@ qmla_status launch_shape(const DecodeArgs &a, hipStream_t stream) {
   const uint8_t *pool = static_cast<const uint8_t *>(a.cache->rows);
   if (a.q_dtype == QMLA_BF16) {
     auto k = k_decode_mfma<R, DR, NW, NSTAGE, uint16_t>;
-    QMLA_HIP(hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 (int)lds));
-    k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, (const uint16_t *)a.q_lat,
-                                    (const uint16_t *)a.q_rope, a.rows, sl2, a.plan, a.out,
-                                    a.out_lse, a.part_o, a.part_lse);
+    QMLA_TRY(ensure_dynamic_lds((const void *)k, lds));
+    k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, a.cache->d_lens, a.batch,
+                                    (const uint16_t *)a.q_lat, (const uint16_t *)a.q_rope, a.rows,
+                                    sl2, a.seq_info, a.part_o, a.part_lse);
   } else {
     auto k = k_decode_mfma<R, DR, NW, NSTAGE, float>;
-    QMLA_HIP(hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 (int)lds));
-    k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, (const float *)a.q_lat,
-                                    (const float *)a.q_rope, a.rows, sl2, a.plan, a.out,
-                                    a.out_lse, a.part_o, a.part_lse);
+    QMLA_TRY(ensure_dynamic_lds((const void *)k, lds));
+    k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, a.cache->d_lens, a.batch,
+                                    (const float *)a.q_lat, (const float *)a.q_rope, a.rows, sl2,
+                                    a.seq_info, a.part_o, a.part_lse);
   }
   QMLA_LAUNCH_CHECK("k_decode_mfma");
+  const int row_blocks = (a.rows + 31) / 32;
+  dim3 mgrid((unsigned)(a.batch * row_blocks), (R / 32 + 3) / 4);
+  k_decode_merge_frag<R><<<mgrid, dim3(256), 0, stream>>>(a.rows, row_blocks, a.seq_info,
+                                                          a.part_o, a.part_lse, a.out, a.out_lse);
+  QMLA_LAUNCH_CHECK("k_decode_merge_frag");
   return QMLA_OK;
 }
 

@@ -56,6 +56,9 @@ struct DecodePlanView {
 // Workspace layout for a decode call with `blocks` pieces:
 //   plan (seg_start, segs, seq tables), then slots x rows x r f32 partial
 //   outputs and slots x rows f32 partial log-sum-exp.
+// The bf16 MFMA path plans inside its kernel: instead of the plan it keeps
+// per-sequence {first slot, slot count} (int2 x batch), and its partial rows
+// are padded to a multiple of 32 (fragment-major layout, see decode_mfma).
 struct DecodeWorkspace {
   size_t plan_bytes = 0;
   size_t part_o_off = 0;
@@ -64,7 +67,8 @@ struct DecodeWorkspace {
   int32_t slots = 0;
 };
 
-DecodeWorkspace decode_workspace_layout(int32_t batch, int32_t rows, int32_t r, int32_t blocks);
+DecodeWorkspace decode_workspace_layout(int32_t batch, int32_t rows, int32_t r, int32_t blocks,
+                                        bool mfma);
 DecodePlanView decode_plan_view(void *ws, int32_t batch, int32_t blocks);
 
 qmla_status launch_decode_plan(const qmla_kv_cache *cache, int32_t batch, int32_t blocks,
@@ -83,7 +87,8 @@ struct DecodeArgs {
   float scale;
   float *out;         // [batch, rows, r]
   float *out_lse;     // [batch, rows] or null
-  DecodePlanView plan;
+  DecodePlanView plan;  // f32 path
+  int2 *seq_info;       // MFMA path: [batch] {first slot, slot count}
   float *part_o;
   float *part_lse;
   int32_t blocks;

@@ -301,8 +301,10 @@ size_t decode_bytes_for(const qmla_layer *L, const qmla_kv_cache *c, int32_t bat
   if (cus <= 0) cus = 256;
   int64_t blocks = std::max<int64_t>(1, std::min<int64_t>((int64_t)cus * 4, (total + 255) / 256));
   (void)L;
-  return decode_workspace_layout(batch, seq * L->cfg.heads, L->cfg.kv_lora_rank, (int32_t)blocks)
-      .total;
+  const int32_t rows = seq * L->cfg.heads;
+  return std::max(
+      decode_workspace_layout(batch, rows, L->cfg.kv_lora_rank, (int32_t)blocks, false).total,
+      decode_workspace_layout(batch, rows, L->cfg.kv_lora_rank, (int32_t)blocks, true).total);
 }
 
 }  // namespace

@@ -356,8 +356,7 @@ qmla_status launch_prefill_shape(const qmla_prefill_dims &d, const uint16_t *q_n
   QMLA_REQUIRE(nblocks <= 0x7fffffff, QMLA_ERR_SHAPE, "too many query tiles");
   const size_t lds = (size_t)kPStages * SH::STAGE_BYTES;
   auto kern = k_prefill_mfma<DN, DR, DV>;
-  QMLA_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                               (int)lds));
+  QMLA_TRY(ensure_dynamic_lds((const void *)kern, lds));
   kern<<<dim3((unsigned)nblocks), dim3(kPWaves * 64), lds, stream>>>(
       q_nope, q_rope, k, k_rope, v, d, scale * 1.4426950408889634f, causal, out, n_qtiles);
   QMLA_LAUNCH_CHECK("k_prefill_mfma");

@@ -7,6 +7,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <vector>
 
@@ -42,6 +43,19 @@ int device_cu_count() {
     cached[dev] = n;
   }
   return cached[dev];
+}
+
+qmla_status ensure_dynamic_lds(const void *fn, size_t bytes) {
+  static std::mutex mu;
+  static std::map<std::pair<const void *, int>, size_t> done;
+  int dev = 0;
+  QMLA_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(mu);
+  size_t &have = done[{fn, dev}];
+  if (have >= bytes) return QMLA_OK;
+  QMLA_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
+  have = bytes;
+  return QMLA_OK;
 }
 
 // ------------------------------------------------------------- kernels ----
