@@ -2,23 +2,30 @@
 """bench.py -- MI355X benchmark of the MLA attention hot path.
 
 Headline workload (one step = one absorbed-latent decode over the batch's
-latent cache, i.e. one attention layer's decode kernels):
+latent cache, i.e. one attention layer's decode: the decode kernel and its
+split-KV merge):
   128 heads, kv_lora_rank 512, rope 64, batch 64, ragged contexts
   U[1024, 32768] + 1 (seeded), bf16 latent cache, scale 1/sqrt(192).
-value = decode tokens/s (batch / step time); the roofline is HBM bytes of
-the latent cache (sum_b T_b * 1152 B) per step against 8 TB/s.
+value = decode tokens/s (batch / step time), the step time from one HIP event
+pair on the launch stream around exactly --steps back-to-back steps (after
+--warmup untimed ones).  roofline: latent-cache bytes (sum_b T_b * 1152 B)
+per step against 8 TB/s; traffic: HBM bytes per step from the committed
+rocprofv3 counter summary (profiles/decode_v3_pmc.md).
 
-Secondary lines (same JSON object, "secondary"): 16-head V2-Lite decode
-(batch 32, 4096 + 1 tokens), causal prefill (batch 4, 2048 tokens, 16 heads)
-and chunked prefill (batch 8, 8192 cached + 512 new, 128 heads), the
-prefills reported in TFLOP/s of unmasked attention work (MHA form,
-dqk 192 + dv 128) against the 2.5 PFLOP/s bf16 dense peak.
+Secondary lines (same JSON object, "secondary"): 16-head decode (batch 32,
+4096 + 1 tokens), causal prefill (batch 4, 2048 tokens, 16 heads) and chunked
+prefill (batch 8, 8192 cached + 512 new, 128 heads), the prefills in TFLOP/s
+of unmasked attention work (MHA form, dqk 192 + dv 128) against the
+2.5 PFLOP/s bf16 dense peak.
 
 Inputs are generated on the device (seeded) before the timed region.  The
 decode caches rotate over replicas totalling >= 2 GB so consecutive steps
 never re-read a cache that could still sit in the 256 MB Infinity Cache.
+cpu_baseline: the oracle's C restatement of the decode on the host cores,
+on a bounded sample (>= 10 s), scaled to the full batch.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+       python bench.py --calibrate   (copy kernel for scaling PMC counters)
 """
 from __future__ import annotations
 
@@ -61,20 +68,21 @@ def fill_bf16(dst_ptr: int, n: int, seed: int, tmp: qmla.DeviceBuffer, stream):
 
 
 def time_steps(step, steps: int, warmup: int, stream):
-    """Runs warmup + timed steps; returns (wall ms per step, per-step event ms)."""
+    """Runs warmup steps, then times exactly `steps` back-to-back steps with
+    one HIP event pair on the launch stream (synchronised on both sides).
+    Returns (wall ms per step, event ms per step)."""
     for i in range(warmup):
         step(i)
     stream.sync()
-    evs = [(qmla.Event(), qmla.Event()) for _ in range(steps)]
+    e0, e1 = qmla.Event(), qmla.Event()
     t0 = time.perf_counter()
+    e0.record(stream)
     for i in range(steps):
-        evs[i][0].record(stream)
         step(warmup + i)
-        evs[i][1].record(stream)
+    e1.record(stream)
     stream.sync()
     wall = (time.perf_counter() - t0) * 1e3 / steps
-    ev = np.array([a.elapsed_ms(b) for a, b in evs])
-    return wall, ev
+    return wall, e0.elapsed_ms(e1) / steps
 
 
 class DecodeBench:
@@ -111,15 +119,13 @@ class DecodeBench:
 
     def run(self, steps, warmup):
         wall, ev = time_steps(self.step, steps, warmup, self.stream)
-        t = float(np.median(ev)) * 1e-3
+        t = ev * 1e-3
         gbs = self.cache_bytes / t / 1e9
         flops = self.tokens * self.heads * (2 * ROW_ELEMS + 2 * 512)
         return {
-            "tok_s": self.batch / (wall * 1e-3),
-            "ms_per_step": wall,
-            "event_ms_median": float(np.median(ev)),
-            "event_ms_p10": float(np.percentile(ev, 10)),
-            "event_ms_p90": float(np.percentile(ev, 90)),
+            "tok_s": self.batch / t,
+            "ms_per_step": ev,
+            "wall_ms_per_step": wall,
             "hbm_gbs": gbs,
             "hbm_frac": gbs / HBM_PEAK_GBS,
             "mfma_tflops": flops / t / 1e12,
@@ -155,40 +161,91 @@ class PrefillBench:
 
     def run(self, steps, warmup):
         wall, ev = time_steps(self.step, steps, warmup, self.stream)
-        t = float(np.median(ev)) * 1e-3
-        tf = self.flops / t / 1e12
-        return {"tflops": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS, "ms_per_step": wall,
-                "event_ms_median": float(np.median(ev)), "gflop_per_step": self.flops / 1e9}
+        tf = self.flops / (ev * 1e-3) / 1e12
+        return {"tflops": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS, "ms_per_step": ev,
+                "wall_ms_per_step": wall, "gflop_per_step": self.flops / 1e9}
 
 
-def cpu_baseline(lens, heads, sample_seqs):
+def cpu_baseline(lens, heads, sample_seqs, min_seconds=10.0):
     """The oracle's absorbed-latent decode (the CPU restatement of the
-    reference path), timed on a sample of the same workload."""
+    reference path), timed on the host cores on a bounded sample of the same
+    workload: the first `sample_seqs` sequences, repeated until at least
+    `min_seconds` have elapsed, scaled by token count to the full batch.  A
+    single-thread figure on a smaller sample is reported beside it."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O  # checker library, used here only as the CPU baseline
+
+    def timed(sample, threads, min_s):
+        O.set_num_threads(threads)
+        rows = O.normal((int(sample.sum()), ROW_ELEMS), 4242)
+        ql = O.normal((len(sample), heads, 512), 4243)
+        qr = O.normal((len(sample), heads, 64), 4244)
+        offs = np.concatenate([[0], np.cumsum(sample)[:-1]]).astype(np.int64)
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            O.decode_absorbed(ql, qr, rows, offs, sample, SCALE)
+            reps += 1
+            dt = time.perf_counter() - t0
+            if dt >= min_s:
+                return dt / reps, reps
+
+    total = float(np.sum(lens))
+    threads = O.num_threads()
     sample = np.asarray(lens[:sample_seqs], np.int32)
-    rows = O.normal((int(sample.sum()), ROW_ELEMS), 4242)
-    ql = O.normal((len(sample), heads, 512), 4243)
-    qr = O.normal((len(sample), heads, 64), 4244)
-    offs = np.concatenate([[0], np.cumsum(sample)[:-1]]).astype(np.int64)
-    t0 = time.perf_counter()
-    O.decode_absorbed(ql, qr, rows, offs, sample, SCALE)
-    dt = time.perf_counter() - t0
-    full_time = dt * float(np.sum(lens)) / float(sample.sum())
-    return {"value": len(lens) / full_time, "unit": "tok/s", "cores": O.num_threads(), "kind": "port",
-            "sample": f"first {len(sample)} of {len(lens)} sequences ({int(sample.sum())} of {int(np.sum(lens))} "
-                      f"tokens, {heads} heads) in {dt:.1f} s; scaled by token count to the full batch; "
-                      f"absorbed-latent f32 C restatement (oracle/mla_oracle.c), OpenMP over (sequence, row block)"}
+    per, reps = timed(sample, threads, min_seconds)
+    full = per * total / float(sample.sum())
+    one = np.asarray(lens[:1], np.int32)
+    per1, reps1 = timed(one, 1, min_seconds / 4)
+    full1 = per1 * total / float(one.sum())
+    O.set_num_threads(threads)
+    return {"value": len(lens) / full, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"first {len(sample)} of {len(lens)} sequences ({int(sample.sum())} of {int(total)} tokens, "
+                      f"{heads} heads) x {reps} runs = {per * reps:.1f} s on {threads} threads; scaled by token "
+                      f"count to the full batch ({full * 1e3:.0f} ms per step); absorbed-latent f32 C restatement "
+                      f"(oracle/mla_oracle.c), OpenMP over (sequence, row block)",
+            "single_thread": {"value": len(lens) / full1, "unit": "tok/s", "cores": 1,
+                              "sample": f"sequence 0 ({int(one.sum())} tokens) x {reps1} runs = "
+                                        f"{per1 * reps1:.1f} s; {full1:.1f} s per full step"}}
+
+
+def copy_calibration(stream, n=256 << 20, reps=4):
+    """A plain streaming kernel of known traffic for scaling the rocprofv3
+    FETCH_SIZE / WRITE_SIZE counters: qmla_f32_to_bf16 over n elements reads
+    4n bytes and writes 2n bytes."""
+    src = qmla.DeviceBuffer(n * 4)
+    dst = qmla.DeviceBuffer(n * 2)
+    qmla.check(qmla.lib().qmla_fill_normal_f32(src.ptr, n, 5, 0.0, 1.0, qmla._sh(stream)))
+    for _ in range(reps):
+        qmla.check(qmla.lib().qmla_f32_to_bf16(src.ptr, dst.ptr, n, qmla._sh(stream)))
+    stream.sync()
+    log(f"copy calibration: {reps} x qmla_f32_to_bf16 over {n} elements "
+        f"({4 * n} bytes read, {2 * n} bytes written per launch)")
+
+
+def measured_traffic():
+    """HBM bytes per decode step from the committed rocprofv3 PMC summary
+    (counter reads scaled by the copy calibration), or None."""
+    path = os.path.join(ROOT, "profiles", "decode_v3_pmc.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_step:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-seqs", type=int, default=32)
+    ap.add_argument("--calibrate", action="store_true",
+                    help="only run the copy kernel used to scale the PMC byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the decode path shards by batch "
@@ -198,6 +255,9 @@ def main():
     dev, cus, arch = qmla.device_info()
     log(f"device {dev} {arch} with {cus} CUs")
     stream = qmla.Stream()
+    if args.calibrate:
+        copy_calibration(stream)
+        return
 
     lens = synth.v3_decode_lengths()
     log(f"v3 decode: batch {len(lens)}, {int(lens.sum())} tokens, {int(lens.sum()) * ROW_BYTES / 1e9:.3f} GB latent")
@@ -237,6 +297,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": main_res["ms_per_step"],
+        "wall_ms_per_step": main_res["wall_ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -257,8 +318,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": main_res["hbm_frac"],
-            "traffic": None,
-            "kernel": "decode step (plan + k_decode_mfma + merge), median of HIP events on the launch stream",
+            "traffic": measured_traffic(),
+            "kernel": "decode step = k_decode_mfma + k_decode_merge_frag (one qmla_decode_absorbed call), "
+                      "HIP events on the launch stream around the timed steps",
             "bytes_per_launch": main_res["bytes_per_step"],
         },
         "cpu_baseline": cpu,

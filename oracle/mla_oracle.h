@@ -184,6 +184,7 @@ void orc_mla_forward_with_latent(const orc_mla_layer *L, const float *xs, int b,
 
 /* OpenMP thread count used by the parallel loops above (for reporting).   */
 int orc_num_threads(void);
+void orc_set_num_threads(int n); /* OpenMP threads for later calls (n > 0) */
 
 #ifdef __cplusplus
 }

@@ -66,6 +66,7 @@ def lib():
             "orc_decode_absorbed_f64": (None, [_f32p, _f32p, _f32p, _i64p, _i32p, C.c_int, C.c_int, C.c_int,
                                                C.c_int, C.c_double, _f64p, C.c_void_p]),
             "orc_num_threads": (C.c_int, []),
+            "orc_set_num_threads": (None, [C.c_int]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -248,6 +249,10 @@ def decode_absorbed(q_lat, q_rope, cache, offsets, lens, scale: float, f64: bool
 
 def num_threads() -> int:
     return lib().orc_num_threads()
+
+
+def set_num_threads(n: int) -> None:
+    lib().orc_set_num_threads(int(n))
 
 
 # ----------------------------------------------------------- MLA layer ----
