@@ -2,140 +2,283 @@
 //
 // Replaces the tiled candle matmuls of fused_prefill_attn
 // (src/attention_kernel.rs:64-107) for bf16 inputs with f32 accumulation.
-// Per block: 4 waves x 64 query rows of one (b, h).  Per 32-key tile:
+// A block holds 4 waves x 64 query rows of one (b, h) and streams 32-key
+// tiles of [k_nope | k_rope] and v through an LDS ring.  Per wave and tile:
 //
-//   S^T[key][q] = sum_d K[key][d] Q[q][d]       d over [k_nope | k_rope]
-//   P^T = exp2(S^T * scale*log2(e) - m)          online softmax, f32
+//   S^T[key][q] = sum_d K[key][d] Q[q][d]      2 x KSTEPS MFMAs (Q in VGPRs)
+//   P^T = exp2(S^T * scale*log2(e) - m)         softmax, f32
 //   O^T[c][q] += sum_key V^T[c][key] P^T[key][q]
 //
-// As in the decode kernel, the S^T accumulator (lane = query row, 16 keys
-// per lane) is used directly as the B operand of the P.V product, and V^T
-// is read from the key-major tile with ds_read_b64_tr_b16.  Each wave
-// covers two 32-row column blocks so every K / V^T operand read feeds two
-// MFMAs.  Key tiles above a wave's causal horizon are skipped (exact: the
-// reference's -1e18 mask gives exp() == 0); blocks are issued heaviest
-// first so the causal triangle balances across compute units.
+// The S^T accumulator (lane = query row, 16 keys per lane) is the B operand
+// of the P.V product, and V^T comes from the key-major tile through
+// ds_read_b64_tr_b16.  The loop is software-pipelined: iteration it
+// computes S^T of tile it+1, then P.V of tile it with the softmax of tile
+// it+1 spread over its MFMAs.  The softmax keeps a lazy fixed reference per
+// row (the first tile's maximum; a block whose later scores exceed it by
+// more than kPSlack redoes its tiles with the true maximum), so the O^T
+// accumulators are never rescaled inside the loop.  Key tiles above a wave's
+// causal horizon are skipped (exact: the reference's -1e18 mask gives
+// exp() == 0); blocks are issued heaviest first so the causal triangle
+// balances across compute units.
 
 #include <cmath>
+#include <type_traits>
+#include <utility>
 
-#include "internal.hpp"
+#include "mfma_pipe.hpp"
 
 namespace qmla {
 
 namespace {
+
+using namespace pipe;
 
 constexpr int kPKeys = 32;      // keys per tile
 constexpr int kPWaves = 4;
 constexpr int kPRowsWave = 64;  // two 32-row MFMA column blocks
 constexpr int kPRows = kPWaves * kPRowsWave;
 constexpr int kPStages = 4;
+constexpr int kPAhead = 4;      // S^T operand reads issued ahead of their MFMAs
+constexpr int kPvAheadP = 3;    // V^T fragments issued ahead of their MFMAs
+constexpr float kPSlack = 16.f;
 
-typedef __attribute__((address_space(3))) void lds_void_p;
-typedef __attribute__((address_space(3))) char lds_char_p;
-typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_p;
-typedef __attribute__((address_space(3))) bf16x8_t lds_bf16x8_p;
+// One LDS region of a stage: 32 key rows of ROWB bytes, filled by 1 KB DMA
+// instructions (RPI rows each).  Chunk positions are XOR-swizzled by row so
+// that the operand reads are free of bank conflicts without padding:
+//  * K regions (S^T operand: 16 rows read the same 16-byte chunk): chunk c
+//    of row r sits at c ^ ((r / RB) & (CPR - 1)), RB = rows per 256-byte bank
+//    cycle -- rows sharing a bank window get distinct chunk positions.
+//  * V region (V^T operand: 4 consecutive rows x one 64-byte group per half
+//    wave): group g of row r sits at g ^ ((r / RB) & (GPR - 1)).
+// The DMA realises the swizzle on the source side: the lane writing LDS
+// position p of row r loads the chunk whose swizzled position is p.
+template <int ROWB>
+struct Region {
+  static_assert(ROWB == 0 || (ROWB >= 32 && ROWB <= 1024 && (ROWB & (ROWB - 1)) == 0), "row bytes");
+  static constexpr int CPR = ROWB / 16;
+  static constexpr int RPI = ROWB ? 1024 / ROWB : 1;
+  static constexpr int INSTR = 32 * ROWB / 1024;
+  static constexpr int BYTES = 32 * ROWB;
+  static constexpr int RB = ROWB >= 256 ? 1 : (ROWB ? 256 / ROWB : 1);
+  static constexpr int GPR = ROWB / 64;
+  static __device__ __forceinline__ int kpos(int r, int c) { return c ^ ((r / RB) & (CPR - 1)); }
+  static __device__ __forceinline__ int vgrp(int r, int g) {
+    return GPR > 1 ? (g ^ ((r / RB) & (GPR - 1))) : g;
+  }
+};
 
 template <int DN_, int DR_, int DV_>
 struct PrefillShape {
   static constexpr int DN = DN_, DR = DR_, DV = DV_;
   static constexpr int DQK = DN + DR;
-  static constexpr int KSTEPS = DQK / 16;
-  static constexpr int CB = DV / 32;
-  static constexpr int NCH = DN / 8;            // 16-byte chunks of k_nope
-  static constexpr int KCH = DQK / 8;           // 16-byte chunks of a K row
-  static constexpr int KRS = KCH + 1;           // padded K row stride (chunks)
-  static constexpr int VCH = DV / 8;
-  static constexpr int VRS = VCH + 1;           // padded V row stride (chunks)
-  static constexpr int KSLOTS = kPKeys * KRS;
-  static constexpr int VSLOTS = kPKeys * VRS;
-  static constexpr int INSTR = (KSLOTS + VSLOTS + 63) / 64;
-  static constexpr int STAGE_BYTES = INSTR * 64 * 16;
-  static constexpr int V_BASE = KSLOTS * 16;    // byte offset of the V tile in a stage
-  static_assert(DN % 8 == 0 && DR % 8 == 0 && DQK % 16 == 0 && DV % 32 == 0, "bad dims");
-  static_assert((INSTR + kPWaves - 1) / kPWaves * (kPStages - 1) < 64, "vmcnt overflow");
+  static constexpr int KSTEPS = DQK / 16;   // S^T k-steps
+  static constexpr int NSTEPS = DN / 16;    // ... of which over k_nope
+  static constexpr int CB = DV / 32;        // P.V column blocks
+  using KN = Region<DN * 2>;
+  using KR = Region<DR * 2>;
+  using VR = Region<DV * 2>;
+  static constexpr int KN_OFF = 0;
+  static constexpr int KR_OFF = KN::BYTES;
+  static constexpr int V_OFF = KN::BYTES + KR::BYTES;
+  static constexpr int STAGE_BYTES = KN::BYTES + KR::BYTES + VR::BYTES;
+  static constexpr int INSTR = KN::INSTR + KR::INSTR + VR::INSTR;
+  static constexpr int MI = (INSTR + kPWaves - 1) / kPWaves;  // DMA slots per wave
+  static constexpr bool EVEN = KN::INSTR % kPWaves == 0 && KR::INSTR % kPWaves == 0 &&
+                               VR::INSTR % kPWaves == 0;
+  static_assert(DN % 16 == 0 && DR % 16 == 0 && DV % 32 == 0 && DN >= 16 && DV >= 32, "dims");
+  static_assert(MI * (kPStages - 1) < 64, "vmcnt range");
 };
 
-template <int N>
-__device__ __forceinline__ void pwait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt out of range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+// Uniform parts of one tile's DMA: base pointers of the three source rows
+// (key0 of the tile), the LDS stage, and the last valid key (tile-relative).
+struct PTileDma {
+  const uint8_t *kn, *kr, *v;
+  uint32_t stage;
+  int last;
+};
+
+// Per-lane part of region instruction i: source offset of the chunk that
+// lands at this lane's LDS position (swizzle inverted), clamped rows.
+template <class RG, bool VSWZ>
+__device__ __forceinline__ uint32_t region_src(int i, int lane, int last) {
+  const int r = i * RG::RPI + lane / RG::CPR;
+  const int p = lane % RG::CPR;
+  const int j = VSWZ ? ((RG::vgrp(r, p >> 2) << 2) | (p & 3)) : RG::kpos(r, p);
+  return (uint32_t)(min(r, last) * (RG::CPR * 16) + j * 16);
 }
 
-__device__ __forceinline__ void pwait_vmcnt_dyn(int n) {
-  switch (n) {
-#define QMLA_W(k) case k: pwait_vmcnt<k>(); break;
-    QMLA_W(0) QMLA_W(1) QMLA_W(2) QMLA_W(3) QMLA_W(4) QMLA_W(5) QMLA_W(6) QMLA_W(7)
-    QMLA_W(8) QMLA_W(9) QMLA_W(10) QMLA_W(11) QMLA_W(12) QMLA_W(13) QMLA_W(14) QMLA_W(15)
-    QMLA_W(16) QMLA_W(17) QMLA_W(18) QMLA_W(19) QMLA_W(20) QMLA_W(21) QMLA_W(22) QMLA_W(23)
-    QMLA_W(24) QMLA_W(25) QMLA_W(26) QMLA_W(27) QMLA_W(28) QMLA_W(29) QMLA_W(30) QMLA_W(31)
-    QMLA_W(32) QMLA_W(33) QMLA_W(34) QMLA_W(35) QMLA_W(36) QMLA_W(37) QMLA_W(38) QMLA_W(39)
-#undef QMLA_W
-    default: pwait_vmcnt<0>(); break;
+// DMA slot k of this wave: instruction k * kPWaves + wave of the tile.
+template <class SH>
+__device__ __forceinline__ void pissue_one(const PTileDma &d, int k, int wave, int lane) {
+  const int ins0 = k * kPWaves, ins = ins0 + wave;
+  if (!SH::EVEN && ins >= SH::INSTR) return;
+  constexpr int E1 = SH::KN::INSTR, E2 = SH::KN::INSTR + SH::KR::INSTR;
+  const uint32_t st = fresh(d.stage);
+  if (SH::EVEN ? ins0 < E1 : ins < E1) {
+    dma16(fresh(d.kn), region_src<typename SH::KN, false>(ins, lane, d.last),
+          st + SH::KN_OFF + ins * 1024);
+  } else if (SH::EVEN ? ins0 < E2 : ins < E2) {
+    if constexpr (SH::KR::INSTR > 0)
+      dma16(fresh(d.kr), region_src<typename SH::KR, false>(ins - E1, lane, d.last),
+            st + SH::KR_OFF + (ins - E1) * 1024);
+  } else {
+    dma16(fresh(d.v), region_src<typename SH::VR, true>(ins - E2, lane, d.last),
+          st + SH::V_OFF + (ins - E2) * 1024);
   }
 }
 
-// o *= alpha on an MFMA accumulator kept in AGPRs (see decode_mfma.hip).
-__device__ __forceinline__ void pagpr_scale16(floatx16_t &o, float alpha) {
-  float e[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) e[i] = o[i];
-  float tmp;
-#define QMLA_S1(i) "v_accvgpr_read_b32 %16, %" #i "\n v_mul_f32 %16, %16, %17\n v_accvgpr_write_b32 %" #i ", %16\n"
-  asm volatile(QMLA_S1(0) QMLA_S1(1) QMLA_S1(2) QMLA_S1(3) QMLA_S1(4) QMLA_S1(5) QMLA_S1(6)
-                   QMLA_S1(7) QMLA_S1(8) QMLA_S1(9) QMLA_S1(10) QMLA_S1(11) QMLA_S1(12)
-                       QMLA_S1(13) QMLA_S1(14) QMLA_S1(15)
-               : "+a"(e[0]), "+a"(e[1]), "+a"(e[2]), "+a"(e[3]), "+a"(e[4]), "+a"(e[5]),
-                 "+a"(e[6]), "+a"(e[7]), "+a"(e[8]), "+a"(e[9]), "+a"(e[10]), "+a"(e[11]),
-                 "+a"(e[12]), "+a"(e[13]), "+a"(e[14]), "+a"(e[15]), "=&v"(tmp)
-               : "v"(alpha));
-#undef QMLA_S1
-#pragma unroll
-  for (int i = 0; i < 16; ++i) o[i] = e[i];
-}
-
-__device__ __forceinline__ uint32_t ppack2_bf16(float a, float b) {
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  bf16x2_t v;
-  v[0] = (__bf16)a;  // v_cvt_pk_bf16_f32, round to nearest even
-  v[1] = (__bf16)b;
-  return __builtin_bit_cast(uint32_t, v);
-}
-
-// One stage = K tile (32 keys x [k_nope | k_rope], padded rows) followed by
-// the V tile (32 keys x dv, padded rows).  Slot s of the stage is written by
-// DMA instruction s / 64, lane s % 64.  Keys past seq_k and pad slots
-// re-load a valid chunk that is never read back.
 template <class SH>
-__device__ __forceinline__ void pissue_tile(const uint8_t *__restrict__ kb,
-                                            const uint8_t *__restrict__ krb,
-                                            const uint8_t *__restrict__ vb, int key0, int seq_k,
-                                            lds_char_p *stage, int wave, int lane) {
-  for (int ins = wave; ins < SH::INSTR; ins += kPWaves) {
-    const int s = ins * 64 + lane;
-    const uint8_t *src;
-    if (s < SH::KSLOTS) {
-      const int t = s / SH::KRS, c = s - t * SH::KRS;
-      int key = key0 + t;
-      key = key < seq_k ? key : seq_k - 1;
-      if (c < SH::NCH)
-        src = kb + (int64_t)key * (SH::DN * 2) + c * 16;
-      else if (c < SH::KCH)
-        src = krb + (int64_t)key * (SH::DR * 2) + (c - SH::NCH) * 16;
-      else
-        src = kb + (int64_t)key * (SH::DN * 2);
-    } else {
-      const int sv = s - SH::KSLOTS;
-      int t = sv / SH::VRS, c = sv - t * SH::VRS;
-      if (t >= kPKeys || c >= SH::VCH) {
-        t = 0;
-        c = 0;
+__device__ __forceinline__ void pissue_tile(const PTileDma &d, int wave, int lane) {
+#pragma unroll
+  for (int k = 0; k < SH::MI; ++k) pissue_one<SH>(d, k, wave, lane);
+}
+
+// Waits until at most k tiles of this wave's DMA are outstanding.
+template <class SH>
+__device__ __forceinline__ void pwait_tiles(int k, int my_instr) {
+  if constexpr (SH::EVEN) {
+    if (k <= 0)
+      wait_vmcnt<0>();
+    else if (k == 1)
+      wait_vmcnt<SH::MI>();
+    else
+      wait_vmcnt<(2 * SH::MI < 63 ? 2 * SH::MI : 63)>();
+  } else {
+    wait_vmcnt_dyn(k * my_instr);
+  }
+}
+
+// Per-lane LDS byte offsets (relative to a stage) of the MFMA operands.
+template <class SH>
+struct PLane {
+  uint32_t s[SH::KSTEPS];  // S^T operand of k-step kk (row n, 8 dims at 8*half)
+  uint32_t v[SH::CB];      // V^T operand of column block cb (k-step / hi via immediates)
+};
+
+template <class SH>
+__device__ __forceinline__ PLane<SH> plane_offsets(int lane) {
+  PLane<SH> la;
+  const int n = lane & 31, half = lane >> 5;
+#pragma unroll
+  for (int kk = 0; kk < SH::KSTEPS; ++kk) {
+    if (kk < SH::NSTEPS)
+      la.s[kk] = SH::KN_OFF + n * (SH::DN * 2) + SH::KN::kpos(n, 2 * kk + half) * 16;
+    else
+      la.s[kk] = SH::KR_OFF + n * (SH::DR * 2) + SH::KR::kpos(n, 2 * (kk - SH::NSTEPS) + half) * 16;
+  }
+  const int g = lane >> 4, sl = lane & 15;
+  const int tok_a = (g >= 2 ? 4 : 0) + (sl >> 2);
+  const int col_in = (g & 1) * 16 + 4 * (sl & 3);  // element within a 32-column block
+#pragma unroll
+  for (int cb = 0; cb < SH::CB; ++cb)
+    la.v[cb] = SH::V_OFF + tok_a * (SH::DV * 2) + SH::VR::vgrp(tok_a, cb) * 64 + col_in * 2;
+  return la;
+}
+
+// S^T of one tile for both column blocks: 2 x KSTEPS MFMAs into VGPR
+// accumulators, operand reads kPAhead steps ahead; with DMA, this wave's
+// slots for the tile in `d` are spread over the MFMAs.
+template <class SH, bool DMA>
+__device__ __forceinline__ void ps_phase(const PLane<SH> &la, uint32_t st,
+                                         const bf16x8_t (&qf)[2][SH::KSTEPS], floatx16_t (&s)[2],
+                                         const PTileDma &d, int wave, int lane) {
+  constexpr int D = kPAhead < SH::KSTEPS ? kPAhead : SH::KSTEPS;
+  bf16x8_t a[D + 1];
+  [&]<int... K>(std::integer_sequence<int, K...>) {
+    ([&] { if constexpr (K < D) a[K] = ds_b128<0>(st + la.s[K]); }(), ...);
+    ([&] {
+      constexpr int kk = K;
+      constexpr int after = (kk + D - 1 < SH::KSTEPS - 1 ? D - 1 : SH::KSTEPS - 1 - kk);
+      wait_lgkm<after>();
+      arrived(a[kk % (D + 1)]);
+      if constexpr (kk == 0) {
+        s[0] = mfma_s_first(a[0], qf[0][0]);
+        s[1] = mfma_s_first(a[0], qf[1][0]);
+      } else {
+        mfma_s_acc(s[0], a[kk % (D + 1)], qf[0][kk]);
+        mfma_s_acc(s[1], a[kk % (D + 1)], qf[1][kk]);
       }
-      int key = key0 + t;
-      key = key < seq_k ? key : seq_k - 1;
-      src = vb + (int64_t)key * (SH::DV * 2) + c * 16;
-    }
-    __builtin_amdgcn_global_load_lds((const void *)src, (lds_void_p *)(stage + ins * 1024), 16, 0,
-                                     0);
+      if constexpr (DMA) {
+#pragma unroll
+        for (int k = 0; k < SH::MI; ++k)
+          if ((k * SH::KSTEPS) / SH::MI == kk) pissue_one<SH>(d, k, wave, lane);
+      }
+      if constexpr (kk + D < SH::KSTEPS) a[(kk + D) % (D + 1)] = ds_b128<0>(st + la.s[kk + D]);
+    }(), ...);
+  }(std::make_integer_sequence<int, SH::KSTEPS>{});
+  mfma_s_drain(s[0]);
+  mfma_s_drain(s[1]);
+}
+
+// V^T fragment j = (k-step ks, column block i): two transposing reads.
+template <class SH, int J>
+__device__ __forceinline__ bf16x8_t pv_frag(const PLane<SH> &la, uint32_t st) {
+  constexpr int ks = J / SH::CB, cb = J % SH::CB;
+  return ds_tr2<ks * 16 * (SH::DV * 2), 8 * (SH::DV * 2)>(st + la.v[cb]);
+}
+
+// O^T += V^T P^T for both column blocks: 2 x 2 x CB MFMAs into the AGPR
+// accumulators, V^T fragments streamed kPvAheadP ahead.
+template <class SH>
+__device__ __forceinline__ void ppv_phase(const PLane<SH> &la, uint32_t st,
+                                          const bf16x8_t (&pb)[2][2], floatx16_t (&o)[2][SH::CB]) {
+  constexpr int NA = 2 * SH::CB;
+  constexpr int DA = kPvAheadP < NA ? kPvAheadP : NA;
+  bf16x8_t a[DA + 1];
+  [&]<int... J>(std::integer_sequence<int, J...>) {
+    ([&] { if constexpr (J < DA) a[J] = pv_frag<SH, J>(la, st); }(), ...);
+    ([&] {
+      constexpr int j = J;
+      constexpr int after = 2 * (j + DA - 1 < NA - 1 ? DA - 1 : NA - 1 - j);
+      wait_lgkm<after>();
+      arrived(a[j % (DA + 1)]);
+      constexpr int ks = j / SH::CB, cb = j % SH::CB;
+      o[0][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[j % (DA + 1)], pb[0][ks], o[0][cb], 0, 0, 0);
+      o[1][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[j % (DA + 1)], pb[1][ks], o[1][cb], 0, 0, 0);
+      if constexpr (j + DA < NA) a[(j + DA) % (DA + 1)] = pv_frag<SH, j + DA>(la, st);
+    }(), ...);
+  }(std::make_integer_sequence<int, NA>{});
+}
+
+// Key (within the tile) of S^T accumulator element j of this lane.
+__device__ __forceinline__ int ptile_key(int j, int half) {
+  return 8 * (j >> 2) + 4 * half + (j & 3);
+}
+
+// Raw maximum of this lane's 16 scores of column block nb; with MASK, keys
+// at or past seq_k or (causal) after the row's absolute position are out.
+template <bool MASK>
+__device__ __forceinline__ float ptile_max(const floatx16_t &s, int key0, int half, int vis_lim) {
+  float x[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) x[j] = (!MASK || key0 + ptile_key(j, half) < vis_lim) ? s[j] : -INFINITY;
+  const float a = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+  const float b = fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7]));
+  const float c = fmaxf(fmaxf(x[8], x[9]), fmaxf(x[10], x[11]));
+  const float e = fmaxf(fmaxf(x[12], x[13]), fmaxf(x[14], x[15]));
+  return fmaxf(fmaxf(a, b), fmaxf(c, e));
+}
+
+// p = exp2(s * sl2 - m) as the two bf16 B-operand fragments; adds to l.
+template <bool MASK>
+__device__ __forceinline__ void ptile_p(const floatx16_t &s, float sl2, float m, int key0,
+                                        int half, int vis_lim, float &l, bf16x8_t (&pb)[2]) {
+  float p[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j], sl2, -m));
+    if (MASK) p[j] = key0 + ptile_key(j, half) < vis_lim ? p[j] : 0.f;
+  }
+  float q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[i] = p[2 * i] + p[2 * i + 1];
+  l += ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    u32x4_t pk;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pk[i] = pack2_bf16(p[ks * 8 + 2 * i], p[ks * 8 + 2 * i + 1]);
+    pb[ks] = __builtin_bit_cast(bf16x8_t, pk);
   }
 }
 
@@ -155,12 +298,18 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
     const uint16_t *__restrict__ v, qmla_prefill_dims d, float scale_log2, int causal,
     uint16_t *__restrict__ out, int n_qtiles) {
   using SH = PrefillShape<DN, DR, DV>;
-  constexpr int VROW = SH::VRS * 16;
   extern __shared__ __attribute__((aligned(16))) char pring_raw[];
-  lds_char_p *ring = (lds_char_p *)pring_raw;
+  lds_char *ring = (lds_char *)pring_raw;
+  const uint32_t ring_u = lds_u32(ring);
+  const uint32_t ovf_flags = ring_u + kPStages * SH::STAGE_BYTES;  // kPWaves words
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   const int n = lane & 31, half = lane >> 5;
+  // A negative scale is applied as |scale| with the sign folded into q
+  // (exact in bf16), so the raw score maximum is also the scaled one.
+  const uint32_t q_sign = scale_log2 < 0.f ? 0x80008000u : 0u;
+  const float sl2 = fabsf(scale_log2);
 
   const int BH = d.batch * d.heads;
   const int L = blockIdx.x;
@@ -179,32 +328,20 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
 
   // Q fragments (B operand of S^T) for the wave's two 32-row column blocks.
   bf16x8_t qf[2][SH::KSTEPS];
-  bool rok[2];
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
     const int row = wrow0 + nb * 32 + n;
-    rok[nb] = row < d.seq_q;
-    const int64_t qrow = bhq + (rok[nb] ? row : d.seq_q - 1);
-    const uint32_t keep = rok[nb] ? 0xffffffffu : 0u;
+    const bool ok = row < d.seq_q;
+    const int64_t qrow = bhq + (ok ? row : d.seq_q - 1);
+    const uint32_t keep = ok ? 0xffffffffu : 0u;
 #pragma unroll
     for (int kk = 0; kk < SH::KSTEPS; ++kk) {
       u32x4_t u = __builtin_bit_cast(u32x4_t, load_q_frag<SH>(q_nope, q_rope, qrow, kk * 16 + half * 8));
-      u[0] &= keep;
-      u[1] &= keep;
-      u[2] &= keep;
-      u[3] &= keep;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) u[i] = (u[i] ^ q_sign) & keep;
       qf[nb][kk] = __builtin_bit_cast(bf16x8_t, u);
     }
   }
-
-  floatx16_t o[2][SH::CB];
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-    for (int cb = 0; cb < SH::CB; ++cb)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) o[nb][cb][j] = 0.f;
-  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
 
   // key horizon (exclusive) of the block and of this wave
   int kend_blk = d.seq_k, kend_w = d.seq_k;
@@ -213,133 +350,159 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
     kend_w = min(d.seq_k, d.q_offset + min(wrow0 + kPRowsWave, d.seq_q));
   }
   if (wrow0 >= d.seq_q) kend_w = 0;  // no query row in this wave
-  const int ntiles = (kend_blk + kPKeys - 1) / kPKeys;
+  const int ntb = (kend_blk + kPKeys - 1) / kPKeys;  // tiles of the block
+  const int ntw = (kend_w + kPKeys - 1) / kPKeys;    // tiles of this wave
   const int my_instr = (SH::INSTR - wave + kPWaves - 1) / kPWaves;
-
-  const int a_off = (n * SH::KRS + half) * 16;
-  const int g = lane >> 4, sl = lane & 15;
-  const int tok_a = (g >= 2 ? 4 : 0) + (sl >> 2);
-  const int col_in = (g & 1) * 16 + 4 * (sl & 3);
-  const int v_off = SH::V_BASE + tok_a * VROW + (col_in >> 3) * 16 + (col_in & 7) * 2;
-  const int row_abs0 = d.q_offset + wrow0 + n;  // absolute row of column block 0
-
+  const PLane<SH> la = plane_offsets<SH>(lane);
+  // a tile needs the mask if one of its keys is invisible to some row of
+  // the wave: past seq_k, or (causal) after the wave's first row
+  const int mask_from = causal ? min(d.seq_k, d.q_offset + wrow0 + 1) : d.seq_k;
+  int vis_lim[2];
 #pragma unroll
-  for (int p = 0; p < kPStages - 1; ++p)
-    if (p < ntiles)
-      pissue_tile<SH>(kb, krb, vb, p * kPKeys, d.seq_k, ring + p * SH::STAGE_BYTES, wave, lane);
+  for (int nb = 0; nb < 2; ++nb)
+    vis_lim[nb] = causal ? min(d.seq_k, d.q_offset + wrow0 + nb * 32 + n + 1) : d.seq_k;
+  auto tile_dma = [&](int t) {
+    const int key0 = t * kPKeys;
+    return PTileDma{kb + (int64_t)key0 * (DN * 2), krb + (int64_t)key0 * (DR * 2),
+                    vb + (int64_t)key0 * (DV * 2), ring_u + (t % kPStages) * SH::STAGE_BYTES,
+                    d.seq_k - 1 - key0};
+  };
+  auto stage_u = [&](int t) { return ring_u + (uint32_t)((t % kPStages) * SH::STAGE_BYTES); };
 
-  for (int it = 0; it < ntiles; ++it) {
-    const int nxt = it + kPStages - 1;
-    if (nxt < ntiles)
-      pissue_tile<SH>(kb, krb, vb, nxt * kPKeys, d.seq_k,
-                      ring + (nxt % kPStages) * SH::STAGE_BYTES, wave, lane);
-    const int ahead = (nxt < ntiles ? nxt : ntiles - 1) - it;
-    pwait_vmcnt_dyn(ahead * my_instr);
+  floatx16_t o[2][SH::CB];
+  floatx16_t s[2];
+  bf16x8_t pb[2][2], pn[2][2];
+  float m_ref[2], l_run[2], m_raw[2];
+  float m_init[2] = {-INFINITY, -INFINITY};
+  for (;;) {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+      for (int cb = 0; cb < SH::CB; ++cb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) o[nb][cb][j] = 0.f;
+      l_run[nb] = 0.f;
+      m_raw[nb] = -INFINITY;
+      m_ref[nb] = m_init[nb];
+    }
+    if (lane == 0) ds_w32(ovf_flags + 4 * wave, 0u);
+
+    // prologue: kPStages-1 tiles in flight, then S and softmax of tile 0
+#pragma unroll
+    for (int p = 0; p < kPStages - 1; ++p)
+      if (p < ntb) pissue_tile<SH>(tile_dma(p), wave, lane);
+    pwait_tiles<SH>(min(kPStages - 2, ntb - 1), my_instr);
+    wait_lgkm<0>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-
-    const int key0 = it * kPKeys;
-    if (key0 < kend_w) {  // wave-uniform: tile not above this wave's horizon
-      const lds_char_p *stage = ring + (it % kPStages) * SH::STAGE_BYTES;
-      const lds_char_p *pa = stage + a_off;
-      const lds_char_p *pv = stage + v_off;
-      floatx16_t s[2];
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) s[nb][j] = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < SH::KSTEPS; ++kk) {
-        const bf16x8_t a = *reinterpret_cast<const lds_bf16x8_p *>(pa + kk * 32);
-        s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[0][kk], s[0], 0, 0, 0);
-        s[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[1][kk], s[1], 0, 0, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-#pragma unroll
-      for (int kk = 0; kk < SH::KSTEPS - 2; ++kk) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-      __builtin_amdgcn_sched_barrier(0);
-
-      u32x4_t pk[2][2];
+    if (ntw > 0) {
+      ps_phase<SH, false>(la, stage_u(0), qf, s, PTileDma{}, wave, lane);
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
-        const int row_abs = row_abs0 + nb * 32;
-        float mt = -INFINITY;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int key = key0 + 8 * (j >> 2) + 4 * half + (j & 3);
-          const bool vis = key < d.seq_k && (!causal || key <= row_abs);
-          const float x = vis ? s[nb][j] * scale_log2 : -INFINITY;
-          s[nb][j] = x;
-          mt = fmaxf(mt, x);
-        }
-        mt = xor32_max(mt);
-        // Lazy rescale (threshold 8 in log2 units, p <= 256).  Key 0 is
-        // visible to every row, so the first tile makes m_run finite.
-        if (m_run[nb] == -INFINITY || mt > m_run[nb] + 8.f) {
-          const float m_new = fmaxf(mt, m_run[nb]);
-          const float alpha = m_run[nb] == -INFINITY ? 0.f : exp2f(m_run[nb] - m_new);
-          m_run[nb] = m_new;
-          l_run[nb] *= alpha;
-#pragma unroll
-          for (int cb = 0; cb < SH::CB; ++cb) pagpr_scale16(o[nb][cb], alpha);
-        }
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float p0 = exp2f(s[nb][ks * 8 + 2 * i] - m_run[nb]);
-            const float p1 = exp2f(s[nb][ks * 8 + 2 * i + 1] - m_run[nb]);
-            l_run[nb] += p0 + p1;
-            pk[nb][ks][i] = ppack2_bf16(p0, p1);
-          }
+        m_raw[nb] = ptile_max<true>(s[nb], 0, half, vis_lim[nb]);
+        // key 0 is visible to every row: the first tile's maximum is finite
+        if (m_ref[nb] == -INFINITY) m_ref[nb] = xor32_max(m_raw[nb]) * sl2;
+        ptile_p<true>(s[nb], sl2, m_ref[nb], 0, half, vis_lim[nb], l_run[nb], pb[nb]);
       }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const bf16x8_t pb0 = __builtin_bit_cast(bf16x8_t, pk[0][ks]);
-        const bf16x8_t pb1 = __builtin_bit_cast(bf16x8_t, pk[1][ks]);
-#pragma unroll
-        for (int cb = 0; cb < SH::CB; ++cb) {
-          const lds_char_p *p1 = pv + ks * 16 * VROW + cb * 64;
-          const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_p *)p1);
-          const bf16x4_t hi =
-              __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_p *)(p1 + 8 * VROW));
-          const bf16x8_t a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-          o[0][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb0, o[0][cb], 0, 0, 0);
-          o[1][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb1, o[1][cb], 0, 0, 0);
-        }
-      }
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-      for (int i = 0; i < 2 * SH::CB - 2; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
+    __builtin_amdgcn_sched_barrier(0);
+
+    // Iteration it: S^T of tile it+1, then P.V of tile it with the softmax
+    // of tile it+1 spread over its MFMAs.  MODE 0: unmasked tile it+1 with
+    // its DMA slots spread over S^T; MODE 1: masked tile it+1, DMA up
+    // front; MODE 2: this wave is past its horizon for tile it+1 (P.V of
+    // tile it only, or nothing).
+    auto step = [&](auto mode_c, int it) __attribute__((always_inline)) {
+      constexpr int MODE = decltype(mode_c)::value;
+      const int nxt = it + kPStages - 1;
+      pwait_tiles<SH>(min(kPStages - 3, ntb - 2 - it), my_instr);
+      // every wave is past iteration it-1 (stage (it-1) % kPStages is free)
+      // and tile it+1 is visible to every wave
+      wait_lgkm<0>();
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (MODE == 0) {
+        ps_phase<SH, true>(la, stage_u(it + 1), qf, s, tile_dma(nxt), wave, lane);
+      } else {
+        if (nxt < ntb) pissue_tile<SH>(tile_dma(nxt), wave, lane);
+        if constexpr (MODE == 1) ps_phase<SH, false>(la, stage_u(it + 1), qf, s, PTileDma{}, wave, lane);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (MODE == 2) {
+        if (it < ntw) ppv_phase<SH>(la, stage_u(it), pb, o);
+      } else {
+        const int key0 = (it + 1) * kPKeys;
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+          m_raw[nb] = fmaxf(m_raw[nb], ptile_max<MODE == 1>(s[nb], key0, half, vis_lim[nb]));
+        ppv_phase<SH>(la, stage_u(it), pb, o);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+          ptile_p<MODE == 1>(s[nb], sl2, m_ref[nb], key0, half, vis_lim[nb], l_run[nb], pn[nb]);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          pb[nb][0] = pn[nb][0];
+          pb[nb][1] = pn[nb][1];
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int it = 0; it + 1 < ntb; ++it) {
+      const int key1 = (it + 1) * kPKeys;
+      if (it + 1 >= ntw)
+        step(std::integral_constant<int, 2>{}, it);
+      else if (key1 + kPKeys > mask_from || it + kPStages - 1 >= ntb)
+        step(std::integral_constant<int, 1>{}, it);
+      else
+        step(std::integral_constant<int, 0>{}, it);
+    }
+    // P.V of the last tile
+    if (ntb - 1 < ntw) {
+      wait_lgkm<0>();
+      ppv_phase<SH>(la, stage_u(ntb - 1), pb, o);
+    }
+
+    // Overflow check: each row's scaled maximum against its reference.
+    bool ovf = false;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) ovf |= xor32_max(m_raw[nb]) * sl2 > m_ref[nb] + kPSlack;
+    if (__ballot(ovf) != 0 && lane == 0) ds_w32(ovf_flags + 4 * wave, 1u);
+    wait_lgkm<0>();
     __builtin_amdgcn_s_barrier();
+    uint32_t f[kPWaves];
+#pragma unroll
+    for (int w = 0; w < kPWaves; ++w) f[w] = ds_r32(ovf_flags + 4 * w);
+    wait_lgkm<0>();
+    uint32_t any = 0;
+#pragma unroll
+    for (int w = 0; w < kPWaves; ++w) {
+      arrived32(f[w]);
+      any |= f[w];
+    }
+    if (__builtin_amdgcn_readfirstlane(any) == 0) break;
+    // Rare: redo the block's tiles with every row's true maximum.
+    __builtin_amdgcn_s_barrier();  // all waves have read the flags
+    m_init[0] = xor32_max(m_raw[0]) * sl2;
+    m_init[1] = xor32_max(m_raw[1]) * sl2;
   }
+  // the final P.V MFMAs complete before their accumulators are read
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 
   // finalise
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
     const float l = xor32_sum(l_run[nb]);
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    if (!rok[nb]) continue;
-    uint16_t *dst = out + (bhq + wrow0 + nb * 32 + n) * DV;
+    const int row = wrow0 + nb * 32 + n;
+    if (row >= d.seq_q) continue;
+    uint16_t *dst = out + (bhq + row) * DV;
 #pragma unroll
     for (int cb = 0; cb < SH::CB; ++cb)
 #pragma unroll
       for (int jq = 0; jq < 4; ++jq) {
         u32x2_t w;
-        w[0] = ppack2_bf16(o[nb][cb][jq * 4 + 0] * inv, o[nb][cb][jq * 4 + 1] * inv);
-        w[1] = ppack2_bf16(o[nb][cb][jq * 4 + 2] * inv, o[nb][cb][jq * 4 + 3] * inv);
+        w[0] = pack2_bf16(o[nb][cb][jq * 4 + 0] * inv, o[nb][cb][jq * 4 + 1] * inv);
+        w[1] = pack2_bf16(o[nb][cb][jq * 4 + 2] * inv, o[nb][cb][jq * 4 + 3] * inv);
         *reinterpret_cast<u32x2_t *>(dst + cb * 32 + 8 * jq + 4 * half) = w;
       }
   }
@@ -354,7 +517,7 @@ qmla_status launch_prefill_shape(const qmla_prefill_dims &d, const uint16_t *q_n
   const int n_qtiles = (d.seq_q + kPRows - 1) / kPRows;
   const int64_t nblocks = (int64_t)d.batch * d.heads * n_qtiles;
   QMLA_REQUIRE(nblocks <= 0x7fffffff, QMLA_ERR_SHAPE, "too many query tiles");
-  const size_t lds = (size_t)kPStages * SH::STAGE_BYTES;
+  const size_t lds = (size_t)kPStages * SH::STAGE_BYTES + kPWaves * 4;
   auto kern = k_prefill_mfma<DN, DR, DV>;
   QMLA_TRY(ensure_dynamic_lds((const void *)kern, lds));
   kern<<<dim3((unsigned)nblocks), dim3(kPWaves * 64), lds, stream>>>(
