@@ -2,24 +2,30 @@
 //
 // Replaces the tiled candle matmuls of fused_prefill_attn
 // (src/attention_kernel.rs:64-107) for bf16 inputs with f32 accumulation.
-// A block holds 4 waves x 64 query rows of one (b, h) and streams 32-key
+// A block holds 8 waves x 32 query rows of one (b, h) and streams 32-key
 // tiles of [k_nope | k_rope] and v through an LDS ring.  Per wave and tile:
 //
-//   S^T[key][q] = sum_d K[key][d] Q[q][d]      2 x KSTEPS MFMAs (Q in VGPRs)
+//   S^T[key][q] = sum_d K[key][d] Q[q][d]      KSTEPS MFMAs (Q in VGPRs)
 //   P^T = exp2(S^T * scale*log2(e) - m)         softmax, f32
 //   O^T[c][q] += sum_key V^T[c][key] P^T[key][q]
 //
 // The S^T accumulator (lane = query row, 16 keys per lane) is the B operand
 // of the P.V product, and V^T comes from the key-major tile through
-// ds_read_b64_tr_b16.  The loop is software-pipelined: iteration it
-// computes S^T of tile it+1, then P.V of tile it with the softmax of tile
-// it+1 spread over its MFMAs.  The softmax keeps a lazy fixed reference per
-// row (the first tile's maximum; a block whose later scores exceed it by
-// more than kPSlack redoes its tiles with the true maximum), so the O^T
-// accumulators are never rescaled inside the loop.  Key tiles above a wave's
-// causal horizon are skipped (exact: the reference's -1e18 mask gives
-// exp() == 0); blocks are issued heaviest first so the causal triangle
-// balances across compute units.
+// ds_read_b64_tr_b16.  Each wave fits in half a SIMD's register file, so
+// two waves share a SIMD: waves 0-3 (group 0) and 4-7 (group 1), one of
+// each per SIMD.  The block advances in barrier-separated steps; in every
+// step one group computes S^T of a tile (MFMA and LDS bound) while the
+// other computes the softmax of its previous S^T (VALU) and then the P.V
+// of the tile before (MFMA), so one wave's softmax runs under the other
+// wave's MFMAs.  Group 1 runs one step behind group 0.
+//
+// The softmax keeps a lazy fixed reference per row (the first tile's
+// maximum; a block whose later scores exceed it by more than kPSlack redoes
+// its tiles with the true maximum), so the O^T accumulators are never
+// rescaled inside the loop.  Key tiles above a wave's causal horizon are
+// skipped (exact: the reference's -1e18 mask gives exp() == 0); blocks are
+// issued heaviest first so the causal triangle balances across compute
+// units.
 
 #include <cmath>
 #include <type_traits>
@@ -34,10 +40,10 @@ namespace {
 using namespace pipe;
 
 constexpr int kPKeys = 32;      // keys per tile
-constexpr int kPWaves = 4;
-constexpr int kPRowsWave = 64;  // two 32-row MFMA column blocks
-constexpr int kPRows = kPWaves * kPRowsWave;
-constexpr int kPStages = 4;
+constexpr int kPWaves = 8;      // two groups of four
+constexpr int kPDmaWaves = 4;   // group 1 issues every tile's DMA
+constexpr int kPRows = kPWaves * 32;
+constexpr int kPStages = 4;     // tile ring depth
 constexpr int kPAhead = 4;      // S^T operand reads issued ahead of their MFMAs
 constexpr int kPvAheadP = 3;    // V^T fragments issued ahead of their MFMAs
 constexpr float kPSlack = 16.f;
@@ -52,9 +58,10 @@ constexpr float kPSlack = 16.f;
 //    wave): group g of row r sits at g ^ ((r / RB) & (GPR - 1)).
 // The DMA realises the swizzle on the source side: the lane writing LDS
 // position p of row r loads the chunk whose swizzled position is p.
-template <int ROWB>
+template <int ROWB_>
 struct Region {
-  static_assert(ROWB == 0 || (ROWB >= 32 && ROWB <= 1024 && (ROWB & (ROWB - 1)) == 0), "row bytes");
+  static_assert(ROWB_ == 0 || (ROWB_ >= 32 && ROWB_ <= 1024 && (ROWB_ & (ROWB_ - 1)) == 0), "row bytes");
+  static constexpr int ROWB = ROWB_;
   static constexpr int CPR = ROWB / 16;
   static constexpr int RPI = ROWB ? 1024 / ROWB : 1;
   static constexpr int INSTR = 32 * ROWB / 1024;
@@ -82,11 +89,10 @@ struct PrefillShape {
   static constexpr int V_OFF = KN::BYTES + KR::BYTES;
   static constexpr int STAGE_BYTES = KN::BYTES + KR::BYTES + VR::BYTES;
   static constexpr int INSTR = KN::INSTR + KR::INSTR + VR::INSTR;
-  static constexpr int MI = (INSTR + kPWaves - 1) / kPWaves;  // DMA slots per wave
-  static constexpr bool EVEN = KN::INSTR % kPWaves == 0 && KR::INSTR % kPWaves == 0 &&
-                               VR::INSTR % kPWaves == 0;
+  static constexpr int MI = (INSTR + kPDmaWaves - 1) / kPDmaWaves;  // DMA slots per wave
   static_assert(DN % 16 == 0 && DR % 16 == 0 && DV % 32 == 0 && DN >= 16 && DV >= 32, "dims");
   static_assert(MI * (kPStages - 1) < 64, "vmcnt range");
+  static_assert(kPStages >= 4 && kPStages <= 7, "ring depth");
 };
 
 // Uniform parts of one tile's DMA: base pointers of the three source rows
@@ -97,55 +103,74 @@ struct PTileDma {
   int last;
 };
 
-// Per-lane part of region instruction i: source offset of the chunk that
-// lands at this lane's LDS position (swizzle inverted), clamped rows.
+// Per-lane part of region instruction i: source offset (within the tile)
+// of the chunk that lands at this lane's LDS position (swizzle inverted).
 template <class RG, bool VSWZ>
-__device__ __forceinline__ uint32_t region_src(int i, int lane, int last) {
+__device__ __forceinline__ uint32_t region_src(int i, int lane) {
   const int r = i * RG::RPI + lane / RG::CPR;
   const int p = lane % RG::CPR;
   const int j = VSWZ ? ((RG::vgrp(r, p >> 2) << 2) | (p & 3)) : RG::kpos(r, p);
-  return (uint32_t)(min(r, last) * (RG::CPR * 16) + j * 16);
+  return (uint32_t)(r * RG::ROWB + j * 16);
 }
 
-// DMA slot k of this wave: instruction k * kPWaves + wave of the tile.
+// The same offset with its key row clamped to `last` (0..31): rows past
+// seq_k read the last valid row.  The chunk stays within its row.
+template <int ROWB>
+__device__ __forceinline__ uint32_t clamp_row(uint32_t voff, int last) {
+  return min(voff, (uint32_t)(last * ROWB) + (voff & (ROWB - 1)));
+}
+
+// Per-lane source offset of DMA slot k of this wave (instruction k *
+// kPDmaWaves + dw of a tile, dw = wave - 4), unclamped; 0 for a slot the
+// wave does not own.
 template <class SH>
-__device__ __forceinline__ void pissue_one(const PTileDma &d, int k, int wave, int lane) {
-  const int ins0 = k * kPWaves, ins = ins0 + wave;
-  if (!SH::EVEN && ins >= SH::INSTR) return;
+__device__ __forceinline__ uint32_t pslot_voff(int k, int wave, int lane) {
+  const int ins = k * kPDmaWaves + wave;
+  constexpr int E1 = SH::KN::INSTR, E2 = SH::KN::INSTR + SH::KR::INSTR;
+  if (ins < E1) return region_src<typename SH::KN, false>(ins, lane);
+  if constexpr (SH::KR::INSTR > 0)
+    if (ins < E2) return region_src<typename SH::KR, false>(ins - E1, lane);
+  if (ins < SH::INSTR) return region_src<typename SH::VR, true>(ins - E2, lane);
+  return 0;
+}
+
+// DMA slot k of this wave for the tile in d (voff from pslot_voff).
+template <class SH>
+__device__ __forceinline__ void pissue_one(const PTileDma &d, int k, int wave, uint32_t voff) {
+  const int ins = k * kPDmaWaves + wave;
+  if (ins >= SH::INSTR) return;
   constexpr int E1 = SH::KN::INSTR, E2 = SH::KN::INSTR + SH::KR::INSTR;
   const uint32_t st = fresh(d.stage);
-  if (SH::EVEN ? ins0 < E1 : ins < E1) {
-    dma16(fresh(d.kn), region_src<typename SH::KN, false>(ins, lane, d.last),
-          st + SH::KN_OFF + ins * 1024);
-  } else if (SH::EVEN ? ins0 < E2 : ins < E2) {
+  const int last = min(d.last, 31);
+  if (ins < E1) {
+    dma16(fresh(d.kn), clamp_row<SH::KN::ROWB>(voff, last), st + SH::KN_OFF + ins * 1024);
+  } else if (ins < E2) {
     if constexpr (SH::KR::INSTR > 0)
-      dma16(fresh(d.kr), region_src<typename SH::KR, false>(ins - E1, lane, d.last),
-            st + SH::KR_OFF + (ins - E1) * 1024);
+      dma16(fresh(d.kr), clamp_row<SH::KR::ROWB>(voff, last), st + SH::KR_OFF + (ins - E1) * 1024);
   } else {
-    dma16(fresh(d.v), region_src<typename SH::VR, true>(ins - E2, lane, d.last),
-          st + SH::V_OFF + (ins - E2) * 1024);
+    dma16(fresh(d.v), clamp_row<SH::VR::ROWB>(voff, last), st + SH::V_OFF + (ins - E2) * 1024);
   }
 }
 
 template <class SH>
-__device__ __forceinline__ void pissue_tile(const PTileDma &d, int wave, int lane) {
+__device__ __forceinline__ void pissue_tile(const PTileDma &d, int wave,
+                                            const uint32_t (&voff)[SH::MI]) {
 #pragma unroll
-  for (int k = 0; k < SH::MI; ++k) pissue_one<SH>(d, k, wave, lane);
+  for (int k = 0; k < SH::MI; ++k) pissue_one<SH>(d, k, wave, voff[k]);
 }
 
-// Waits until at most k tiles of this wave's DMA are outstanding.
+// Waits until at most k tiles (0 <= k <= kPStages - 2) of this wave's DMA
+// are outstanding; my_instr = the wave's DMA instructions per tile.
 template <class SH>
 __device__ __forceinline__ void pwait_tiles(int k, int my_instr) {
-  if constexpr (SH::EVEN) {
-    if (k <= 0)
-      wait_vmcnt<0>();
-    else if (k == 1)
-      wait_vmcnt<SH::MI>();
-    else
-      wait_vmcnt<(2 * SH::MI < 63 ? 2 * SH::MI : 63)>();
-  } else {
-    wait_vmcnt_dyn(k * my_instr);
-  }
+  constexpr int MAXN = (kPStages - 2) * SH::MI;
+  static_assert(MAXN < 64, "vmcnt range");
+  const int n = k <= 0 ? 0 : k * my_instr;
+  bool done = false;
+  [&]<int... N>(std::integer_sequence<int, N...>) {
+    (void)((N > 0 && !done && n == N ? (wait_vmcnt<N>(), done = true) : false), ...);
+  }(std::make_integer_sequence<int, MAXN + 1>{});
+  if (!done) wait_vmcnt<0>();
 }
 
 // Per-lane LDS byte offsets (relative to a stage) of the MFMA operands.
@@ -175,15 +200,17 @@ __device__ __forceinline__ PLane<SH> plane_offsets(int lane) {
   return la;
 }
 
-// S^T of one tile for both column blocks: 2 x KSTEPS MFMAs into VGPR
-// accumulators, operand reads kPAhead steps ahead; with DMA, this wave's
-// slots for the tile in `d` are spread over the MFMAs.
-template <class SH, bool DMA>
+// S^T of one tile for the wave's 32 rows: one chain of KSTEPS MFMAs into a
+// VGPR accumulator, operand reads kPAhead steps ahead.  With dma_on, the
+// wave's DMA slots of the tile in d are spread over the MFMAs.
+template <class SH>
 __device__ __forceinline__ void ps_phase(const PLane<SH> &la, uint32_t st,
-                                         const bf16x8_t (&qf)[2][SH::KSTEPS], floatx16_t (&s)[2],
-                                         const PTileDma &d, int wave, int lane) {
+                                         const bf16x8_t (&qf)[SH::KSTEPS], floatx16_t &s,
+                                         bool dma_on, const PTileDma &d, int dw,
+                                         const uint32_t (&voff)[SH::MI]) {
   constexpr int D = kPAhead < SH::KSTEPS ? kPAhead : SH::KSTEPS;
   bf16x8_t a[D + 1];
+  __builtin_amdgcn_s_setprio(2);
   [&]<int... K>(std::integer_sequence<int, K...>) {
     ([&] { if constexpr (K < D) a[K] = ds_b128<0>(st + la.s[K]); }(), ...);
     ([&] {
@@ -191,23 +218,18 @@ __device__ __forceinline__ void ps_phase(const PLane<SH> &la, uint32_t st,
       constexpr int after = (kk + D - 1 < SH::KSTEPS - 1 ? D - 1 : SH::KSTEPS - 1 - kk);
       wait_lgkm<after>();
       arrived(a[kk % (D + 1)]);
-      if constexpr (kk == 0) {
-        s[0] = mfma_s_first(a[0], qf[0][0]);
-        s[1] = mfma_s_first(a[0], qf[1][0]);
-      } else {
-        mfma_s_acc(s[0], a[kk % (D + 1)], qf[0][kk]);
-        mfma_s_acc(s[1], a[kk % (D + 1)], qf[1][kk]);
-      }
-      if constexpr (DMA) {
+      if constexpr (kk == 0)
+        s = mfma_s_first(a[0], qf[0]);
+      else
+        mfma_s_acc(s, a[kk % (D + 1)], qf[kk]);
 #pragma unroll
-        for (int k = 0; k < SH::MI; ++k)
-          if ((k * SH::KSTEPS) / SH::MI == kk) pissue_one<SH>(d, k, wave, lane);
-      }
+      for (int k = 0; k < SH::MI; ++k)
+        if ((k * SH::KSTEPS) / SH::MI == kk && dma_on) pissue_one<SH>(d, k, dw, voff[k]);
       if constexpr (kk + D < SH::KSTEPS) a[(kk + D) % (D + 1)] = ds_b128<0>(st + la.s[kk + D]);
     }(), ...);
   }(std::make_integer_sequence<int, SH::KSTEPS>{});
-  mfma_s_drain(s[0]);
-  mfma_s_drain(s[1]);
+  __builtin_amdgcn_s_setprio(0);
+  mfma_s_drain(s);
 }
 
 // V^T fragment j = (k-step ks, column block i): two transposing reads.
@@ -217,41 +239,45 @@ __device__ __forceinline__ bf16x8_t pv_frag(const PLane<SH> &la, uint32_t st) {
   return ds_tr2<ks * 16 * (SH::DV * 2), 8 * (SH::DV * 2)>(st + la.v[cb]);
 }
 
-// O^T += V^T P^T for both column blocks: 2 x 2 x CB MFMAs into the AGPR
-// accumulators, V^T fragments streamed kPvAheadP ahead.
-template <class SH>
-__device__ __forceinline__ void ppv_phase(const PLane<SH> &la, uint32_t st,
-                                          const bf16x8_t (&pb)[2][2], floatx16_t (&o)[2][SH::CB]) {
+// O^T += V^T P^T: 2 x CB MFMAs, V^T fragments streamed kPvAheadP ahead.
+// Each MFMA reads its accumulator CB MFMAs after the one that wrote it; P^T
+// (VALU-written) is consumed a full step after it was formed.
+// mid() runs after the first fragments are requested (their LDS latency
+// overlaps it).
+template <class SH, class MID>
+__device__ __forceinline__ void ppv_phase(const PLane<SH> &la, uint32_t st, const bf16x8_t (&pb)[2],
+                                          floatx16_t (&o)[SH::CB], MID &&mid) {
   constexpr int NA = 2 * SH::CB;
   constexpr int DA = kPvAheadP < NA ? kPvAheadP : NA;
   bf16x8_t a[DA + 1];
   [&]<int... J>(std::integer_sequence<int, J...>) {
     ([&] { if constexpr (J < DA) a[J] = pv_frag<SH, J>(la, st); }(), ...);
+    mid();
     ([&] {
       constexpr int j = J;
       constexpr int after = 2 * (j + DA - 1 < NA - 1 ? DA - 1 : NA - 1 - j);
       wait_lgkm<after>();
       arrived(a[j % (DA + 1)]);
       constexpr int ks = j / SH::CB, cb = j % SH::CB;
-      o[0][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[j % (DA + 1)], pb[0][ks], o[0][cb], 0, 0, 0);
-      o[1][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[j % (DA + 1)], pb[1][ks], o[1][cb], 0, 0, 0);
+      // in place (asm): the accumulators never move between registers
+      mfma_s_acc(o[cb], a[j % (DA + 1)], pb[ks]);
       if constexpr (j + DA < NA) a[(j + DA) % (DA + 1)] = pv_frag<SH, j + DA>(la, st);
     }(), ...);
   }(std::make_integer_sequence<int, NA>{});
 }
 
-// Key (within the tile) of S^T accumulator element j of this lane.
-__device__ __forceinline__ int ptile_key(int j, int half) {
-  return 8 * (j >> 2) + 4 * half + (j & 3);
-}
+// S^T accumulator element j of lane (n, half) holds key 8 (j / 4) + 4 half
+// + j % 4 of the tile for query row n.
 
-// Raw maximum of this lane's 16 scores of column block nb; with MASK, keys
-// at or past seq_k or (causal) after the row's absolute position are out.
+// Raw maximum of this lane's 16 scores; with MASK, keys at or past seq_k or
+// (causal) after the row's absolute position are out.
 template <bool MASK>
 __device__ __forceinline__ float ptile_max(const floatx16_t &s, int key0, int half, int vis_lim) {
+  // keys of this lane: key0 + 4 half + 8 (j / 4) + j % 4; rel < 0 <=> visible
+  const int rel = MASK ? vfresh(key0 + 4 * half - vis_lim) : 0;
   float x[16];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) x[j] = (!MASK || key0 + ptile_key(j, half) < vis_lim) ? s[j] : -INFINITY;
+  for (int j = 0; j < 16; ++j) x[j] = (!MASK || rel + 8 * (j >> 2) + (j & 3) < 0) ? s[j] : -INFINITY;
   const float a = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
   const float b = fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7]));
   const float c = fmaxf(fmaxf(x[8], x[9]), fmaxf(x[10], x[11]));
@@ -263,11 +289,12 @@ __device__ __forceinline__ float ptile_max(const floatx16_t &s, int key0, int ha
 template <bool MASK>
 __device__ __forceinline__ void ptile_p(const floatx16_t &s, float sl2, float m, int key0,
                                         int half, int vis_lim, float &l, bf16x8_t (&pb)[2]) {
+  const int rel = MASK ? vfresh(key0 + 4 * half - vis_lim) : 0;
   float p[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j], sl2, -m));
-    if (MASK) p[j] = key0 + ptile_key(j, half) < vis_lim ? p[j] : 0.f;
+    if (MASK) p[j] = rel + 8 * (j >> 2) + (j & 3) < 0 ? p[j] : 0.f;
   }
   float q[8];
 #pragma unroll
@@ -291,6 +318,15 @@ __device__ __forceinline__ bf16x8_t load_q_frag(const uint16_t *__restrict__ qn,
 }
 
 // grid.x = batch * heads * n_qtiles (heaviest query tiles first when causal)
+//
+// Schedule.  Step k (0 <= k < 2 * ntb + 3, a barrier before each) is local
+// step k - g of a group-g wave.  Local step 2j: S^T of tile j.  Local step
+// 2j + 1: softmax of tile j, then P.V of tile j - 1.  Tile j is therefore
+// read last in step 2j + 2 (group 1's P.V), and the DMA of tile j +
+// kPStages into its stage is issued at step 2j + 5 (odd steps k >= 3 issue
+// tile (k - 5) / 2 + kPStages; the prologue issues tiles 0 .. kPStages - 2).
+// Before step 2m every wave waits for its share of tile m, so tile m is
+// complete in LDS when group 0 reads it.
 template <int DN, int DR, int DV>
 __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
     const uint16_t *__restrict__ q_nope, const uint16_t *__restrict__ q_rope,
@@ -304,6 +340,7 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
   const uint32_t ovf_flags = ring_u + kPStages * SH::STAGE_BYTES;  // kPWaves words
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2;
   const int lane = tid & 63;
   const int n = lane & 31, half = lane >> 5;
   // A negative scale is applied as |scale| with the sign folded into q
@@ -311,13 +348,31 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
   const uint32_t q_sign = scale_log2 < 0.f ? 0x80008000u : 0u;
   const float sl2 = fabsf(scale_log2);
 
+  // Block order.  Query tiles are ranked by work (rank 0 = heaviest when
+  // causal) and issued rank pair by rank pair.  Within a pair, the two
+  // tiles of one (b, h) get block indices 8 apart: blocks are dealt to the
+  // 8 XCDs round-robin, so both land on the same XCD at nearly the same
+  // time and the second one's K/V reads hit that XCD's L2.
   const int BH = d.batch * d.heads;
   const int L = blockIdx.x;
-  const int qt = causal ? (n_qtiles - 1 - L / BH) : (L / BH);
-  const int bh = L % BH;
+  int rank, bh;
+  if ((BH & 7) == 0 && L < 2 * BH * (n_qtiles >> 1)) {
+    const int pr = L / (2 * BH), rem = L - pr * 2 * BH;
+    const int x = rem & 7, r = rem >> 3;
+    rank = 2 * pr + (r & 1);
+    bh = (r >> 1) * 8 + x;
+  } else if ((BH & 7) == 0) {
+    rank = n_qtiles - 1;  // odd tile count: the last rank alone
+    bh = L - 2 * BH * (n_qtiles >> 1);
+  } else {
+    rank = L / BH;
+    bh = L % BH;
+  }
+  const int qt = causal ? n_qtiles - 1 - rank : rank;
   const int b = bh / d.heads, h = bh - b * d.heads;
   const int q0 = qt * kPRows;
-  const int wrow0 = q0 + wave * kPRowsWave;
+  // The two waves sharing a SIMD (w, w + 4) own adjacent 32-row blocks.
+  const int row_first = q0 + 32 * (2 * (wave & 3) + grp);
 
   const int64_t bhq = (int64_t)bh * d.seq_q;
   const int64_t bhk = (int64_t)bh * d.seq_k;
@@ -326,41 +381,26 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
   const uint8_t *krb = reinterpret_cast<const uint8_t *>(k_rope + bkr * DR);
   const uint8_t *vb = reinterpret_cast<const uint8_t *>(v + bhk * DV);
 
-  // Q fragments (B operand of S^T) for the wave's two 32-row column blocks.
-  bf16x8_t qf[2][SH::KSTEPS];
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const int row = wrow0 + nb * 32 + n;
-    const bool ok = row < d.seq_q;
-    const int64_t qrow = bhq + (ok ? row : d.seq_q - 1);
-    const uint32_t keep = ok ? 0xffffffffu : 0u;
-#pragma unroll
-    for (int kk = 0; kk < SH::KSTEPS; ++kk) {
-      u32x4_t u = __builtin_bit_cast(u32x4_t, load_q_frag<SH>(q_nope, q_rope, qrow, kk * 16 + half * 8));
-#pragma unroll
-      for (int i = 0; i < 4; ++i) u[i] = (u[i] ^ q_sign) & keep;
-      qf[nb][kk] = __builtin_bit_cast(bf16x8_t, u);
-    }
-  }
-
   // key horizon (exclusive) of the block and of this wave
   int kend_blk = d.seq_k, kend_w = d.seq_k;
   if (causal) {
     kend_blk = min(d.seq_k, d.q_offset + min(q0 + kPRows, d.seq_q));
-    kend_w = min(d.seq_k, d.q_offset + min(wrow0 + kPRowsWave, d.seq_q));
+    kend_w = min(d.seq_k, d.q_offset + min(row_first + 32, d.seq_q));
   }
-  if (wrow0 >= d.seq_q) kend_w = 0;  // no query row in this wave
+  if (row_first >= d.seq_q) kend_w = 0;  // no query row in this wave
   const int ntb = (kend_blk + kPKeys - 1) / kPKeys;  // tiles of the block
   const int ntw = (kend_w + kPKeys - 1) / kPKeys;    // tiles of this wave
-  const int my_instr = (SH::INSTR - wave + kPWaves - 1) / kPWaves;
+  // group 1's waves issue the DMA (slot k of wave dw: instruction k * 4 + dw)
+  const int dw = wave & 3;
+  const int my_instr = grp == 1 ? (SH::INSTR - dw + kPDmaWaves - 1) / kPDmaWaves : 0;
   const PLane<SH> la = plane_offsets<SH>(lane);
+  uint32_t voff[SH::MI];
+#pragma unroll
+  for (int i = 0; i < SH::MI; ++i) voff[i] = pslot_voff<SH>(i, dw, lane);
   // a tile needs the mask if one of its keys is invisible to some row of
   // the wave: past seq_k, or (causal) after the wave's first row
-  const int mask_from = causal ? min(d.seq_k, d.q_offset + wrow0 + 1) : d.seq_k;
-  int vis_lim[2];
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb)
-    vis_lim[nb] = causal ? min(d.seq_k, d.q_offset + wrow0 + nb * 32 + n + 1) : d.seq_k;
+  const int mask_from = causal ? min(d.seq_k, d.q_offset + row_first + 1) : d.seq_k;
+  const int vis_lim = causal ? min(d.seq_k, d.q_offset + row_first + n + 1) : d.seq_k;
   auto tile_dma = [&](int t) {
     const int key0 = t * kPKeys;
     return PTileDma{kb + (int64_t)key0 * (DN * 2), krb + (int64_t)key0 * (DR * 2),
@@ -369,103 +409,123 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
   };
   auto stage_u = [&](int t) { return ring_u + (uint32_t)((t % kPStages) * SH::STAGE_BYTES); };
 
-  floatx16_t o[2][SH::CB];
-  floatx16_t s[2];
-  bf16x8_t pb[2][2], pn[2][2];
-  float m_ref[2], l_run[2], m_raw[2];
-  float m_init[2] = {-INFINITY, -INFINITY};
+  // Q fragments (B operand of S^T) of the wave's 32 rows.
+  bf16x8_t qf[SH::KSTEPS];
+  {
+    const int row = row_first + n;
+    const bool ok = row < d.seq_q;
+    const int64_t qrow = bhq + (ok ? row : d.seq_q - 1);
+    const uint32_t keep = ok ? 0xffffffffu : 0u;
+#pragma unroll
+    for (int kk = 0; kk < SH::KSTEPS; ++kk) {
+      u32x4_t u = __builtin_bit_cast(u32x4_t, load_q_frag<SH>(q_nope, q_rope, qrow, kk * 16 + half * 8));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) u[i] = (u[i] ^ q_sign) & keep;
+      qf[kk] = __builtin_bit_cast(bf16x8_t, u);
+    }
+  }
+
+  floatx16_t o[SH::CB];
+  floatx16_t s;
+  bf16x8_t pb[2], pn[2];
+  float m_ref = -INFINITY, l_run, m_raw;
+  float m_init = -INFINITY;
+  const int nsteps = 2 * ntb + 3;
   for (;;) {
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
+    for (int cb = 0; cb < SH::CB; ++cb)
 #pragma unroll
-      for (int cb = 0; cb < SH::CB; ++cb)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) o[nb][cb][j] = 0.f;
-      l_run[nb] = 0.f;
-      m_raw[nb] = -INFINITY;
-      m_ref[nb] = m_init[nb];
-    }
+      for (int j = 0; j < 16; ++j) o[cb][j] = 0.f;
+    l_run = 0.f;
+    m_raw = -INFINITY;
     if (lane == 0) ds_w32(ovf_flags + 4 * wave, 0u);
 
-    // prologue: kPStages-1 tiles in flight, then S and softmax of tile 0
 #pragma unroll
     for (int p = 0; p < kPStages - 1; ++p)
-      if (p < ntb) pissue_tile<SH>(tile_dma(p), wave, lane);
-    pwait_tiles<SH>(min(kPStages - 2, ntb - 1), my_instr);
-    wait_lgkm<0>();
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    if (ntw > 0) {
-      ps_phase<SH, false>(la, stage_u(0), qf, s, PTileDma{}, wave, lane);
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        m_raw[nb] = ptile_max<true>(s[nb], 0, half, vis_lim[nb]);
-        // key 0 is visible to every row: the first tile's maximum is finite
-        if (m_ref[nb] == -INFINITY) m_ref[nb] = xor32_max(m_raw[nb]) * sl2;
-        ptile_p<true>(s[nb], sl2, m_ref[nb], 0, half, vis_lim[nb], l_run[nb], pb[nb]);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
+      if (grp == 1 && p < ntb) pissue_tile<SH>(tile_dma(p), dw, voff);
 
-    // Iteration it: S^T of tile it+1, then P.V of tile it with the softmax
-    // of tile it+1 spread over its MFMAs.  MODE 0: unmasked tile it+1 with
-    // its DMA slots spread over S^T; MODE 1: masked tile it+1, DMA up
-    // front; MODE 2: this wave is past its horizon for tile it+1 (P.V of
-    // tile it only, or nothing).
-    auto step = [&](auto mode_c, int it) __attribute__((always_inline)) {
-      constexpr int MODE = decltype(mode_c)::value;
-      const int nxt = it + kPStages - 1;
-      pwait_tiles<SH>(min(kPStages - 3, ntb - 2 - it), my_instr);
-      // every wave is past iteration it-1 (stage (it-1) % kPStages is free)
-      // and tile it+1 is visible to every wave
+    // softmax of tile j (its S^T is in s) into pn
+    auto sm = [&](auto mask_c, int j) __attribute__((always_inline)) {
+      constexpr bool MASK = decltype(mask_c)::value;
+      const int key0 = j * kPKeys;
+      const float mr = ptile_max<MASK>(s, key0, half, vis_lim);
+      if (j == 0) {
+        // key 0 is visible to every row: the first tile's maximum is finite
+        m_raw = mr;
+        m_ref = m_init == -INFINITY ? xor32_max(mr) * sl2 : m_init;
+      } else {
+        m_raw = fmaxf(m_raw, mr);
+      }
+      ptile_p<MASK>(s, sl2, m_ref, key0, half, vis_lim, l_run, pn);
+    };
+
+    // Step k: vmcnt wait (even k), barrier.  At odd steps k >= 3, group 1
+    // issues tile (k - 5) / 2 + kPStages, spread over its S^T MFMAs when it
+    // has an S^T in that step.
+    int k = 0;
+    auto head = [&]() __attribute__((always_inline)) {
+      if ((k & 1) == 0) {
+        // tile k/2 complete (this wave's share); later tiles may stay in flight
+        const int m = k >> 1;
+        const int last = min(ntb - 1, max(kPStages - 2, m + kPStages - 3));
+        pwait_tiles<SH>(last - m, my_instr);
+      }
       wait_lgkm<0>();
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (MODE == 0) {
-        ps_phase<SH, true>(la, stage_u(it + 1), qf, s, tile_dma(nxt), wave, lane);
-      } else {
-        if (nxt < ntb) pissue_tile<SH>(tile_dma(nxt), wave, lane);
-        if constexpr (MODE == 1) ps_phase<SH, false>(la, stage_u(it + 1), qf, s, PTileDma{}, wave, lane);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      if constexpr (MODE == 2) {
-        if (it < ntw) ppv_phase<SH>(la, stage_u(it), pb, o);
-      } else {
-        const int key0 = (it + 1) * kPKeys;
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
-          m_raw[nb] = fmaxf(m_raw[nb], ptile_max<MODE == 1>(s[nb], key0, half, vis_lim[nb]));
-        ppv_phase<SH>(la, stage_u(it), pb, o);
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
-          ptile_p<MODE == 1>(s[nb], sl2, m_ref[nb], key0, half, vis_lim[nb], l_run[nb], pn[nb]);
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-          pb[nb][0] = pn[nb][0];
-          pb[nb][1] = pn[nb][1];
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
+      ++k;
     };
-    for (int it = 0; it + 1 < ntb; ++it) {
-      const int key1 = (it + 1) * kPKeys;
-      if (it + 1 >= ntw)
-        step(std::integral_constant<int, 2>{}, it);
-      else if (key1 + kPKeys > mask_from || it + kPStages - 1 >= ntb)
-        step(std::integral_constant<int, 1>{}, it);
+    // tile DMA'd in the step just begun (k - 1), or ntb if none
+    auto dma_tile = [&]() {
+      return (grp == 1 && k >= 4 && (k & 1) == 0) ? (k - 6) / 2 + kPStages : ntb;
+    };
+    auto dma_only = [&]() __attribute__((always_inline)) {
+      const int t = dma_tile();
+      if (t < ntb) pissue_tile<SH>(tile_dma(t), dw, voff);
+    };
+    // The wave's local steps: S^T of tile j, then softmax of tile j with the
+    // P.V of tile j - 1.  Tiles before jm need no mask.
+    const int jm = min(ntw, mask_from / kPKeys);  // first tile needing the mask
+    if (grp == 1) head();  // group 1 starts one step late
+    if (ntw > 0) {
+      head();
+      ps_phase<SH>(la, stage_u(0), qf, s, false, PTileDma{}, dw, voff);
+      head();
+      if (jm == 0)
+        sm(std::true_type{}, 0);
       else
-        step(std::integral_constant<int, 0>{}, it);
+        sm(std::false_type{}, 0);
+      pb[0] = pn[0];
+      pb[1] = pn[1];
+      __builtin_amdgcn_sched_barrier(0);
+      auto body = [&](auto mask_c, int j) __attribute__((always_inline)) {
+        head();
+        const int t = dma_tile();
+        ps_phase<SH>(la, stage_u(j), qf, s, t < ntb, tile_dma(t), dw, voff);
+        __builtin_amdgcn_sched_barrier(0);
+        head();
+        ppv_phase<SH>(la, stage_u(j - 1), pb, o,
+                      [&]() __attribute__((always_inline)) { sm(mask_c, j); });
+        pb[0] = pn[0];
+        pb[1] = pn[1];
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      int j = 1;
+      for (; j < jm; ++j) body(std::false_type{}, j);
+      for (; j < ntw; ++j) body(std::true_type{}, j);
+      head();  // no S^T of tile ntw
+      dma_only();
+      head();
+      ppv_phase<SH>(la, stage_u(ntw - 1), pb, o, [] {});
+      __builtin_amdgcn_sched_barrier(0);
     }
-    // P.V of the last tile
-    if (ntb - 1 < ntw) {
-      wait_lgkm<0>();
-      ppv_phase<SH>(la, stage_u(ntb - 1), pb, o);
+    while (k < nsteps) {
+      head();
+      dma_only();
     }
 
     // Overflow check: each row's scaled maximum against its reference.
-    bool ovf = false;
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) ovf |= xor32_max(m_raw[nb]) * sl2 > m_ref[nb] + kPSlack;
+    const bool ovf = ntw > 0 && xor32_max(m_raw) * sl2 > m_ref + kPSlack;
     if (__ballot(ovf) != 0 && lane == 0) ds_w32(ovf_flags + 4 * wave, 1u);
     wait_lgkm<0>();
     __builtin_amdgcn_s_barrier();
@@ -482,27 +542,24 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
     if (__builtin_amdgcn_readfirstlane(any) == 0) break;
     // Rare: redo the block's tiles with every row's true maximum.
     __builtin_amdgcn_s_barrier();  // all waves have read the flags
-    m_init[0] = xor32_max(m_raw[0]) * sl2;
-    m_init[1] = xor32_max(m_raw[1]) * sl2;
+    m_init = xor32_max(m_raw) * sl2;
   }
   // the final P.V MFMAs complete before their accumulators are read
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 
   // finalise
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const float l = xor32_sum(l_run[nb]);
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    const int row = wrow0 + nb * 32 + n;
-    if (row >= d.seq_q) continue;
+  const float l = xor32_sum(l_run);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const int row = row_first + n;
+  if (row < d.seq_q) {
     uint16_t *dst = out + (bhq + row) * DV;
 #pragma unroll
     for (int cb = 0; cb < SH::CB; ++cb)
 #pragma unroll
       for (int jq = 0; jq < 4; ++jq) {
         u32x2_t w;
-        w[0] = pack2_bf16(o[nb][cb][jq * 4 + 0] * inv, o[nb][cb][jq * 4 + 1] * inv);
-        w[1] = pack2_bf16(o[nb][cb][jq * 4 + 2] * inv, o[nb][cb][jq * 4 + 3] * inv);
+        w[0] = pack2_bf16(o[cb][jq * 4 + 0] * inv, o[cb][jq * 4 + 1] * inv);
+        w[1] = pack2_bf16(o[cb][jq * 4 + 2] * inv, o[cb][jq * 4 + 3] * inv);
         *reinterpret_cast<u32x2_t *>(dst + cb * 32 + 8 * jq + 4 * half) = w;
       }
   }
@@ -518,6 +575,7 @@ qmla_status launch_prefill_shape(const qmla_prefill_dims &d, const uint16_t *q_n
   const int64_t nblocks = (int64_t)d.batch * d.heads * n_qtiles;
   QMLA_REQUIRE(nblocks <= 0x7fffffff, QMLA_ERR_SHAPE, "too many query tiles");
   const size_t lds = (size_t)kPStages * SH::STAGE_BYTES + kPWaves * 4;
+  static_assert((size_t)kPStages * SH::STAGE_BYTES + kPWaves * 4 <= 160 * 1024, "LDS");
   auto kern = k_prefill_mfma<DN, DR, DV>;
   QMLA_TRY(ensure_dynamic_lds((const void *)kern, lds));
   kern<<<dim3((unsigned)nblocks), dim3(kPWaves * 64), lds, stream>>>(
