@@ -352,7 +352,9 @@ qmla_status validate_decode(const qmla_decode_dims *d, const qmla_kv_cache *c) {
                c->r, c->dr);
   int64_t total = 0;
   for (int32_t i = 0; i < d->batch; ++i) total += c->h_lens[i];
-  QMLA_REQUIRE(total < (int64_t)1 << 31, QMLA_ERR_UNSUPPORTED, "%lld tokens in one call",
+  // the in-kernel plan adds decode_mfma_seg_tokens() virtual tokens per sequence
+  const int64_t virt = total + (int64_t)d->batch * decode_mfma_seg_tokens(d->rows);
+  QMLA_REQUIRE(virt < (int64_t)1 << 31, QMLA_ERR_UNSUPPORTED, "%lld tokens in one call",
                (long long)total);
   return QMLA_OK;
 }

@@ -430,7 +430,11 @@ __device__ __forceinline__ bool any_flag(uint32_t flags) {
 
 // ---- in-kernel split plan.  The concatenated tokens of the batch are cut
 // into gridDim.x pieces of `chunk` tokens; piece i covers [i*chunk,
-// (i+1)*chunk).  A (piece, sequence) overlap is a segment; every segment
+// (i+1)*chunk).  Each sequence is preceded by seg_tokens virtual tokens in
+// this stream: a segment costs a fixed setup (Q load, prologue, partial
+// store) on top of its tiles, and a piece that starts a new sequence gets
+// correspondingly fewer real tokens.  A (piece, sequence) overlap of real
+// tokens is a segment; every segment
 // writes a partial result to its own slot: sequence b owns slots
 // sb[b] .. sb[b] + ns[b] - 1 (ns[b] = pieces it touches), in piece order.
 // Each block derives its own segments (no separate planning launch): the
@@ -473,31 +477,31 @@ __device__ int32_t lds_exscan(int32_t *a, int32_t n, int32_t *tmp) {
 
 // One planning round: fills list[0..count) with this block's segments of
 // sequences >= from, sets *next to the first sequence not listed (batch
-// when done).  scratch: 2 * (batch + 1) + NT int32 of idle LDS.
+// when done).  scratch: 2 * (batch + 1) + NT int32 of idle LDS.  In the
+// virtual stream, sequence b occupies [P[b], P[b + 1]) with its real
+// tokens at [P[b] + seg_tokens, P[b + 1]).
 template <int NT>
 __device__ void plan_round(const int32_t *__restrict__ lens, int32_t batch, int32_t from,
-                           int32_t *scratch, SegDesc *list, int32_t *meta,
+                           int32_t seg_tokens, int32_t *scratch, SegDesc *list, int32_t *meta,
                            int2 *__restrict__ seq_info) {
   const int tid = threadIdx.x;
   const int blocks = gridDim.x, piece = blockIdx.x;
   int32_t *P = scratch, *SB = scratch + batch + 1, *tmp = SB + batch + 1;
-  for (int b = tid; b < batch; b += NT) P[b] = lens[b];
+  for (int b = tid; b < batch; b += NT) P[b] = lens[b] + seg_tokens;
   __syncthreads();
   const int32_t N = lds_exscan<NT>(P, batch, tmp);
   if (tid == 0) P[batch] = N;
   const int32_t chunk = max(1, (N + blocks - 1) / blocks);
   __syncthreads();
-  for (int b = tid; b < batch; b += NT) {
-    const int32_t p0 = P[b], p1 = P[b + 1];
-    SB[b] = p1 > p0 ? (p1 - 1) / chunk - p0 / chunk + 1 : 0;
-  }
+  // pieces touching the real tokens [v0, v1) of sequence b
+  auto touched = [&](int32_t v0, int32_t v1) { return v1 > v0 ? (v1 - 1) / chunk - v0 / chunk + 1 : 0; };
+  for (int b = tid; b < batch; b += NT) SB[b] = touched(P[b] + seg_tokens, P[b + 1]);
   __syncthreads();
   (void)lds_exscan<NT>(SB, batch, tmp);
   if (from == 0 && blockIdx.y == 0) {
     for (int b = tid; b < batch; b += NT) {
-      const int32_t p0 = P[b], p1 = P[b + 1];
-      if (min(p0 / chunk, blocks - 1) == piece)
-        seq_info[b] = make_int2(SB[b], p1 > p0 ? (p1 - 1) / chunk - p0 / chunk + 1 : 0);
+      const int32_t v0 = P[b] + seg_tokens, v1 = P[b + 1];
+      if (min(v0 / chunk, blocks - 1) == piece) seq_info[b] = make_int2(SB[b], touched(v0, v1));
     }
   }
   if (tid == 0) {
@@ -509,13 +513,14 @@ __device__ void plan_round(const int32_t *__restrict__ lens, int32_t batch, int3
       if (P[mid + 1] > start) hi = mid; else lo = mid + 1;
     }
     int32_t cnt = 0, b = lo;
-    for (; b < batch && P[b] < end && cnt < kSegCap; ++b) {
-      const int32_t p0 = P[b], p1 = P[b + 1];
-      if (p1 <= p0) continue;
-      list[cnt++] = SegDesc{b, max(start, p0) - p0, min(end, p1) - p0, SB[b] + (piece - p0 / chunk)};
+    for (; b < batch && P[b] + seg_tokens < end && cnt < kSegCap; ++b) {
+      const int32_t v0 = P[b] + seg_tokens, v1 = P[b + 1];
+      const int32_t a = max(start, v0), e = min(end, v1);
+      if (e <= a) continue;  // empty sequence, or real tokens outside the piece
+      list[cnt++] = SegDesc{b, a - v0, e - v0, SB[b] + (piece - v0 / chunk)};
     }
     meta[0] = cnt;
-    meta[1] = (b < batch && P[b] < end) ? b : batch;
+    meta[1] = (b < batch && P[b] + seg_tokens < end) ? b : batch;
   }
   __syncthreads();
 }
@@ -537,8 +542,8 @@ template <int R, int DR, int NW, int NSTAGE, typename QT>
 __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
     const uint8_t *__restrict__ pool, const int64_t *__restrict__ offsets,
     const int32_t *__restrict__ lens, int32_t batch, const QT *__restrict__ q_lat,
-    const QT *__restrict__ q_rope, int32_t rows, float scale_log2, int2 *__restrict__ seq_info,
-    float *__restrict__ part_o, float *__restrict__ part_lse) {
+    const QT *__restrict__ q_rope, int32_t rows, float scale_log2, int32_t seg_tokens,
+    int2 *__restrict__ seq_info, float *__restrict__ part_o, float *__restrict__ part_lse) {
   using SH = DecodeShape<R, DR>;
   using PS = PvSplit<R, NW>;
   static_assert(NSTAGE >= 3, "the pipelined loop keeps two stages resident");
@@ -590,7 +595,8 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
 
   int32_t next_seq = 0;
   do {
-  plan_round<NW * 64>(lens, batch, next_seq, (int32_t *)ring_raw, seg_list, seg_meta, seq_info);
+  plan_round<NW * 64>(lens, batch, next_seq, seg_tokens, (int32_t *)ring_raw, seg_list, seg_meta,
+                      seq_info);
   const int32_t nseg = __builtin_amdgcn_readfirstlane(seg_meta[0]);
   next_seq = __builtin_amdgcn_readfirstlane(seg_meta[1]);
   for (int32_t si = 0; si < nseg; ++si) {
@@ -833,19 +839,20 @@ qmla_status launch_shape(const DecodeArgs &a, hipStream_t stream) {
   const int passes = (a.rows + NW * 32 - 1) / (NW * 32);
   dim3 grid(a.blocks, passes), block(NW * 64);
   const float sl2 = a.scale * 1.4426950408889634f;
+  const int32_t seg_tokens = decode_mfma_seg_tokens(a.rows);
   const uint8_t *pool = static_cast<const uint8_t *>(a.cache->rows);
   if (a.q_dtype == QMLA_BF16) {
     auto k = k_decode_mfma<R, DR, NW, NSTAGE, uint16_t>;
     QMLA_TRY(ensure_dynamic_lds((const void *)k, lds));
     k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, a.cache->d_lens, a.batch,
                                     (const uint16_t *)a.q_lat, (const uint16_t *)a.q_rope, a.rows,
-                                    sl2, a.seq_info, a.part_o, a.part_lse);
+                                    sl2, seg_tokens, a.seq_info, a.part_o, a.part_lse);
   } else {
     auto k = k_decode_mfma<R, DR, NW, NSTAGE, float>;
     QMLA_TRY(ensure_dynamic_lds((const void *)k, lds));
     k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, a.cache->d_lens, a.batch,
                                     (const float *)a.q_lat, (const float *)a.q_rope, a.rows, sl2,
-                                    a.seq_info, a.part_o, a.part_lse);
+                                    seg_tokens, a.seq_info, a.part_o, a.part_lse);
   }
   QMLA_LAUNCH_CHECK("k_decode_mfma");
   const int row_blocks = (a.rows + 31) / 32;
@@ -871,6 +878,11 @@ bool decode_mfma_supported(int32_t rows, int32_t r, int32_t dr) {
 }
 
 int decode_mfma_blocks_per_cu(int32_t rows) { return rows <= 64 ? 2 : 1; }
+
+// Virtual tokens charged per sequence start in the split plan: the fixed
+// cost of a segment (Q load, prologue latency, l exchange, partial store),
+// ~32K clocks at 128 rows, over the loop's ~100 clocks per token.
+int32_t decode_mfma_seg_tokens(int32_t rows) { return rows > 64 ? 320 : 64; }
 
 qmla_status launch_decode_mfma(const DecodeArgs &a, hipStream_t stream) {
   QMLA_REQUIRE(a.rows <= 65535 * 128, QMLA_ERR_SHAPE, "too many query rows");
