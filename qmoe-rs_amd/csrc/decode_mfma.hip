@@ -732,7 +732,9 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
     const int frow = row0 + wave * 32 + fn;
     if (fh == 0) ds_w32(l_rows + 4 * (wave * 32 + fn), __builtin_bit_cast(uint32_t, l_run));
     const int slot = sg.slot;
-    if (fh == 0) part_lse[(int64_t)slot * (row_blocks * 32) + frow] = lse;
+    // rows past the padded partial layout (a wave beyond the last 32-row
+    // block of this pass) store nothing
+    if (fh == 0 && frow < row_blocks * 32) part_lse[(int64_t)slot * (row_blocks * 32) + frow] = lse;
     __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
     __builtin_amdgcn_s_barrier();
     // every denominator first: no LDS access between the output stores
@@ -751,6 +753,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
 #pragma unroll
     for (int r = 0; r < PS::NRB; ++r) {
       const int rb = blockIdx.y * NW + rg + r * PS::RW;  // 32-row block of the padded rows
+      if (rb >= row_blocks) continue;
       float *blk = part_o + (((int64_t)slot * row_blocks + rb) * (R / 32)) * 1024 + fl * 4;
 #pragma unroll
       for (int i = 0; i < PS::NCB; ++i) {

@@ -77,6 +77,25 @@ def test_decode_f32_v2lite_subset(qmla_gpu):
     np.testing.assert_allclose(lse, rlse, rtol=1e-5)
 
 
+@pytest.mark.parametrize("rows_m", [70, 96])
+def test_decode_bf16_rows_not_multiple_of_pass(qmla_gpu, rows_m):
+    """Row counts that leave the last wave of a 128-row pass without rows:
+    its partial results must not be stored (they would land in the next
+    split slot).  Several sequences and two split counts, so neighbouring
+    slots belong to different sequences."""
+    q = qmla_gpu
+    lens = [300, 1, 2048, 77, 515, 4096]
+    cache, rows, offs = make_cache(q, lens, 512, 64, q.BF16, 131)
+    ql, qr = O.normal((6, rows_m, 512), 132), O.normal((6, rows_m, 64), 133)
+    ref, rlse = O.decode_absorbed(ql, qr, rows, offs, lens, 0.08)
+    for splits in (0, 37):
+        out, lse = run(q, cache, ql, qr, 0.08, splits=splits)
+        err = rel_err(out, ref)
+        print(f"rows={rows_m} splits={splits} rel_err={err:.2e}")
+        assert err < TOL_BF16
+        np.testing.assert_allclose(lse, rlse, atol=2e-2)
+
+
 def test_decode_bf16_v2lite_full(qmla_gpu):
     """C2: batch 32, 16 heads, 4096 cached + 1, bf16 cache, scale 1/sqrt(192)."""
     q = qmla_gpu
