@@ -353,7 +353,8 @@ qmla_status validate_decode(const qmla_decode_dims *d, const qmla_kv_cache *c) {
   int64_t total = 0;
   for (int32_t i = 0; i < d->batch; ++i) total += c->h_lens[i];
   // the in-kernel plan adds decode_mfma_seg_tokens() virtual tokens per sequence
-  const int64_t virt = total + (int64_t)d->batch * decode_mfma_seg_tokens(d->rows);
+  const int64_t virt =
+      total + (int64_t)d->batch * decode_mfma_seg_tokens(d->rows, d->kv_lora_rank, d->rope_dim);
   QMLA_REQUIRE(virt < (int64_t)1 << 31, QMLA_ERR_UNSUPPORTED, "%lld tokens in one call",
                (long long)total);
   return QMLA_OK;
@@ -368,7 +369,7 @@ int32_t choose_blocks(const qmla_decode_dims *d, const qmla_kv_cache *c, int32_t
   int cus = device_cu_count();
   if (cus <= 0) cus = 256;
   int per_cu = (c->dtype == QMLA_BF16 && decode_mfma_supported(d->rows, d->kv_lora_rank, d->rope_dim))
-                   ? decode_mfma_blocks_per_cu(d->rows)
+                   ? decode_mfma_blocks_per_cu(d->rows, d->kv_lora_rank, d->rope_dim)
                    : 4;
   int64_t target = (int64_t)cus * per_cu;
   const int64_t min_tokens = 256;

@@ -836,13 +836,356 @@ __global__ __launch_bounds__(256) void k_decode_merge_frag(
   }
 }
 
+// ---- narrow decode: one 32-row block (rows <= 32), all four SIMDs ------
+// With few query rows the MFMA work per token is small, so a block puts
+// four waves on one 32-row block instead of one wave: wave w computes S^T
+// over its quarter of the latent dims (KSTEPS / 4 k-steps); the four
+// partial S^T are summed through LDS; wave v takes the softmax of
+// accumulator elements 4v..4v+3 (tokens 8v + 4 half + 0..3 of each lane's
+// row); P^T goes through the P^T staging rows; and the P.V product is split
+// by column, wave w owning column blocks w * CB/4 .. (w + 1) * CB/4 - 1.
+// Three barriers per tile and no software pipelining: this path is bound
+// by HBM by a wide margin, and the kNarrowStages-tile ring keeps
+// kNarrowStages - 1 tiles in flight.
+constexpr int kNarrowStages = 3;
+constexpr int kNarrowRed = 4 * 4 * 64 * 16;  // partial S^T: [wave][quarter][lane] x 16 B
+
+// Partial S^T of one tile over the KQ k-steps at per-lane stage offsets sa.
+template <int KQ>
+__device__ __forceinline__ void narrow_s_phase(uint32_t st, const uint32_t (&sa)[KQ],
+                                               const bf16x8_t (&qf)[KQ], floatx16_t &s) {
+  constexpr int D = KQ < 4 ? KQ : 4;
+  bf16x8_t a[D + 1];
+  [&]<int... K>(std::integer_sequence<int, K...>) {
+    ([&] { if constexpr (K < D) a[K] = ds_b128<0>(st + sa[K]); }(), ...);
+    ([&] {
+      constexpr int kk = K;
+      constexpr int after = (kk + D - 1 < KQ - 1 ? D - 1 : KQ - 1 - kk);
+      wait_lgkm<after>();
+      arrived(a[kk % (D + 1)]);
+      if constexpr (kk == 0)
+        s = mfma_s_first(a[0], qf[0]);
+      else
+        mfma_s_acc(s, a[kk % (D + 1)], qf[kk]);
+      if constexpr (kk + D < KQ) a[(kk + D) % (D + 1)] = ds_b128<0>(st + sa[kk + D]);
+    }(), ...);
+  }(std::make_integer_sequence<int, KQ>{});
+  mfma_s_drain(s);
+}
+
+// Quarter q (elements 4q .. 4q+3) of an S^T accumulator to LDS.
+template <int Q>
+__device__ __forceinline__ void red_write(uint32_t addr, const floatx16_t &s) {
+  const floatx4_t v = __builtin_shufflevector(s, s, 4 * Q, 4 * Q + 1, 4 * Q + 2, 4 * Q + 3);
+  asm volatile("ds_write_b128 %0, %1" : : "v"(addr), "v"(v));
+}
+
+template <int R, int DR>
+constexpr size_t narrow_lds_bytes() {
+  return (size_t)kNarrowStages * DecodeShape<R, DR>::STAGE_BYTES + kNarrowRed + 32 * kPRow +
+         4 * 32 * 4 + 4 * 4 + kSegCap * sizeof(SegDesc) + 16;
+}
+
+template <int R, int DR, typename QT>
+__global__ __launch_bounds__(256) void k_decode_narrow(
+    const uint8_t *__restrict__ pool, const int64_t *__restrict__ offsets,
+    const int32_t *__restrict__ lens, int32_t batch, const QT *__restrict__ q_lat,
+    const QT *__restrict__ q_rope, int32_t rows, float scale_log2, int32_t seg_tokens,
+    int2 *__restrict__ seq_info, float *__restrict__ part_o, float *__restrict__ part_lse) {
+  using SH = DecodeShape<R, DR>;
+  constexpr int NW = 4, NSTAGE = kNarrowStages;
+  constexpr int KQ = SH::KSTEPS / NW;  // k-steps of this wave's S^T quarter
+  constexpr int NCB = SH::CB / NW;     // P.V column blocks of this wave
+  static_assert(SH::KSTEPS % NW == 0 && SH::CB % NW == 0, "narrow split");
+  extern __shared__ __attribute__((aligned(16))) char ring_raw[];
+  lds_char *ring = (lds_char *)ring_raw;
+  const uint32_t ring_u = lds_u32(ring);
+  const uint32_t red_u = ring_u + NSTAGE * SH::STAGE_BYTES;
+  const uint32_t pbuf_u = red_u + kNarrowRed;
+  const uint32_t xrow_u = pbuf_u + 32 * kPRow;  // [wave][32 rows] f32 exchange
+  const uint32_t flags_u = xrow_u + 4 * 32 * 4;  // NW words
+  lds_char *seg_lds = ring + (flags_u + 4 * NW - ring_u);
+  SegDesc *seg_list = (SegDesc *)seg_lds;
+  int32_t *seg_meta = (int32_t *)(seg_lds + kSegCap * sizeof(SegDesc));
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int n = lane & 31, half = lane >> 5;
+  const bool row_ok = n < rows;
+  const int row_c = row_ok ? n : rows - 1;
+  const int my_instr = (SH::INSTR - wave + NW - 1) / NW;
+  const uint32_t q_sign = scale_log2 < 0.f ? 0x80008000u : 0u;
+  const float sl2 = fabsf(scale_log2);
+
+  // S^T operand offsets (within a stage) of this wave's k-steps
+  uint32_t sa[KQ];
+#pragma unroll
+  for (int kk = 0; kk < KQ; ++kk) {
+    const int ks = wave * KQ + kk;
+    if (ks < SH::KV_STEPS) {
+      sa[kk] = SH::kv_row(n) + half * 16 + ks * 32;
+    } else {
+      const int rk = ks - SH::KV_STEPS;
+      sa[kk] = SH::KV_BYTES + n * (DR * 2) + (((2 * rk + half) ^ (n & (SH::RCH - 1))) * 16);
+    }
+  }
+  // V^T operand base of this wave's column blocks
+  uint32_t v_off;
+  {
+    const int g = lane >> 4, sl = lane & 15;
+    const int tok_a = (g >= 2 ? 4 : 0) + (sl >> 2);
+    const int col_in = (g & 1) * 16 + 4 * (sl & 3);
+    v_off = SH::kv_row(tok_a) + (col_in >> 3) * 16 + (col_in & 7) * 2 + wave * NCB * 64;
+  }
+  // P^T staging: B-operand chunk (k-step ks, half h) of row n at n*kPRow +
+  // ks*32 + h*16; this wave's softmax fills positions 4 (wave % 2) .. +3 of
+  // chunk (wave / 2, half).
+  const uint32_t p_wr = pbuf_u + n * kPRow + (wave >> 1) * 32 + half * 16 + (wave & 1) * 8;
+  const uint32_t p_rd = pbuf_u + n * kPRow + half * 16;
+  const uint32_t red_wr = red_u + (uint32_t)((wave * 4) * 64 + lane) * 16;
+  const uint32_t red_rd = red_u + (uint32_t)(wave * 64 + lane) * 16;  // + w * 4 * 64 * 16
+  const uint32_t v_kv = (lane / (SH::ROW_B / 16)) * (SH::W * 2) + (lane % (SH::ROW_B / 16)) * 16;
+  const WaveDma wd = wave_dma<SH, NW>(wave);
+  const uint32_t v_rope = (lane / SH::RCH) * (SH::W * 2) + SH::ROW_B +
+                          ((lane % SH::RCH) ^ ((lane / SH::RCH) & (SH::RCH - 1))) * 16;
+
+  int32_t next_seq = 0;
+  do {
+  plan_round<NW * 64>(lens, batch, next_seq, seg_tokens, (int32_t *)ring_raw, seg_list, seg_meta,
+                      seq_info);
+  const int32_t nseg = __builtin_amdgcn_readfirstlane(seg_meta[0]);
+  next_seq = __builtin_amdgcn_readfirstlane(seg_meta[1]);
+  for (int32_t si = 0; si < nseg; ++si) {
+    SegDesc sg;
+    {
+      const SegDesc d = seg_list[si];
+      sg.seq = __builtin_amdgcn_readfirstlane(d.seq);
+      sg.t0 = __builtin_amdgcn_readfirstlane(d.t0);
+      sg.t1 = __builtin_amdgcn_readfirstlane(d.t1);
+      sg.slot = __builtin_amdgcn_readfirstlane(d.slot);
+    }
+    const int64_t qrow_c = (int64_t)sg.seq * rows + row_c;
+    const uint8_t *seq_base = pool + offsets[sg.seq] * (int64_t)(SH::W * 2);
+    bf16x8_t qf[KQ];
+    const uint32_t keep = row_ok ? 0xffffffffu : 0u;
+#pragma unroll
+    for (int kk = 0; kk < KQ; ++kk) {
+      u32x4_t u = __builtin_bit_cast(
+          u32x4_t, load_q8<R, DR, QT>(q_lat, q_rope, qrow_c, (wave * KQ + kk) * 16 + half * 8));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) u[i] = (u[i] ^ q_sign) & keep;
+      qf[kk] = __builtin_bit_cast(bf16x8_t, u);
+    }
+    const int T = sg.t1 - sg.t0;
+    const int ntiles = (T + kTok - 1) / kTok;
+    auto stage = [&](int t) { return ring + (t % NSTAGE) * SH::STAGE_BYTES; };
+
+    floatx16_t o[NCB];
+    floatx16_t s;
+    float m_ref = 0.f, l_run, m_raw;
+    float m_init = -INFINITY;
+    for (;;) {
+#pragma unroll
+      for (int i = 0; i < NCB; ++i)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) o[i][j] = 0.f;
+      l_run = 0.f;
+      m_raw = -INFINITY;
+      if (lane == 0) ds_w32(flags_u + 4 * wave, 0u);
+#pragma unroll
+      for (int p = 0; p < NSTAGE - 1; ++p)
+        if (p < ntiles)
+          issue_any_tile<SH, NW>(seq_base, sg.t0 + p * kTok, sg.t1, stage(p), wave, lane, v_kv,
+                                 v_rope, wd);
+      for (int it = 0; it < ntiles; ++it) {
+        // tile it complete and visible; P.V of tile it-1 done everywhere
+        wait_tiles<SH, NW>(min(NSTAGE - 2, ntiles - 1 - it), my_instr);
+        wait_lgkm<0>();
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        const int nxt = it + NSTAGE - 1;
+        if (nxt < ntiles)
+          issue_any_tile<SH, NW>(seq_base, sg.t0 + nxt * kTok, sg.t1, stage(nxt), wave, lane, v_kv,
+                                 v_rope, wd);
+        const uint32_t st = lds_u32(stage(it));
+        // partial S^T over this wave's k-steps, to LDS by quarter
+        narrow_s_phase<KQ>(st, sa, qf, s);
+        red_write<0>(red_wr, s);
+        red_write<1>(red_wr + 1 * 64 * 16, s);
+        red_write<2>(red_wr + 2 * 64 * 16, s);
+        red_write<3>(red_wr + 3 * 64 * 16, s);
+        wait_lgkm<0>();
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        // full scores of accumulator elements 4 wave .. 4 wave + 3
+        float sc[4] = {0.f, 0.f, 0.f, 0.f};
+        {
+          // (read as floats: element-wise bit casts of a vector lane are
+          // avoided -- the compiler here returned lane 0 for them)
+          floatx4_t r[4];
+#pragma unroll
+          for (int w = 0; w < 4; ++w)
+            asm volatile("ds_read_b128 %0, %1" : "=v"(r[w]) : "v"(red_rd + w * 4 * 64 * 16));
+          wait_lgkm<0>();
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            asm volatile("" : "+v"(r[w]));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sc[e] += r[w][e];
+          }
+        }
+        const int valid = T - it * kTok;
+        const int tok0 = 8 * wave + 4 * half;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (tok0 + e < valid) mx = fmaxf(mx, sc[e]);
+        if (it == 0) {
+          // reference: the first tile's row maximum over all 32 tokens
+          const float mrow = xor32_max(mx);
+          if (half == 0) ds_w32(xrow_u + 4 * (wave * 32 + n), __builtin_bit_cast(uint32_t, mrow));
+          wait_lgkm<0>();
+          __builtin_amdgcn_s_barrier();
+          uint32_t xv[4];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) xv[w] = ds_r32(xrow_u + 4 * (w * 32 + n));
+          wait_lgkm<0>();
+          float mf = -INFINITY;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            arrived32(xv[w]);
+            mf = fmaxf(mf, __builtin_bit_cast(float, xv[w]));
+          }
+          m_ref = m_init == -INFINITY ? mf * sl2 : m_init;
+        }
+        m_raw = fmaxf(m_raw, mx);
+        float p[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[e], sl2, -m_ref));
+          p[e] = tok0 + e < valid ? p[e] : 0.f;
+        }
+        l_run += (p[0] + p[1]) + (p[2] + p[3]);
+        {
+          u32x2_t pw;
+          pw[0] = pack2_bf16(p[0], p[1]);
+          pw[1] = pack2_bf16(p[2], p[3]);
+          asm volatile("ds_write_b64 %0, %1" : : "v"(p_wr), "v"(pw));
+        }
+        wait_lgkm<0>();
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        // P.V of this wave's column blocks
+        {
+          const bf16x8_t b0 = ds_b128<0>(p_rd), b1 = ds_b128<32>(p_rd);
+          const uint32_t vb = st + v_off;
+          bf16x8_t va[2 * NCB];
+          [&]<int... J>(std::integer_sequence<int, J...>) {
+            ((va[J] = ds_tr2<(J / NCB) * SH::HI16 + (J % NCB) * 64, SH::HI8>(vb)), ...);
+          }(std::make_integer_sequence<int, 2 * NCB>{});
+          wait_lgkm<0>();
+          bf16x8_t bb[2] = {b0, b1};
+          arrived(bb[0]);
+          arrived(bb[1]);
+#pragma unroll
+          for (int j = 0; j < 2 * NCB; ++j) {
+            arrived(va[j]);
+            o[j % NCB] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[j], bb[j / NCB], o[j % NCB], 0, 0, 0);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // Overflow check: this wave's maximum against the reference.
+      const float m_seg = xor32_max(m_raw) * sl2;
+      const bool ovf = __ballot(m_seg > m_ref + kRefSlack) != 0;
+      if (ovf && lane == 0) ds_w32(flags_u + 4 * wave, 1u);
+      wait_lgkm<0>();
+      __builtin_amdgcn_s_barrier();
+      if (!any_flag<NW>(flags_u)) break;
+      // Rare: redo the segment with every row's true maximum.
+      {
+        const float mrow = xor32_max(m_raw);
+        if (half == 0) ds_w32(xrow_u + 4 * (wave * 32 + n), __builtin_bit_cast(uint32_t, mrow));
+        wait_lgkm<0>();
+        __builtin_amdgcn_s_barrier();
+        uint32_t xv[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) xv[w] = ds_r32(xrow_u + 4 * (w * 32 + n));
+        wait_lgkm<0>();
+        float mf = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          arrived32(xv[w]);
+          mf = fmaxf(mf, __builtin_bit_cast(float, xv[w]));
+        }
+        m_init = mf * sl2;
+      }
+      __builtin_amdgcn_s_barrier();  // every wave has read the flags and maxima
+    }
+    // the final P.V MFMAs complete before their accumulators are read
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+    // ---- finalise: row sums over the four waves' tokens
+    const int fl = vfresh(lane), fn = fl & 31, fh = fl >> 5;
+    const float lpart = xor32_sum(l_run);
+    if (fh == 0) ds_w32(xrow_u + 4 * (wave * 32 + fn), __builtin_bit_cast(uint32_t, lpart));
+    wait_lgkm<0>();
+    __builtin_amdgcn_s_barrier();
+    float l_row = 0.f;
+    {
+      uint32_t xv[4];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) xv[w] = ds_r32(xrow_u + 4 * (w * 32 + fn));
+      wait_lgkm<0>();
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        arrived32(xv[w]);
+        l_row += __builtin_bit_cast(float, xv[w]);
+      }
+    }
+    const int slot = sg.slot;
+    if (wave == 0 && fh == 0)
+      part_lse[(int64_t)slot * 32 + fn] = (m_ref + log2f(l_row)) * 0.69314718055994531f;
+    const float inv = 1.f / l_row;
+    float *blk = part_o + ((int64_t)slot * SH::CB) * 1024 + fl * 4;
+#pragma unroll
+    for (int i = 0; i < NCB; ++i) {
+      const int cb = wave * NCB + i;
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) {
+        floatx4_t v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = o[i][jq * 4 + e] * inv;
+        *reinterpret_cast<floatx4_t *>(blk + cb * 1024 + jq * 256) = v;
+      }
+    }
+    // xrow and the stages are rewritten by the next segment only after its
+    // first barrier
+    wait_lgkm<0>();
+    __builtin_amdgcn_s_barrier();
+  }
+  // the next planning round reuses the stage ring: every wave is done with it
+  __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
+  __builtin_amdgcn_s_barrier();
+  } while (next_seq < batch);
+}
+
+template <int R>
+qmla_status launch_merge(const DecodeArgs &a, hipStream_t stream) {
+  const int row_blocks = (a.rows + 31) / 32;
+  dim3 mgrid((unsigned)(a.batch * row_blocks), (R / 32 + 3) / 4);
+  k_decode_merge_frag<R><<<mgrid, dim3(256), 0, stream>>>(a.rows, row_blocks, a.seq_info,
+                                                          a.part_o, a.part_lse, a.out, a.out_lse);
+  QMLA_LAUNCH_CHECK("k_decode_merge_frag");
+  return QMLA_OK;
+}
+
 template <int R, int DR, int NW, int NSTAGE>
 qmla_status launch_shape(const DecodeArgs &a, hipStream_t stream) {
   const size_t lds = decode_lds_bytes<R, DR, NW, NSTAGE>();
   const int passes = (a.rows + NW * 32 - 1) / (NW * 32);
   dim3 grid(a.blocks, passes), block(NW * 64);
   const float sl2 = a.scale * 1.4426950408889634f;
-  const int32_t seg_tokens = decode_mfma_seg_tokens(a.rows);
+  const int32_t seg_tokens = decode_mfma_seg_tokens(a.rows, R, DR);
   const uint8_t *pool = static_cast<const uint8_t *>(a.cache->rows);
   if (a.q_dtype == QMLA_BF16) {
     auto k = k_decode_mfma<R, DR, NW, NSTAGE, uint16_t>;
@@ -858,16 +1201,37 @@ qmla_status launch_shape(const DecodeArgs &a, hipStream_t stream) {
                                     seg_tokens, a.seq_info, a.part_o, a.part_lse);
   }
   QMLA_LAUNCH_CHECK("k_decode_mfma");
-  const int row_blocks = (a.rows + 31) / 32;
-  dim3 mgrid((unsigned)(a.batch * row_blocks), (R / 32 + 3) / 4);
-  k_decode_merge_frag<R><<<mgrid, dim3(256), 0, stream>>>(a.rows, row_blocks, a.seq_info,
-                                                          a.part_o, a.part_lse, a.out, a.out_lse);
-  QMLA_LAUNCH_CHECK("k_decode_merge_frag");
-  return QMLA_OK;
+  return launch_merge<R>(a, stream);
+}
+
+template <int R, int DR>
+qmla_status launch_narrow(const DecodeArgs &a, hipStream_t stream) {
+  const size_t lds = narrow_lds_bytes<R, DR>();
+  dim3 grid(a.blocks, 1), block(256);
+  const float sl2 = a.scale * 1.4426950408889634f;
+  const int32_t seg_tokens = decode_mfma_seg_tokens(a.rows, R, DR);
+  const uint8_t *pool = static_cast<const uint8_t *>(a.cache->rows);
+  if (a.q_dtype == QMLA_BF16) {
+    auto k = k_decode_narrow<R, DR, uint16_t>;
+    QMLA_TRY(ensure_dynamic_lds((const void *)k, lds));
+    k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, a.cache->d_lens, a.batch,
+                                    (const uint16_t *)a.q_lat, (const uint16_t *)a.q_rope, a.rows,
+                                    sl2, seg_tokens, a.seq_info, a.part_o, a.part_lse);
+  } else {
+    auto k = k_decode_narrow<R, DR, float>;
+    QMLA_TRY(ensure_dynamic_lds((const void *)k, lds));
+    k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, a.cache->d_lens, a.batch,
+                                    (const float *)a.q_lat, (const float *)a.q_rope, a.rows, sl2,
+                                    seg_tokens, a.seq_info, a.part_o, a.part_lse);
+  }
+  QMLA_LAUNCH_CHECK("k_decode_narrow");
+  return launch_merge<R>(a, stream);
 }
 
 template <int R, int DR>
 qmla_status launch_dims(const DecodeArgs &a, hipStream_t stream) {
+  if constexpr (R == 512 && DR == 64)
+    if (decode_narrow_path(a.rows, R, DR)) return launch_narrow<R, DR>(a, stream);
   if (a.rows <= 32) return launch_shape<R, DR, 1, 3>(a, stream);
   if (a.rows <= 64) return launch_shape<R, DR, 2, 4>(a, stream);
   return launch_shape<R, DR, 4, 4>(a, stream);
@@ -880,12 +1244,26 @@ bool decode_mfma_supported(int32_t rows, int32_t r, int32_t dr) {
   return (r == 512 && dr == 64) || (r == 64 && dr == 16) || (r == 128 && dr == 32);
 }
 
-int decode_mfma_blocks_per_cu(int32_t rows) { return rows <= 64 ? 2 : 1; }
+// The narrow path (one 32-row block over all four SIMDs) serves r = 512 /
+// dr = 64 with at most 32 query rows; its 3-stage ring allows one block per
+// compute unit.
+bool decode_narrow_path(int32_t rows, int32_t r, int32_t dr) {
+  return rows <= 32 && r == 512 && dr == 64;
+}
+
+int decode_mfma_blocks_per_cu(int32_t rows, int32_t r, int32_t dr) {
+  if (decode_narrow_path(rows, r, dr)) return 1;
+  return rows <= 64 ? 2 : 1;
+}
 
 // Virtual tokens charged per sequence start in the split plan: the fixed
-// cost of a segment (Q load, prologue latency, l exchange, partial store),
-// ~32K clocks at 128 rows, over the loop's ~100 clocks per token.
-int32_t decode_mfma_seg_tokens(int32_t rows) { return rows > 64 ? 320 : 64; }
+// cost of a segment (Q load, prologue latency, l exchange, partial store)
+// over the loop's cost per token -- ~32K clocks over ~100 clocks per token
+// at 128 rows, ~8K clocks over ~35 for the narrow path.
+int32_t decode_mfma_seg_tokens(int32_t rows, int32_t r, int32_t dr) {
+  if (decode_narrow_path(rows, r, dr)) return 256;
+  return rows > 64 ? 320 : 64;
+}
 
 qmla_status launch_decode_mfma(const DecodeArgs &a, hipStream_t stream) {
   QMLA_REQUIRE(a.rows <= 65535 * 128, QMLA_ERR_SHAPE, "too many query rows");

@@ -97,8 +97,9 @@ qmla_status launch_decode_f32(const DecodeArgs &a, hipStream_t stream);
 qmla_status launch_decode_mfma(const DecodeArgs &a, hipStream_t stream);
 bool decode_mfma_supported(int32_t rows, int32_t r, int32_t dr);
 // Pieces per compute unit the MFMA decode kernel runs concurrently.
-int decode_mfma_blocks_per_cu(int32_t rows);
-int32_t decode_mfma_seg_tokens(int32_t rows);
+bool decode_narrow_path(int32_t rows, int32_t r, int32_t dr);
+int decode_mfma_blocks_per_cu(int32_t rows, int32_t r, int32_t dr);
+int32_t decode_mfma_seg_tokens(int32_t rows, int32_t r, int32_t dr);
 
 // Prefill attention (prefill_*.hip).
 qmla_status launch_prefill_f32(const qmla_prefill_dims &d, const float *q_nope,

@@ -96,6 +96,25 @@ def test_decode_bf16_rows_not_multiple_of_pass(qmla_gpu, rows_m):
         np.testing.assert_allclose(lse, rlse, atol=2e-2)
 
 
+@pytest.mark.parametrize("rows_m", [1, 7, 32])
+def test_decode_bf16_narrow_rows(qmla_gpu, rows_m):
+    """At most 32 query rows over kv_lora_rank 512 take the four-wave narrow
+    path (S^T split over the latent dims, P.V over the columns): partial
+    tiles, a one-token sequence, two split counts and a negative scale."""
+    q = qmla_gpu
+    lens = [1, 31, 33, 300, 1025, 64]
+    cache, rows, offs = make_cache(q, lens, 512, 64, q.BF16, 141)
+    ql, qr = O.normal((6, rows_m, 512), 142), O.normal((6, rows_m, 64), 143)
+    for scale in (0.09, -0.05):
+        ref, rlse = O.decode_absorbed(ql, qr, rows, offs, lens, scale)
+        for splits in (0, 9):
+            out, lse = run(q, cache, ql, qr, scale, splits=splits)
+            err = rel_err(out, ref)
+            print(f"rows={rows_m} scale={scale} splits={splits} rel_err={err:.2e}")
+            assert err < TOL_BF16
+            np.testing.assert_allclose(lse, rlse, atol=2e-2)
+
+
 def test_decode_bf16_v2lite_full(qmla_gpu):
     """C2: batch 32, 16 heads, 4096 cached + 1, bf16 cache, scale 1/sqrt(192)."""
     q = qmla_gpu
