@@ -448,9 +448,36 @@ struct SegDesc {
   int32_t seq, t0, t1, slot;
 };
 
-// Exclusive scan of a[0..n) in LDS by NT threads; returns the total.
+// Exclusive scan of a[0..n) in LDS; returns the total.  Up to 512 values
+// are scanned by wave 0 alone (lane-local runs, then a shuffle scan: one
+// barrier in all); longer arrays by all NT threads (log-step, two barriers
+// per step).
 template <int NT>
 __device__ int32_t lds_exscan(int32_t *a, int32_t n, int32_t *tmp) {
+  if (n <= 512) {
+    if (threadIdx.x < 64) {
+      const int lane = threadIdx.x;
+      const int per = (n + 63) / 64;
+      const int lo = min(n, lane * per), hi = min(n, lo + per);
+      int32_t local = 0;
+      for (int i = lo; i < hi; ++i) local += a[i];
+      int32_t incl = local;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int32_t v = __shfl_up(incl, off);
+        if (lane >= off) incl += v;
+      }
+      int32_t run = incl - local;
+      for (int i = lo; i < hi; ++i) {
+        const int32_t v = a[i];
+        a[i] = run;
+        run += v;
+      }
+      if (lane == 63) tmp[0] = incl;
+    }
+    __syncthreads();
+    return tmp[0];
+  }
   const int tid = threadIdx.x;
   const int per = (n + NT - 1) / NT;
   const int lo = min(n, tid * per), hi = min(n, lo + per);
@@ -610,6 +637,19 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
     }
     const int64_t qrow_c = (int64_t)sg.seq * rows + row_c;
     const uint8_t *seq_base = pool + offsets[sg.seq] * (int64_t)(SH::W * 2);
+    const int T = sg.t1 - sg.t0;
+    const int ntiles = (T + kTok - 1) / kTok;
+    auto stage = [&](int t) { return ring + (t % NSTAGE) * SH::STAGE_BYTES; };
+    // prologue: NSTAGE-1 tiles in flight (issued before the Q loads so the
+    // two latencies overlap; a restart issues them again)
+    auto prologue = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int p = 0; p < NSTAGE - 1; ++p)
+        if (p < ntiles)
+          issue_any_tile<SH, NW>(seq_base, sg.t0 + p * kTok, sg.t1, stage(p), wave, lane, v_kv,
+                                 v_rope, wd);
+    };
+    prologue();
 
     // Q fragment = B operand of S^T: dims kk*16 + 8*half .. +7 of this row.
     bf16x8_t qf[SH::KSTEPS];
@@ -622,10 +662,6 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
       for (int i = 0; i < 4; ++i) u[i] = (u[i] ^ q_sign) & keep;
       qf[kk] = __builtin_bit_cast(bf16x8_t, u);
     }
-
-    const int T = sg.t1 - sg.t0;
-    const int ntiles = (T + kTok - 1) / kTok;
-    auto stage = [&](int t) { return ring + (t % NSTAGE) * SH::STAGE_BYTES; };
 
     floatx16_t o[PS::NCB][PS::NRB];
     floatx16_t s;
@@ -642,12 +678,8 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
       l_run = 0.f;
       if (lane == 0) ds_w32(ovf_flags + 4 * wave, 0u);
 
-      // prologue: NSTAGE-1 tiles in flight, then S and softmax of tile 0
-#pragma unroll
-      for (int p = 0; p < NSTAGE - 1; ++p)
-        if (p < ntiles)
-          issue_any_tile<SH, NW>(seq_base, sg.t0 + p * kTok, sg.t1, stage(p), wave, lane, v_kv,
-                                 v_rope, wd);
+      // prologue in flight (re-issued on a restart), then S and softmax of tile 0
+      if (m_init != -INFINITY) prologue();
       wait_tiles<SH, NW>(min(NSTAGE - 2, ntiles - 1), my_instr);
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
@@ -850,10 +882,12 @@ __global__ __launch_bounds__(256) void k_decode_merge_frag(
 constexpr int kNarrowStages = 3;
 constexpr int kNarrowRed = 4 * 4 * 64 * 16;  // partial S^T: [wave][quarter][lane] x 16 B
 
-// Partial S^T of one tile over the KQ k-steps at per-lane stage offsets sa.
-template <int KQ>
+// Partial S^T of one tile over the KQ k-steps at per-lane stage offsets sa;
+// dma(kk) runs after MFMA kk (DMA slots spread under the MFMAs).
+template <int KQ, class DMAF>
 __device__ __forceinline__ void narrow_s_phase(uint32_t st, const uint32_t (&sa)[KQ],
-                                               const bf16x8_t (&qf)[KQ], floatx16_t &s) {
+                                               const bf16x8_t (&qf)[KQ], floatx16_t &s,
+                                               DMAF &&dma) {
   constexpr int D = KQ < 4 ? KQ : 4;
   bf16x8_t a[D + 1];
   [&]<int... K>(std::integer_sequence<int, K...>) {
@@ -867,6 +901,7 @@ __device__ __forceinline__ void narrow_s_phase(uint32_t st, const uint32_t (&sa)
         s = mfma_s_first(a[0], qf[0]);
       else
         mfma_s_acc(s, a[kk % (D + 1)], qf[kk]);
+      dma(kk);
       if constexpr (kk + D < KQ) a[(kk + D) % (D + 1)] = ds_b128<0>(st + sa[kk + D]);
     }(), ...);
   }(std::make_integer_sequence<int, KQ>{});
@@ -966,6 +1001,18 @@ __global__ __launch_bounds__(256) void k_decode_narrow(
     }
     const int64_t qrow_c = (int64_t)sg.seq * rows + row_c;
     const uint8_t *seq_base = pool + offsets[sg.seq] * (int64_t)(SH::W * 2);
+    const int T = sg.t1 - sg.t0;
+    const int ntiles = (T + kTok - 1) / kTok;
+    auto stage = [&](int t) { return ring + (t % NSTAGE) * SH::STAGE_BYTES; };
+    // prologue DMA before the Q loads (latencies overlap); re-issued on a restart
+    auto prologue = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int p = 0; p < NSTAGE - 1; ++p)
+        if (p < ntiles)
+          issue_any_tile<SH, NW>(seq_base, sg.t0 + p * kTok, sg.t1, stage(p), wave, lane, v_kv,
+                                 v_rope, wd);
+    };
+    prologue();
     bf16x8_t qf[KQ];
     const uint32_t keep = row_ok ? 0xffffffffu : 0u;
 #pragma unroll
@@ -976,10 +1023,6 @@ __global__ __launch_bounds__(256) void k_decode_narrow(
       for (int i = 0; i < 4; ++i) u[i] = (u[i] ^ q_sign) & keep;
       qf[kk] = __builtin_bit_cast(bf16x8_t, u);
     }
-    const int T = sg.t1 - sg.t0;
-    const int ntiles = (T + kTok - 1) / kTok;
-    auto stage = [&](int t) { return ring + (t % NSTAGE) * SH::STAGE_BYTES; };
-
     floatx16_t o[NCB];
     floatx16_t s;
     float m_ref = 0.f, l_run, m_raw;
@@ -992,24 +1035,30 @@ __global__ __launch_bounds__(256) void k_decode_narrow(
       l_run = 0.f;
       m_raw = -INFINITY;
       if (lane == 0) ds_w32(flags_u + 4 * wave, 0u);
-#pragma unroll
-      for (int p = 0; p < NSTAGE - 1; ++p)
-        if (p < ntiles)
-          issue_any_tile<SH, NW>(seq_base, sg.t0 + p * kTok, sg.t1, stage(p), wave, lane, v_kv,
-                                 v_rope, wd);
+      if (m_init != -INFINITY) prologue();
       for (int it = 0; it < ntiles; ++it) {
         // tile it complete and visible; P.V of tile it-1 done everywhere
         wait_tiles<SH, NW>(min(NSTAGE - 2, ntiles - 1 - it), my_instr);
         wait_lgkm<0>();
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
+        // DMA of tile nxt: a full tile's slots go under the S^T MFMAs, a
+        // partial (clamped) one is issued up front
         const int nxt = it + NSTAGE - 1;
-        if (nxt < ntiles)
+        const bool full_nxt = nxt < ntiles && (nxt + 1) * kTok <= T;
+        if (nxt < ntiles && !full_nxt)
           issue_any_tile<SH, NW>(seq_base, sg.t0 + nxt * kTok, sg.t1, stage(nxt), wave, lane, v_kv,
                                  v_rope, wd);
+        const FullTileDma fd{seq_base + (int64_t)(sg.t0 + nxt * kTok) * (SH::W * 2), stage(nxt),
+                             wave, v_kv, v_rope, wd};
         const uint32_t st = lds_u32(stage(it));
         // partial S^T over this wave's k-steps, to LDS by quarter
-        narrow_s_phase<KQ>(st, sa, qf, s);
+        narrow_s_phase<KQ>(st, sa, qf, s, [&](int kk) __attribute__((always_inline)) {
+          constexpr int MI = DmaSlots<SH, NW>::MI;
+#pragma unroll
+          for (int k = 0; k < MI; ++k)
+            if ((k * KQ) / MI == kk && full_nxt) issue_full_one<SH, NW>(fd, k);
+        });
         red_write<0>(red_wr, s);
         red_write<1>(red_wr + 1 * 64 * 16, s);
         red_write<2>(red_wr + 2 * 64 * 16, s);
