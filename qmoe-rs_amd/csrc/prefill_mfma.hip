@@ -44,8 +44,8 @@ constexpr int kPWaves = 8;      // two groups of four
 constexpr int kPDmaWaves = 4;   // group 1 issues every tile's DMA
 constexpr int kPRows = kPWaves * 32;
 constexpr int kPStages = 4;     // tile ring depth
-constexpr int kPAhead = 4;      // S^T operand reads issued ahead of their MFMAs
-constexpr int kPvAheadP = 3;    // V^T fragments issued ahead of their MFMAs
+constexpr int kPAhead = 5;      // S^T operand reads issued ahead of their MFMAs
+constexpr int kPvAheadP = 2;    // V^T fragments issued ahead of their MFMAs
 constexpr float kPSlack = 16.f;
 
 // One LDS region of a stage: 32 key rows of ROWB bytes, filled by 1 KB DMA
@@ -371,8 +371,9 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
   const int qt = causal ? n_qtiles - 1 - rank : rank;
   const int b = bh / d.heads, h = bh - b * d.heads;
   const int q0 = qt * kPRows;
-  // The two waves sharing a SIMD (w, w + 4) own adjacent 32-row blocks.
-  const int row_first = q0 + 32 * (2 * (wave & 3) + grp);
+  // The two waves sharing a SIMD (w, w + 4) own 32-row blocks r and 7 - r:
+  // on the causal diagonal every SIMD then keeps one busy wave to the end.
+  const int row_first = q0 + 32 * (grp == 0 ? (wave & 3) : 7 - (wave & 3));
 
   const int64_t bhq = (int64_t)bh * d.seq_q;
   const int64_t bhk = (int64_t)bh * d.seq_k;
