@@ -332,7 +332,7 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
     const uint16_t *__restrict__ q_nope, const uint16_t *__restrict__ q_rope,
     const uint16_t *__restrict__ k, const uint16_t *__restrict__ k_rope,
     const uint16_t *__restrict__ v, qmla_prefill_dims d, float scale_log2, int causal,
-    uint16_t *__restrict__ out, int n_qtiles) {
+    uint16_t *__restrict__ out, int n_qtiles, int pair_tiles) {
   using SH = PrefillShape<DN, DR, DV>;
   extern __shared__ __attribute__((aligned(16))) char pring_raw[];
   lds_char *ring = (lds_char *)pring_raw;
@@ -349,14 +349,18 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
   const float sl2 = fabsf(scale_log2);
 
   // Block order.  Query tiles are ranked by work (rank 0 = heaviest when
-  // causal) and issued rank pair by rank pair.  Within a pair, the two
-  // tiles of one (b, h) get block indices 8 apart: blocks are dealt to the
+  // causal).  Unpaired: rank by rank.  Paired (pair_tiles, when K/V exceed
+  // the Infinity Cache): rank pair by rank pair, and within a pair the two
+  // tiles of one (b, h) get block indices 8 apart -- blocks are dealt to the
   // 8 XCDs round-robin, so both land on the same XCD at nearly the same
   // time and the second one's K/V reads hit that XCD's L2.
   const int BH = d.batch * d.heads;
   const int L = blockIdx.x;
   int rank, bh;
-  if ((BH & 7) == 0 && L < 2 * BH * (n_qtiles >> 1)) {
+  if (!pair_tiles) {
+    rank = L / BH;
+    bh = L % BH;
+  } else if ((BH & 7) == 0 && L < 2 * BH * (n_qtiles >> 1)) {
     const int pr = L / (2 * BH), rem = L - pr * 2 * BH;
     const int x = rem & 7, r = rem >> 3;
     rank = 2 * pr + (r & 1);
@@ -577,10 +581,17 @@ qmla_status launch_prefill_shape(const qmla_prefill_dims &d, const uint16_t *q_n
   QMLA_REQUIRE(nblocks <= 0x7fffffff, QMLA_ERR_SHAPE, "too many query tiles");
   const size_t lds = (size_t)kPStages * SH::STAGE_BYTES + kPWaves * 4;
   static_assert((size_t)kPStages * SH::STAGE_BYTES + kPWaves * 4 <= 160 * 1024, "LDS");
+  // Pair the query tiles of each (b, h) on one XCD only when the K/V
+  // stream does not fit the 256 MB Infinity Cache (otherwise re-reads hit
+  // it anyway and the plain heaviest-first order balances better).
+  const int64_t kv_bytes = (int64_t)d.batch * d.heads * d.seq_k * (DN + DV) * 2 +
+                           (int64_t)d.batch * d.k_rope_heads * d.seq_k * DR * 2;
+  const int pair_tiles = n_qtiles > 1 && kv_bytes > ((int64_t)256 << 20) ? 1 : 0;
   auto kern = k_prefill_mfma<DN, DR, DV>;
   QMLA_TRY(ensure_dynamic_lds((const void *)kern, lds));
   kern<<<dim3((unsigned)nblocks), dim3(kPWaves * 64), lds, stream>>>(
-      q_nope, q_rope, k, k_rope, v, d, scale * 1.4426950408889634f, causal, out, n_qtiles);
+      q_nope, q_rope, k, k_rope, v, d, scale * 1.4426950408889634f, causal, out, n_qtiles,
+      pair_tiles);
   QMLA_LAUNCH_CHECK("k_prefill_mfma");
   return QMLA_OK;
 }
