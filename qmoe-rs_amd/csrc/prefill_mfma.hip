@@ -20,9 +20,11 @@
 // wave's MFMAs.  Group 1 runs one step behind group 0.
 //
 // The softmax keeps a lazy fixed reference per row (the first tile's
-// maximum; a block whose later scores exceed it by more than kPSlack redoes
-// its tiles with the true maximum), so the O^T accumulators are never
-// rescaled inside the loop.  Key tiles above a wave's causal horizon are
+// maximum; a block in which some probability exceeds kPOverflow redoes its
+// tiles with a reference at or above the true maximum), so the O^T
+// accumulators are never rescaled inside the loop.  Only the first tile
+// takes a maximum: later tiles are checked through the largest 16-key
+// partial sum of p, an upper bound of every p in it.  Key tiles above a wave's causal horizon are
 // skipped (exact: the reference's -1e18 mask gives exp() == 0); blocks are
 // issued heaviest first so the causal triangle balances across compute
 // units.
@@ -46,7 +48,7 @@ constexpr int kPRows = kPWaves * 32;
 constexpr int kPStages = 4;     // tile ring depth
 constexpr int kPAhead = 5;      // S^T operand reads issued ahead of their MFMAs
 constexpr int kPvAheadP = 2;    // V^T fragments issued ahead of their MFMAs
-constexpr float kPSlack = 16.f;
+constexpr float kPOverflow = 65536.f;  // largest p kept (2^16) before a restart
 
 // One LDS region of a stage: 32 key rows of ROWB bytes, filled by 1 KB DMA
 // instructions (RPI rows each).  Chunk positions are XOR-swizzled by row so
@@ -285,10 +287,12 @@ __device__ __forceinline__ float ptile_max(const floatx16_t &s, int key0, int ha
   return fmaxf(fmaxf(a, b), fmaxf(c, e));
 }
 
-// p = exp2(s * sl2 - m) as the two bf16 B-operand fragments; adds to l.
+// p = exp2(s * sl2 - m) as the two bf16 B-operand fragments; adds the
+// lane's 16-key sum to l and folds it into the running maximum tmax.
 template <bool MASK>
 __device__ __forceinline__ void ptile_p(const floatx16_t &s, float sl2, float m, int key0,
-                                        int half, int vis_lim, float &l, bf16x8_t (&pb)[2]) {
+                                        int half, int vis_lim, float &l, float &tmax,
+                                        bf16x8_t (&pb)[2]) {
   const int rel = MASK ? vfresh(key0 + 4 * half - vis_lim) : 0;
   float p[16];
 #pragma unroll
@@ -299,7 +303,9 @@ __device__ __forceinline__ void ptile_p(const floatx16_t &s, float sl2, float m,
   float q[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) q[i] = p[2 * i] + p[2 * i + 1];
-  l += ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
+  const float t = ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
+  l += t;
+  tmax = fmaxf(tmax, t);
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     u32x4_t pk;
@@ -433,7 +439,7 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
   floatx16_t o[SH::CB];
   floatx16_t s;
   bf16x8_t pb[2], pn[2];
-  float m_ref = -INFINITY, l_run, m_raw;
+  float m_ref = -INFINITY, l_run, t_max;
   float m_init = -INFINITY;
   const int nsteps = 2 * ntb + 3;
   for (;;) {
@@ -442,26 +448,25 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
 #pragma unroll
       for (int j = 0; j < 16; ++j) o[cb][j] = 0.f;
     l_run = 0.f;
-    m_raw = -INFINITY;
+    t_max = 0.f;
     if (lane == 0) ds_w32(ovf_flags + 4 * wave, 0u);
 
 #pragma unroll
     for (int p = 0; p < kPStages - 1; ++p)
       if (grp == 1 && p < ntb) pissue_tile<SH>(tile_dma(p), dw, voff);
 
-    // softmax of tile j (its S^T is in s) into pn
+    // softmax of tile j (its S^T is in s) into pn; tile 0 sets the
+    // reference (key 0 is visible to every row, so its maximum is finite)
     auto sm = [&](auto mask_c, int j) __attribute__((always_inline)) {
       constexpr bool MASK = decltype(mask_c)::value;
       const int key0 = j * kPKeys;
-      const float mr = ptile_max<MASK>(s, key0, half, vis_lim);
-      if (j == 0) {
-        // key 0 is visible to every row: the first tile's maximum is finite
-        m_raw = mr;
-        m_ref = m_init == -INFINITY ? xor32_max(mr) * sl2 : m_init;
-      } else {
-        m_raw = fmaxf(m_raw, mr);
-      }
-      ptile_p<MASK>(s, sl2, m_ref, key0, half, vis_lim, l_run, pn);
+      ptile_p<MASK>(s, sl2, m_ref, key0, half, vis_lim, l_run, t_max, pn);
+    };
+    auto sm0 = [&](auto mask_c) __attribute__((always_inline)) {
+      constexpr bool MASK = decltype(mask_c)::value;
+      const float mr = ptile_max<MASK>(s, 0, half, vis_lim);
+      m_ref = m_init == -INFINITY ? xor32_max(mr) * sl2 : m_init;
+      ptile_p<MASK>(s, sl2, m_ref, 0, half, vis_lim, l_run, t_max, pn);
     };
 
     // Step k: vmcnt wait (even k), barrier.  At odd steps k >= 3, group 1
@@ -497,9 +502,9 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
       ps_phase<SH>(la, stage_u(0), qf, s, false, PTileDma{}, dw, voff);
       head();
       if (jm == 0)
-        sm(std::true_type{}, 0);
+        sm0(std::true_type{});
       else
-        sm(std::false_type{}, 0);
+        sm0(std::false_type{});
       pb[0] = pn[0];
       pb[1] = pn[1];
       __builtin_amdgcn_sched_barrier(0);
@@ -529,8 +534,9 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
       dma_only();
     }
 
-    // Overflow check: each row's scaled maximum against its reference.
-    const bool ovf = ntw > 0 && xor32_max(m_raw) * sl2 > m_ref + kPSlack;
+    // Overflow check: some p of the row above kPOverflow.
+    const float t_row = xor32_max(t_max);
+    const bool ovf = ntw > 0 && t_row > kPOverflow;
     if (__ballot(ovf) != 0 && lane == 0) ds_w32(ovf_flags + 4 * wave, 1u);
     wait_lgkm<0>();
     __builtin_amdgcn_s_barrier();
@@ -545,9 +551,11 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
       any |= f[w];
     }
     if (__builtin_amdgcn_readfirstlane(any) == 0) break;
-    // Rare: redo the block's tiles with every row's true maximum.
+    // Rare: redo the block's tiles with a reference at or above every
+    // row's true maximum (each p <= its 16-key sum <= t_row), so no p of
+    // the second pass exceeds 1.
     __builtin_amdgcn_s_barrier();  // all waves have read the flags
-    m_init = xor32_max(m_raw) * sl2;
+    m_init = m_ref + log2f(t_row);
   }
   // the final P.V MFMAs complete before their accumulators are read
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");

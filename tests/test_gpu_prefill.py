@@ -97,6 +97,27 @@ def test_prefill_shapes_mla_dims(qmla_gpu, bf16, sq, sk, causal, krh):
     assert err < (TOL_BF16 if bf16 else TOL_F32)
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_bf16_growing_scores_restart(qmla_gpu, causal):
+    """Keys drift along a direction every query shares, so the scores grow
+    along the keys by up to ~60 bits beyond the first key tile's maximum --
+    far past the kernel's reference slack.  The block-restart path runs and
+    the result must still match the oracle."""
+    q = qmla_gpu
+    s = 600
+    arrs = inputs(1, 2, s, s, 128, 64, 128, 1, 400)
+    u = O.normal((128,), 450)
+    u /= np.linalg.norm(u)
+    arrs[0] += 2.0 * u
+    arrs[2] += np.linspace(0.0, 150.0, s, dtype=np.float32)[:, None] * u
+    out, used = gpu_prefill(q, arrs, 192 ** -0.5, causal, bf16=True)
+    ref = O.fused_prefill_attn(*[np.asarray(x) for x in used], 192 ** -0.5, causal)
+    err = rel_err(out, ref)
+    print(f"growing scores causal={causal} rel_err={err:.2e}")
+    assert np.isfinite(out).all()
+    assert err < TOL_BF16
+
+
 def test_rope_key_shared_equals_broadcast(qmla_gpu):
     """k_rope_heads = 1 (latent layout) == the reference's head-broadcast copy."""
     q = qmla_gpu
