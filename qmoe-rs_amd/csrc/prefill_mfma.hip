@@ -92,6 +92,10 @@ struct PrefillShape {
   static constexpr int STAGE_BYTES = KN::BYTES + KR::BYTES + VR::BYTES;
   static constexpr int INSTR = KN::INSTR + KR::INSTR + VR::INSTR;
   static constexpr int MI = (INSTR + kPDmaWaves - 1) / kPDmaWaves;  // DMA slots per wave
+  // every region boundary falls on a slot boundary: slot k's region is a
+  // compile-time fact, the same for every DMA wave
+  static constexpr bool EVEN = KN::INSTR % kPDmaWaves == 0 && KR::INSTR % kPDmaWaves == 0 &&
+                               VR::INSTR % kPDmaWaves == 0;
   static_assert(DN % 16 == 0 && DR % 16 == 0 && DV % 32 == 0 && DN >= 16 && DV >= 32, "dims");
   static_assert(MI * (kPStages - 1) < 64, "vmcnt range");
   static_assert(kPStages >= 4 && kPStages <= 7, "ring depth");
@@ -136,29 +140,41 @@ __device__ __forceinline__ uint32_t pslot_voff(int k, int wave, int lane) {
   return 0;
 }
 
-// DMA slot k of this wave for the tile in d (voff from pslot_voff).
-template <class SH>
-__device__ __forceinline__ void pissue_one(const PTileDma &d, int k, int wave, uint32_t voff) {
-  const int ins = k * kPDmaWaves + wave;
-  if (ins >= SH::INSTR) return;
+// DMA slot K of this wave for the tile in d (voff from pslot_voff).
+// CLAMP: rows past d.last re-load row d.last (the tile's last valid key);
+// a full tile (d.last >= 31) needs no clamp.
+template <class SH, int K, bool CLAMP>
+__device__ __forceinline__ void pissue_one(const PTileDma &d, int wave, uint32_t voff) {
   constexpr int E1 = SH::KN::INSTR, E2 = SH::KN::INSTR + SH::KR::INSTR;
+  constexpr int INS0 = K * kPDmaWaves;
+  const int ins = INS0 + wave;
+  if (!SH::EVEN && ins >= SH::INSTR) return;
   const uint32_t st = fresh(d.stage);
-  const int last = min(d.last, 31);
-  if (ins < E1) {
-    dma16(fresh(d.kn), clamp_row<SH::KN::ROWB>(voff, last), st + SH::KN_OFF + ins * 1024);
-  } else if (ins < E2) {
+  const int last = CLAMP ? min(d.last, 31) : 31;
+  auto cl = [&](auto rb) { return CLAMP ? clamp_row<decltype(rb)::value>(voff, last) : voff; };
+  if (SH::EVEN ? INS0 < E1 : ins < E1) {
+    dma16(fresh(d.kn), cl(std::integral_constant<int, SH::KN::ROWB>{}),
+          st + SH::KN_OFF + ins * 1024);
+  } else if (SH::EVEN ? INS0 < E2 : ins < E2) {
     if constexpr (SH::KR::INSTR > 0)
-      dma16(fresh(d.kr), clamp_row<SH::KR::ROWB>(voff, last), st + SH::KR_OFF + (ins - E1) * 1024);
+      dma16(fresh(d.kr), cl(std::integral_constant<int, SH::KR::ROWB>{}),
+            st + SH::KR_OFF + (ins - E1) * 1024);
   } else {
-    dma16(fresh(d.v), clamp_row<SH::VR::ROWB>(voff, last), st + SH::V_OFF + (ins - E2) * 1024);
+    dma16(fresh(d.v), cl(std::integral_constant<int, SH::VR::ROWB>{}),
+          st + SH::V_OFF + (ins - E2) * 1024);
   }
 }
 
+// Every slot of this wave for the tile in d, clamped unless it is full.
 template <class SH>
 __device__ __forceinline__ void pissue_tile(const PTileDma &d, int wave,
                                             const uint32_t (&voff)[SH::MI]) {
-#pragma unroll
-  for (int k = 0; k < SH::MI; ++k) pissue_one<SH>(d, k, wave, voff[k]);
+  [&]<int... K>(std::integer_sequence<int, K...>) {
+    if (d.last >= 31)
+      (pissue_one<SH, K, false>(d, wave, voff[K]), ...);
+    else
+      (pissue_one<SH, K, true>(d, wave, voff[K]), ...);
+  }(std::make_integer_sequence<int, SH::MI>{});
 }
 
 // Waits until at most k tiles (0 <= k <= kPStages - 2) of this wave's DMA
@@ -203,12 +219,12 @@ __device__ __forceinline__ PLane<SH> plane_offsets(int lane) {
 }
 
 // S^T of one tile for the wave's 32 rows: one chain of KSTEPS MFMAs into a
-// VGPR accumulator, operand reads kPAhead steps ahead.  With dma_on, the
-// wave's DMA slots of the tile in d are spread over the MFMAs.
-template <class SH>
+// VGPR accumulator, operand reads kPAhead steps ahead.  With DMA, the
+// wave's DMA slots of the full tile in d are spread over the MFMAs.
+template <class SH, bool DMA>
 __device__ __forceinline__ void ps_phase(const PLane<SH> &la, uint32_t st,
                                          const bf16x8_t (&qf)[SH::KSTEPS], floatx16_t &s,
-                                         bool dma_on, const PTileDma &d, int dw,
+                                         const PTileDma &d, int dw,
                                          const uint32_t (&voff)[SH::MI]) {
   constexpr int D = kPAhead < SH::KSTEPS ? kPAhead : SH::KSTEPS;
   bf16x8_t a[D + 1];
@@ -224,9 +240,12 @@ __device__ __forceinline__ void ps_phase(const PLane<SH> &la, uint32_t st,
         s = mfma_s_first(a[0], qf[0]);
       else
         mfma_s_acc(s, a[kk % (D + 1)], qf[kk]);
-#pragma unroll
-      for (int k = 0; k < SH::MI; ++k)
-        if ((k * SH::KSTEPS) / SH::MI == kk && dma_on) pissue_one<SH>(d, k, dw, voff[k]);
+      if constexpr (DMA)
+        [&]<int... M>(std::integer_sequence<int, M...>) {
+          ([&] {
+            if constexpr ((M * SH::KSTEPS) / SH::MI == kk) pissue_one<SH, M, false>(d, dw, voff[M]);
+          }(), ...);
+        }(std::make_integer_sequence<int, SH::MI>{});
       if constexpr (kk + D < SH::KSTEPS) a[(kk + D) % (D + 1)] = ds_b128<0>(st + la.s[kk + D]);
     }(), ...);
   }(std::make_integer_sequence<int, SH::KSTEPS>{});
@@ -455,18 +474,18 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
     for (int p = 0; p < kPStages - 1; ++p)
       if (grp == 1 && p < ntb) pissue_tile<SH>(tile_dma(p), dw, voff);
 
-    // softmax of tile j (its S^T is in s) into pn; tile 0 sets the
+    // softmax of tile j (its S^T is in s) into pout; tile 0 sets the
     // reference (key 0 is visible to every row, so its maximum is finite)
-    auto sm = [&](auto mask_c, int j) __attribute__((always_inline)) {
+    auto sm = [&](auto mask_c, int j, bf16x8_t (&pout)[2]) __attribute__((always_inline)) {
       constexpr bool MASK = decltype(mask_c)::value;
       const int key0 = j * kPKeys;
-      ptile_p<MASK>(s, sl2, m_ref, key0, half, vis_lim, l_run, t_max, pn);
+      ptile_p<MASK>(s, sl2, m_ref, key0, half, vis_lim, l_run, t_max, pout);
     };
     auto sm0 = [&](auto mask_c) __attribute__((always_inline)) {
       constexpr bool MASK = decltype(mask_c)::value;
       const float mr = ptile_max<MASK>(s, 0, half, vis_lim);
       m_ref = m_init == -INFINITY ? xor32_max(mr) * sl2 : m_init;
-      ptile_p<MASK>(s, sl2, m_ref, 0, half, vis_lim, l_run, t_max, pn);
+      ptile_p<MASK>(s, sl2, m_ref, 0, half, vis_lim, l_run, t_max, pb);
     };
 
     // Step k: vmcnt wait (even k), barrier.  At odd steps k >= 3, group 1
@@ -478,7 +497,11 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
         // tile k/2 complete (this wave's share); later tiles may stay in flight
         const int m = k >> 1;
         const int last = min(ntb - 1, max(kPStages - 2, m + kPStages - 3));
-        pwait_tiles<SH>(last - m, my_instr);
+        // steady state: kPStages - 3 whole tiles of MI slots (group 0 has none)
+        if (SH::EVEN && last - m == kPStages - 3)
+          wait_vmcnt<(kPStages - 3) * SH::MI>();
+        else
+          pwait_tiles<SH>(last - m, my_instr);
       }
       wait_lgkm<0>();
       __builtin_amdgcn_s_barrier();
@@ -499,30 +522,48 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
     if (grp == 1) head();  // group 1 starts one step late
     if (ntw > 0) {
       head();
-      ps_phase<SH>(la, stage_u(0), qf, s, false, PTileDma{}, dw, voff);
+      ps_phase<SH, false>(la, stage_u(0), qf, s, PTileDma{}, dw, voff);
       head();
       if (jm == 0)
         sm0(std::true_type{});
       else
         sm0(std::false_type{});
-      pb[0] = pn[0];
-      pb[1] = pn[1];
       __builtin_amdgcn_sched_barrier(0);
-      auto body = [&](auto mask_c, int j) __attribute__((always_inline)) {
+      // Local steps 2j, 2j + 1: S^T of tile j (with this step's DMA, if
+      // any), then the P.V of tile j - 1 (P^T in pin) with the softmax of
+      // tile j into pout.  A partial tile's DMA goes out before the S^T.
+      auto body = [&](auto mask_c, int j, bf16x8_t (&pin)[2], bf16x8_t (&pout)[2])
+                      __attribute__((always_inline)) {
         head();
         const int t = dma_tile();
-        ps_phase<SH>(la, stage_u(j), qf, s, t < ntb, tile_dma(t), dw, voff);
+        const PTileDma td = tile_dma(t);
+        if (t < ntb && td.last >= 31) {
+          ps_phase<SH, true>(la, stage_u(j), qf, s, td, dw, voff);
+        } else {
+          if (t < ntb) pissue_tile<SH>(td, dw, voff);
+          ps_phase<SH, false>(la, stage_u(j), qf, s, td, dw, voff);
+        }
         __builtin_amdgcn_sched_barrier(0);
         head();
-        ppv_phase<SH>(la, stage_u(j - 1), pb, o,
-                      [&]() __attribute__((always_inline)) { sm(mask_c, j); });
-        pb[0] = pn[0];
-        pb[1] = pn[1];
+        ppv_phase<SH>(la, stage_u(j - 1), pin, o,
+                      [&]() __attribute__((always_inline)) { sm(mask_c, j, pout); });
         __builtin_amdgcn_sched_barrier(0);
       };
-      int j = 1;
-      for (; j < jm; ++j) body(std::false_type{}, j);
-      for (; j < ntw; ++j) body(std::true_type{}, j);
+      // two tiles per trip, so the P^T fragments alternate between pb and
+      // pn without copies; after an odd tile count the last ones move to pb
+      auto run = [&](auto mask_c, int j, int jend) __attribute__((always_inline)) {
+        for (; j + 1 < jend; j += 2) {
+          body(mask_c, j, pb, pn);
+          body(mask_c, j + 1, pn, pb);
+        }
+        if (j < jend) {
+          body(mask_c, j, pb, pn);
+          pb[0] = pn[0];
+          pb[1] = pn[1];
+        }
+      };
+      run(std::false_type{}, 1, jm);
+      run(std::true_type{}, max(jm, 1), ntw);
       head();  // no S^T of tile ntw
       dma_only();
       head();
