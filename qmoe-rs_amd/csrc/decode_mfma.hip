@@ -267,54 +267,94 @@ __device__ __forceinline__ bf16x8_t v_frag(uint32_t vb) {
   return ds_tr2<ks * SH::HI16 + i * PS::CW * 64, SH::HI8>(vb);
 }
 
-template <class SH, class PS>
+// mid.part<j>() runs after the MFMAs of V^T fragment j (the softmax of the
+// next tile, spread over the MFMAs: this wave is alone on its SIMD, so its
+// VALU work hides only under its own MFMAs).
+// LDS read order of pv_phase: the P^T fragments of k-step 0 (NRB reads)
+// and V^T fragments 0 .. DA-1 (two reads each) up front; after the MFMAs of
+// fragment j, V^T fragment j + DA, and after those of fragment 0 the P^T
+// fragments of k-step 1 (first needed by fragment NCB).  wait_after(j) =
+// reads issued after the last one fragment j needs, at its wait.
+template <int NA, int DA, int NRB, int NCB>
+struct PvOrder {
+  static constexpr int issued_before(int j) {
+    int n = NRB + 2 * DA;
+    for (int i = 0; i < j; ++i) n += (i + DA < NA ? 2 : 0) + (i == 0 ? NRB : 0);
+    return n;
+  }
+  static constexpr int last_a(int j) { return j < DA ? NRB + 2 * j + 1 : issued_before(j - DA) + 1; }
+  static constexpr int last_p1() { return issued_before(0) + (DA < NA ? 2 : 0) + NRB - 1; }
+  static constexpr int wait_after(int j) {
+    int need = last_a(j);
+    if (j == 0 && NRB - 1 > need) need = NRB - 1;
+    if (j == NCB && last_p1() > need) need = last_p1();
+    return issued_before(j) - 1 - need;
+  }
+};
+
+// mid.part<j>() runs after the MFMAs of V^T fragment j (the softmax of the
+// next tile, spread over the MFMAs: this wave is alone on its SIMD, so its
+// VALU work hides only under its own MFMAs).
+template <class SH, class PS, class MID>
 __device__ __forceinline__ void pv_phase(const LaneAddr<SH> &la, const lds_char *st,
                                          uint32_t pbuf, int cw,
-                                         floatx16_t (&o)[PS::NCB][PS::NRB]) {
+                                         floatx16_t (&o)[PS::NCB][PS::NRB], MID &mid) {
   constexpr int NA = 2 * PS::NCB;  // V^T fragments (k-step, column block)
   constexpr int DA = kPvAhead < NA ? kPvAhead : NA;
+  using ORD = PvOrder<NA, DA, PS::NRB, PS::NCB>;
   const uint32_t vb = lds_u32(st) + la.v + cw * 64;
   const uint32_t pb = pbuf + la.p_rd;
   bf16x8_t b[2][PS::NRB], a[DA + 1];
-  [&]<int... R>(std::integer_sequence<int, R...>) {
-    ((b[0][R] = ds_b128<R * PS::RW * 32 * kPRow>(pb)), ...);
-    ((b[1][R] = ds_b128<R * PS::RW * 32 * kPRow + 32>(pb)), ...);
-  }(std::make_integer_sequence<int, PS::NRB>{});
+  auto read_p = [&](auto ks_c) __attribute__((always_inline)) {
+    constexpr int KS = decltype(ks_c)::value;
+    [&]<int... R>(std::integer_sequence<int, R...>) {
+      ((b[KS][R] = ds_b128<R * PS::RW * 32 * kPRow + KS * 32>(pb)), ...);
+    }(std::make_integer_sequence<int, PS::NRB>{});
+  };
+  read_p(std::integral_constant<int, 0>{});
   [&]<int... J>(std::integer_sequence<int, J...>) {
     ([&] { if constexpr (J < DA) a[J] = v_frag<SH, PS, J>(vb); }(), ...);
     ([&] {
       constexpr int j = J;
-      // two reads per V^T fragment issued after fragment j
-      constexpr int after = 2 * (j + DA - 1 < NA - 1 ? DA - 1 : NA - 1 - j);
+      constexpr int after = ORD::wait_after(j);
+      static_assert(after >= 0 && after <= 15, "lgkmcnt");
       wait_lgkm<after>();
       arrived(a[j % (DA + 1)]);
-      if constexpr (j == 0) {  // the P^T fragments were read before V^T fragment 0
+      if constexpr (j == 0 || j == PS::NCB) {
 #pragma unroll
-        for (int r = 0; r < PS::NRB; ++r) {
-          arrived(b[0][r]);
-          arrived(b[1][r]);
-        }
+        for (int r = 0; r < PS::NRB; ++r) arrived(b[j == 0 ? 0 : 1][r]);
       }
 #pragma unroll
       for (int r = 0; r < PS::NRB; ++r)
         o[j % PS::NCB][r] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
             a[j % (DA + 1)], b[j / PS::NCB][r], o[j % PS::NCB][r], 0, 0, 0);
+      mid.template part<j, NA>();
       if constexpr (j + DA < NA) a[(j + DA) % (DA + 1)] = v_frag<SH, PS, j + DA>(vb);
+      if constexpr (j == 0) read_p(std::integral_constant<int, 1>{});
+      __builtin_amdgcn_sched_barrier(0);
     }(), ...);
   }(std::make_integer_sequence<int, NA>{});
 }
 
+struct NoMid {
+  template <int J, int N>
+  __device__ __forceinline__ void part() {}
+};
+
 // Online softmax in the log2 domain with a lazy fixed reference.  The
 // reference m (scaled units) is the first tile's row maximum, or the one a
-// restart hands in, and then stays fixed: p = exp2(s * scale_log2 - m) <=
-// 2^kRefSlack as long as no later score exceeds m by more than kRefSlack.
-// Each lane tracks the raw maximum of every tile it sees; after the segment
-// the block checks it, and in the rare case of an overflow redoes the
-// segment with the true maximum as reference (see the kernel).  The O^T
+// restart hands in, and then stays fixed: p = exp2(s * scale_log2 - m).
+// Each lane tracks the largest 16-token partial sum of p it forms, an upper
+// bound of every p in it; after the segment the block checks it against
+// kOverflow, and in the rare case of an overflow redoes the segment with a
+// reference at or above the true maximum (see the kernel).  The O^T
 // accumulators are therefore only ever MFMA-accumulated, zeroed at a
 // segment start or read at the end -- never rescaled in registers, which
 // keeps all 256 of them in AGPRs -- and the per-tile softmax has no branch,
-// so the scheduler can spread it over the P.V MFMAs.
+// so it splits into pieces spread over the P.V MFMAs.
+constexpr float kOverflow = 65536.f;  // largest p kept (2^16) before a restart
+// The narrow kernel (4 scores per lane and tile) checks row maxima instead:
+// a score above m + kRefSlack restarts its segment.
 constexpr float kRefSlack = 16.f;
 
 // Token (within the tile) of S^T accumulator element j of this lane.
@@ -337,27 +377,48 @@ __device__ __forceinline__ float tile_max(const floatx16_t &s, int valid, int ha
 }
 
 // p = exp2(s * sl2 - m) packed into the two bf16 B-operand fragments of
-// P^T; adds the tile's probability mass to l.  sl2 >= 0.
+// P^T; adds the lane's 16-token mass to l and folds it into tmax.  sl2 >= 0.
+// part<I, N>() computes the I-th of N pieces: score pairs i with
+// i * N / 8 == I, and the totals with the last piece.
+template <bool MASK>
+struct TileSoftmax {
+  const floatx16_t &s;
+  float sl2, m;
+  int valid, half;
+  float &l, &tmax;
+  bf16x8_t (&pb)[2];
+  float q[8];
+  u32x4_t pk[2];
+
+  template <int I, int N>
+  __device__ __forceinline__ void part() {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i * N / 8 != I) continue;
+      float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * i], sl2, -m));
+      float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * i + 1], sl2, -m));
+      if (MASK) {
+        p0 = tile_tok(2 * i, half) < valid ? p0 : 0.f;
+        p1 = tile_tok(2 * i + 1, half) < valid ? p1 : 0.f;
+      }
+      q[i] = p0 + p1;
+      pk[i / 4][i % 4] = pack2_bf16(p0, p1);
+    }
+    if constexpr (I == N - 1) {
+      const float t = ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
+      l += t;
+      tmax = fmaxf(tmax, t);
+      pb[0] = __builtin_bit_cast(bf16x8_t, pk[0]);
+      pb[1] = __builtin_bit_cast(bf16x8_t, pk[1]);
+    }
+  }
+};
+
 template <bool MASK>
 __device__ __forceinline__ void tile_p(const floatx16_t &s, float sl2, float m, int valid,
-                                       int half, float &l, bf16x8_t (&pb)[2]) {
-  float p[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    p[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j], sl2, -m));
-    if (MASK) p[j] = tile_tok(j, half) < valid ? p[j] : 0.f;
-  }
-  float q[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) q[i] = p[2 * i] + p[2 * i + 1];
-  l += ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    u32x4_t pk;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pk[i] = pack2_bf16(p[ks * 8 + 2 * i], p[ks * 8 + 2 * i + 1]);
-    pb[ks] = __builtin_bit_cast(bf16x8_t, pk);
-  }
+                                       int half, float &l, float &tmax, bf16x8_t (&pb)[2]) {
+  TileSoftmax<MASK> t{s, sl2, m, valid, half, l, tmax, pb};
+  t.template part<0, 1>();
 }
 
 template <class SH, int NW>
@@ -666,7 +727,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
     floatx16_t o[PS::NCB][PS::NRB];
     floatx16_t s;
     bf16x8_t pn[2];
-    float m_run, l_run, m_raw;
+    float m_run, l_run, t_max;
     float m_init = -INFINITY;  // reference to (re)start the segment with
     for (;;) {
 #pragma unroll
@@ -684,9 +745,9 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
       s_phase<SH, NW, false>(la, stage(0), qf, s, FullTileDma{});
-      m_raw = tile_max<true>(s, T, half);
-      m_run = m_init == -INFINITY ? xor32_max(m_raw) * sl2 : m_init;
-      tile_p<true>(s, sl2, m_run, T, half, l_run, pn);
+      t_max = 0.f;
+      m_run = m_init == -INFINITY ? xor32_max(tile_max<true>(s, T, half)) * sl2 : m_init;
+      tile_p<true>(s, sl2, m_run, T, half, l_run, t_max, pn);
       __builtin_amdgcn_sched_barrier(0);
 
       // Steady state, iteration it: publish P of tile it, S^T of tile it+1,
@@ -722,9 +783,8 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         const int valid = T - (it + 1) * kTok;
-        m_raw = fmaxf(m_raw, tile_max<!FAST>(s, valid, half));
-        pv_phase<SH, PS>(la, stage(it), pbuf_u, cw, o);
-        tile_p<!FAST>(s, sl2, m_run, valid, half, l_run, pn);
+        TileSoftmax<!FAST> sm{s, sl2, m_run, valid, half, l_run, t_max, pn};
+        pv_phase<SH, PS>(la, stage(it), pbuf_u, cw, o, sm);
         __builtin_amdgcn_sched_barrier(0);
       };
       int it = 0;
@@ -736,11 +796,14 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
       p_write(la, pbuf_u, pn);
       __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
       __builtin_amdgcn_s_barrier();
-      pv_phase<SH, PS>(la, stage(ntiles - 1), pbuf_u, cw, o);
+      {
+        NoMid none;
+        pv_phase<SH, PS>(la, stage(ntiles - 1), pbuf_u, cw, o, none);
+      }
 
-      // Overflow check: the segment's scaled maximum against the reference.
-      const float m_seg = xor32_max(m_raw) * sl2;
-      const bool ovf = __ballot(m_seg > m_run + kRefSlack) != 0;  // every lane votes
+      // Overflow check: some p of the row above kOverflow.
+      const float t_row = xor32_max(t_max);
+      const bool ovf = __ballot(t_row > kOverflow) != 0;  // every lane votes
       if (ovf && lane == 0) ds_w32(ovf_flags + 4 * wave, 1u);
       // Every wave is done with the stages and the P^T rows (the next
       // segment's or attempt's prologue refills them) and every overflow
@@ -748,10 +811,11 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
       __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
       __builtin_amdgcn_s_barrier();
       if (!any_flag<NW>(ovf_flags)) break;
-      // Rare: some row's maximum outgrew the reference.  Redo the segment
-      // with its true maximum as reference (cannot overflow).
+      // Rare: some row's scores outgrew the reference.  Redo the segment
+      // with a reference at or above every row's true maximum (each p <=
+      // its 16-token sum <= t_row), so no p of the second pass exceeds 1.
       __builtin_amdgcn_s_barrier();  // all waves have read the flags
-      m_init = m_seg;
+      m_init = m_run + log2f(t_row);
     }
 
     // ---- finalise: denominators of this wave's rows, shared with the
@@ -1230,6 +1294,7 @@ qmla_status launch_merge(const DecodeArgs &a, hipStream_t stream) {
 
 template <int R, int DR, int NW, int NSTAGE>
 qmla_status launch_shape(const DecodeArgs &a, hipStream_t stream) {
+  static_assert(decode_lds_bytes<R, DR, NW, NSTAGE>() <= 160 * 1024, "LDS budget");
   const size_t lds = decode_lds_bytes<R, DR, NW, NSTAGE>();
   const int passes = (a.rows + NW * 32 - 1) / (NW * 32);
   dim3 grid(a.blocks, passes), block(NW * 64);
