@@ -172,6 +172,23 @@ QMLA_API qmla_status qmla_cache_set_lengths(qmla_kv_cache *cache, const int32_t 
 /* Length read (`cache.k.dim(2)`, src/model.rs:259) from the host mirror. */
 QMLA_API qmla_status qmla_cache_lengths(const qmla_kv_cache *cache, int32_t *lengths_out);
 QMLA_API qmla_status qmla_cache_describe(const qmla_kv_cache *cache, qmla_cache_desc *out);
+/* Capacity growth.  KVCache::append (src/model.rs:99-104) grows its tensors
+ * without bound; here growth is explicit, so that a caller that sized the
+ * cache up front keeps its pool (and pointers) fixed.
+ * qmla_cache_reserve raises sequence i's capacity to at least
+ * min_capacity[i] (host array [num_seqs]; smaller entries change nothing).
+ * The pool is re-laid out: live rows move to new offsets, so pointers from
+ * qmla_cache_describe are stale afterwards.  It synchronises `stream`; no
+ * work on another stream may use the cache meanwhile.  On failure the
+ * cache is unchanged.
+ * qmla_cache_set_growth(cache, 1): appends and the layer calls that would
+ * pass a sequence's capacity first grow it to max(needed, 2 x capacity, 16)
+ * instead of failing with QMLA_ERR_CAPACITY.  Off by default; clones
+ * inherit it.  qmla_cache_capacity reads the host mirror of the capacities. */
+QMLA_API qmla_status qmla_cache_reserve(qmla_kv_cache *cache, const int32_t *min_capacity,
+                               qmla_stream stream);
+QMLA_API qmla_status qmla_cache_set_growth(qmla_kv_cache *cache, int32_t enable);
+QMLA_API qmla_status qmla_cache_capacity(const qmla_kv_cache *cache, int32_t *capacity_out);
 
 /* ------------------------------------------- absorbed latent decode ------
  * The attention core of MlaAttention::forward_with_cache,
@@ -248,7 +265,11 @@ QMLA_API qmla_status qmla_layer_workspace_bytes(const qmla_layer *layer, const q
  * Appends the seq new latent rows of sequences 0..batch-1 to the cache
  * (positions continue from each sequence's current length, which must be
  * equal across the batch as in the reference's uniform KVCache), then
- * attends all cached + new tokens without a mask (as :297-302). */
+ * attends all cached + new tokens without a mask (as :297-302).
+ * f32 cache: f32 throughout.  bf16 cache: the new rows are stored rounded
+ * to bf16 and the attention core is the bf16 MFMA decode (kv_lora_rank /
+ * rope 512/64, 128/32 or 64/16; other shapes return QMLA_ERR_UNSUPPORTED);
+ * the projections stay f32. */
 QMLA_API qmla_status qmla_layer_forward_with_cache(const qmla_layer *layer, const float *xs, int32_t batch,
                                           int32_t seq, qmla_kv_cache *cache, float *out,
                                           void *workspace, size_t workspace_bytes,

@@ -6,8 +6,10 @@
 // token is one latent row [c_kv | k_pe] written once into a per-sequence
 // contiguous range of a single HBM pool; appends touch only the new rows.
 
+#include <algorithm>
 #include <cstring>
 #include <new>
+#include <vector>
 
 #include "internal.hpp"
 
@@ -56,9 +58,69 @@ qmla_status check_append(const qmla_kv_cache *c, int32_t seq0, int32_t n_seqs, i
   return QMLA_OK;
 }
 
+// Re-lays the pool out with capacities new_cap (each >= the old one): the
+// live rows [0, len) of every sequence move to its new offset.  On failure
+// the cache is left as it was.
+qmla_status regrow(qmla_kv_cache *c, const std::vector<int32_t> &new_cap, hipStream_t s) {
+  const size_t rb = c->row_bytes();
+  std::vector<int64_t> off(c->num_seqs);
+  int64_t total = 0;
+  for (int32_t i = 0; i < c->num_seqs; ++i) {
+    off[i] = total;
+    total += new_cap[i];
+  }
+  void *pool = nullptr;
+  QMLA_REQUIRE(hipMalloc(&pool, total > 0 ? (size_t)total * rb : 256) == hipSuccess, QMLA_ERR_OOM,
+               "cannot allocate a %lld-row pool", (long long)total);
+  auto bail = [&](const char *what) {
+    (void)hipStreamSynchronize(s);
+    (void)hipFree(pool);
+    return fail(QMLA_ERR_HIP, "%s failed while growing the cache", what);
+  };
+  char *dst = static_cast<char *>(pool);
+  const char *src = static_cast<const char *>(c->rows);
+  for (int32_t i = 0; i < c->num_seqs; ++i)
+    if (c->h_lens[i] > 0 &&
+        hipMemcpyAsync(dst + off[i] * rb, src + c->h_offsets[i] * rb, (size_t)c->h_lens[i] * rb,
+                       hipMemcpyDeviceToDevice, s) != hipSuccess)
+      return bail("row copy");
+  if (hipMemcpyAsync(c->d_offsets, off.data(), sizeof(int64_t) * c->num_seqs,
+                     hipMemcpyHostToDevice, s) != hipSuccess ||
+      hipMemcpyAsync(c->d_cap, new_cap.data(), sizeof(int32_t) * c->num_seqs,
+                     hipMemcpyHostToDevice, s) != hipSuccess)
+    return bail("table upload");
+  // the copies and uploads read host vectors and the old pool: finish them
+  if (hipStreamSynchronize(s) != hipSuccess) return bail("stream synchronize");
+  (void)hipFree(c->rows);
+  c->rows = pool;
+  c->h_offsets = off;
+  c->h_cap = new_cap;
+  c->total_rows = total;
+  return QMLA_OK;
+}
+
+qmla_status make_room(qmla_kv_cache *c, int32_t seq0, int32_t n_seqs, int32_t n_new,
+                      hipStream_t stream) {
+  if (c->grow && n_new > 0 && seq0 >= 0 && n_seqs >= 0 && seq0 + (int64_t)n_seqs <= c->num_seqs) {
+    std::vector<int32_t> cap = c->h_cap;
+    bool more = false;
+    for (int32_t i = seq0; i < seq0 + n_seqs; ++i) {
+      const int64_t need = (int64_t)c->h_lens[i] + n_new;
+      if (need <= cap[i]) continue;
+      QMLA_REQUIRE(need <= 0x7fffffff, QMLA_ERR_CAPACITY, "sequence %d: %lld rows", i,
+                   (long long)need);
+      cap[i] = (int32_t)std::min<int64_t>(0x7fffffff,
+                                          std::max<int64_t>({need, 2 * (int64_t)cap[i], 16}));
+      more = true;
+    }
+    if (more) QMLA_TRY(regrow(c, cap, stream));
+  }
+  return check_append(c, seq0, n_seqs, n_new);
+}
+
 qmla_status launch_cache_append(qmla_kv_cache *c, const void *rows, qmla_dtype rows_dtype,
                                 int32_t seq0, int32_t n_seqs, int32_t n_new, hipStream_t stream) {
-  QMLA_TRY(check_append(c, seq0, n_seqs, n_new));
+  QMLA_TRY(make_room(c, seq0, n_seqs, n_new, stream));
   int64_t nrows = (int64_t)n_seqs * n_new;
   if (nrows == 0) return QMLA_OK;
   QMLA_REQUIRE(rows != nullptr, QMLA_ERR_INVALID_ARG, "rows is NULL");
@@ -185,6 +247,7 @@ qmla_status qmla_cache_clone(const qmla_kv_cache *src, qmla_kv_cache **out, qmla
   c->h_offsets = src->h_offsets;
   c->h_lens = src->h_lens;
   c->h_cap = src->h_cap;
+  c->grow = src->grow;
   hipStream_t s = as_stream(stream);
   // Wait for pending work on src's stream before reading its rows.
   if (hipStreamSynchronize(s) != hipSuccess) {
@@ -241,6 +304,34 @@ qmla_status qmla_cache_set_lengths(qmla_kv_cache *cache, const int32_t *lengths,
 qmla_status qmla_cache_lengths(const qmla_kv_cache *cache, int32_t *lengths_out) {
   QMLA_REQUIRE(cache && lengths_out, QMLA_ERR_INVALID_ARG, "NULL pointer");
   std::memcpy(lengths_out, cache->h_lens.data(), sizeof(int32_t) * cache->num_seqs);
+  return QMLA_OK;
+}
+
+qmla_status qmla_cache_reserve(qmla_kv_cache *cache, const int32_t *min_capacity,
+                               qmla_stream stream) {
+  QMLA_REQUIRE(cache && min_capacity, QMLA_ERR_INVALID_ARG, "NULL pointer");
+  std::vector<int32_t> cap = cache->h_cap;
+  bool more = false;
+  for (int32_t i = 0; i < cache->num_seqs; ++i) {
+    QMLA_REQUIRE(min_capacity[i] >= 0, QMLA_ERR_SHAPE, "min_capacity[%d] = %d is negative", i,
+                 min_capacity[i]);
+    if (min_capacity[i] > cap[i]) {
+      cap[i] = min_capacity[i];
+      more = true;
+    }
+  }
+  return more ? regrow(cache, cap, as_stream(stream)) : QMLA_OK;
+}
+
+qmla_status qmla_cache_set_growth(qmla_kv_cache *cache, int32_t enable) {
+  QMLA_REQUIRE(cache, QMLA_ERR_INVALID_ARG, "cache is NULL");
+  cache->grow = enable != 0;
+  return QMLA_OK;
+}
+
+qmla_status qmla_cache_capacity(const qmla_kv_cache *cache, int32_t *capacity_out) {
+  QMLA_REQUIRE(cache && capacity_out, QMLA_ERR_INVALID_ARG, "NULL pointer");
+  std::memcpy(capacity_out, cache->h_cap.data(), sizeof(int32_t) * cache->num_seqs);
   return QMLA_OK;
 }
 

@@ -24,6 +24,7 @@ struct qmla_kv_cache {
   std::vector<int64_t> h_offsets;
   std::vector<int32_t> h_lens;
   std::vector<int32_t> h_cap;
+  bool grow = false;  // appends past capacity grow it instead of failing
 
   size_t elem_bytes() const { return dtype == QMLA_BF16 ? 2 : 4; }
   size_t row_bytes() const { return (size_t)row_elems * elem_bytes(); }
@@ -118,5 +119,9 @@ qmla_status launch_prefill_bf16(const qmla_prefill_dims &d, const uint16_t *q_no
 qmla_status launch_cache_append(qmla_kv_cache *cache, const void *rows, qmla_dtype rows_dtype,
                                 int32_t seq0, int32_t n_seqs, int32_t n_new, hipStream_t stream);
 qmla_status check_append(const qmla_kv_cache *cache, int32_t seq0, int32_t n_seqs, int32_t n_new);
+// check_append, after growing the sequences that need it when the cache's
+// growth mode is on.
+qmla_status make_room(qmla_kv_cache *cache, int32_t seq0, int32_t n_seqs, int32_t n_new,
+                      hipStream_t stream);
 
 }  // namespace qmla

@@ -417,9 +417,12 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
                                           void *workspace, size_t workspace_bytes,
                                           qmla_stream stream) {
   QMLA_TRY(check_layer_call(L, xs, batch, seq, cache, out));
-  QMLA_REQUIRE(cache->dtype == QMLA_F32, QMLA_ERR_UNSUPPORTED,
-               "the f32 layer needs an f32 latent cache");
-  QMLA_TRY(check_append(cache, 0, batch, seq));
+  // f32 cache: f32 decode core.  bf16 cache: the new rows are rounded to
+  // bf16 on append and the core is the bf16 MFMA decode (q rounded to bf16,
+  // f32 accumulation) for the latent shapes it serves.
+  QMLA_REQUIRE(cache->dtype == QMLA_F32 || cache->dtype == QMLA_BF16, QMLA_ERR_UNSUPPORTED,
+               "the layer needs an f32 or bf16 latent cache");
+  QMLA_TRY(make_room(cache, 0, batch, seq, as_stream(stream)));
   const auto &g = L->cfg;
   const int H = g.heads, dn = g.qk_nope, dr = g.qk_rope, dv = g.v_dim, r = g.kv_lora_rank;
   const size_t dec_bytes = decode_bytes_for(L, cache, batch, seq);
@@ -473,7 +476,7 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
   QMLA_REQUIRE(cache->h_lens[0] == 0, QMLA_ERR_SHAPE,
                "forward_prefill starts a sequence: cache lengths must be 0 (got %d)",
                cache->h_lens[0]);
-  QMLA_TRY(check_append(cache, 0, batch, seq));
+  QMLA_TRY(make_room(cache, 0, batch, seq, as_stream(stream)));
   const auto &g = L->cfg;
   const int H = g.heads, dn = g.qk_nope, dr = g.qk_rope, dv = g.v_dim, r = g.kv_lora_rank;
   const LayerWs w = layer_ws(L, cache, batch, seq, decode_bytes_for(L, cache, batch, seq));

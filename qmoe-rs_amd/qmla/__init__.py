@@ -96,6 +96,9 @@ SIGNATURES = {
     "qmla_cache_set_lengths": (_st, [_vp, C.POINTER(_i32), _vp]),
     "qmla_cache_lengths": (_st, [_vp, C.POINTER(_i32)]),
     "qmla_cache_describe": (_st, [_vp, C.POINTER(CacheDesc)]),
+    "qmla_cache_reserve": (_st, [_vp, C.POINTER(_i32), _vp]),
+    "qmla_cache_set_growth": (_st, [_vp, _i32]),
+    "qmla_cache_capacity": (_st, [_vp, C.POINTER(_i32)]),
     "qmla_decode_workspace_bytes": (_st, [C.POINTER(DecodeDims), _vp, C.POINTER(_sz)]),
     "qmla_decode_workspace_bytes_splits": (_st, [C.POINTER(DecodeDims), _vp, _i32, C.POINTER(_sz)]),
     "qmla_decode_absorbed": (_st, [C.POINTER(DecodeDims), _vp, _st, _vp, _vp, _d, _vp, _vp, _vp, _sz, _vp]),
@@ -261,7 +264,8 @@ def reference_eager_attn_numpy(q, k, v, scale: float, causal: bool, dtype: int =
 class KVCache:
     """Latent KV cache (replaces KVCache, src/model.rs:86-105)."""
 
-    def __init__(self, capacity, kv_lora_rank: int, rope_dim: int, dtype: int = BF16, _handle=None):
+    def __init__(self, capacity, kv_lora_rank: int, rope_dim: int, dtype: int = BF16, _handle=None,
+                 grow: bool = False):
         cap = np.ascontiguousarray(capacity, np.int32)
         self.num_seqs = int(cap.size)
         self.r, self.dr, self.dtype = kv_lora_rank, rope_dim, dtype
@@ -271,6 +275,21 @@ class KVCache:
                                           kv_lora_rank, rope_dim, dtype, C.byref(h)))
             _handle = h.value
         self.handle = _handle
+        if grow:
+            self.set_growth(True)
+
+    def reserve(self, min_capacity, stream=None):
+        """Grow capacities to at least min_capacity (Tensor::cat never runs out of room)."""
+        a = np.ascontiguousarray(min_capacity, np.int32)
+        check(lib().qmla_cache_reserve(self.handle, a.ctypes.data_as(C.POINTER(C.c_int32)), _sh(stream)))
+
+    def set_growth(self, enable: bool):
+        check(lib().qmla_cache_set_growth(self.handle, 1 if enable else 0))
+
+    def capacity(self) -> np.ndarray:
+        out = np.empty(self.num_seqs, np.int32)
+        check(lib().qmla_cache_capacity(self.handle, out.ctypes.data_as(C.POINTER(C.c_int32))))
+        return out
 
     def append(self, rows, n_seqs: int, n_new: int, rows_dtype: int = F32, stream=None):
         check(lib().qmla_cache_append(self.handle, _p(rows), rows_dtype, n_seqs, n_new, _sh(stream)))

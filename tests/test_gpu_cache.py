@@ -75,3 +75,59 @@ def test_clone_is_deep(qmla_gpu):
     assert list(c2.lengths()) == [3] and list(cache.lengths()) == [5]
     np.testing.assert_array_equal(c2.read_rows()[:3], bf16_bits(a[0]))
     np.testing.assert_array_equal(cache.read_rows()[:5], bf16_bits(np.concatenate([a[0], b[0]])))
+
+
+def _seq_rows(cache, i):
+    """Live rows of sequence i (host copy), wherever the pool holds them."""
+    pool, offs, lens = cache.read_rows(), cache.offsets(), cache.lengths()
+    return pool[offs[i]:offs[i] + lens[i]]
+
+
+def test_reserve_keeps_rows_and_moves_offsets(qmla_gpu):
+    q = qmla_gpu
+    cache = q.KVCache([3, 4, 2], 8, 8, q.BF16)
+    a = [O.normal((1, n, 16), 40 + i) for i, n in enumerate((3, 1, 2))]
+    for i, x in enumerate(a):
+        cache.append_seq(i, q.DeviceBuffer.from_numpy(x), x.shape[1])
+    cache.reserve([10, 2, 5])            # sequence 1 keeps its capacity of 4
+    assert list(cache.capacity()) == [10, 4, 5]
+    assert list(cache.offsets()) == [0, 10, 14]
+    assert list(cache.lengths()) == [3, 1, 2]
+    for i, x in enumerate(a):
+        np.testing.assert_array_equal(_seq_rows(cache, i), bf16_bits(x[0]))
+    more = O.normal((1, 7, 16), 50)
+    cache.append_seq(0, q.DeviceBuffer.from_numpy(more), 7)   # fits only after the reserve
+    np.testing.assert_array_equal(_seq_rows(cache, 0), bf16_bits(np.concatenate([a[0][0], more[0]])))
+    with pytest.raises(q.QmlaError) as e:
+        cache.reserve([-1, 0, 0])
+    assert e.value.status == 2
+    assert list(cache.capacity()) == [10, 4, 5]
+
+
+def test_growth_mode_append_never_runs_out(qmla_gpu):
+    """With growth on, appends behave like Tensor::cat (src/model.rs:99-104):
+    any number of rows fit, and decode over the grown cache matches the
+    oracle on the concatenated rows."""
+    q = qmla_gpu
+    cache = q.KVCache([2, 2], 64, 16, q.F32, grow=True)
+    chunks = [O.normal((2, n, 80), 60 + k) for k, n in enumerate((2, 5, 1, 30, 3))]
+    for x in chunks:
+        cache.append(q.DeviceBuffer.from_numpy(x), 2, x.shape[1])
+    full = np.concatenate(chunks, 1)
+    assert list(cache.lengths()) == [41, 41]
+    assert all(c >= 41 for c in cache.capacity())
+    for i in range(2):
+        np.testing.assert_array_equal(_seq_rows(cache, i), full[i])
+    c2 = cache.clone()                   # clones keep the growth mode
+    c2.append(q.DeviceBuffer.from_numpy(O.normal((2, 40, 80), 70)), 2, 40)
+    assert list(c2.lengths()) == [81, 81]
+    ql, qr = O.normal((2, 4, 64), 71), O.normal((2, 4, 16), 72)
+    out = q.DeviceBuffer(2 * 4 * 64 * 4)
+    ws_n = q.decode_workspace_bytes(cache, 2, 4)
+    ws = q.DeviceBuffer(ws_n)
+    q.decode_absorbed(cache, 2, 4, q.DeviceBuffer.from_numpy(ql), q.DeviceBuffer.from_numpy(qr), 0.2,
+                      out, workspace=ws, workspace_bytes=ws_n)
+    got = out.to_numpy(np.float32, (2, 4, 64))
+    ref, _ = O.decode_absorbed(ql, qr, full.reshape(-1, 80), np.array([0, 41], np.int64),
+                               np.array([41, 41], np.int32), 0.2)
+    assert np.abs(got - ref).max() / np.abs(ref).max() < 1e-4

@@ -88,3 +88,33 @@ def test_layer_argument_errors(qmla_gpu):
     with pytest.raises(q.QmlaError) as e:
         layer.forward_with_cache(O.normal((1, 1, 512), 1), wrong)
     assert e.value.status == 2
+
+
+@pytest.mark.parametrize("dims", [
+    # hidden, heads, qk_nope, qk_rope, v_dim, kv_lora_rank
+    (512, 8, 32, 16, 32, 64),      # the tiny CPU-path shape
+    (512, 16, 128, 64, 128, 512),  # V2-Lite head shape (hidden reduced)
+])
+def test_bf16_cache_prefill_then_decode(qmla_gpu, dims):
+    """forward_prefill then forward_with_cache steps over a bf16 latent
+    cache: the decode core is the bf16 MFMA kernel; the reference is the
+    oracle's f32 decompressed path on the same weights and inputs
+    (tolerance 2e-2)."""
+    q = qmla_gpu
+    hidden, H, dn, dr, dv, r = dims
+    w = O.MlaWeights.random(hidden, H, dn, dr, dv, r, seed=900 + r)
+    layer = q.MlaLayer(w)
+    b, s = 2, 45
+    xs = O.normal((b, s, hidden), 901)
+    cache = q.KVCache([s + 3] * b, r, dr, q.BF16)
+    out = layer.forward_prefill(xs, cache)
+    ref, (k, v, kr) = O.mla_forward_prefill(w, xs)
+    assert rel_err(out, ref) < 2e-2
+    for step in range(3):
+        x1 = O.normal((b, 1, hidden), 910 + step)
+        out1 = layer.forward_with_cache(x1, cache)
+        ref1, (k, v, kr) = O.mla_forward_with_cache(w, x1, k, v, kr, return_cache=True)
+        err = rel_err(out1, ref1)
+        print(f"dims={dims} step {step} rel_err={err:.2e}")
+        assert err < 2e-2
+    assert list(cache.lengths()) == [s + 3] * b
