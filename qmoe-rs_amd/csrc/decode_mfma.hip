@@ -896,7 +896,11 @@ __global__ __launch_bounds__(256) void k_decode_merge_frag(
 #pragma unroll
   for (int j = 0; j < 16; ++j) acc[j] = 0.f;
   float mx = -INFINITY, wsum = 0.f;
+  // unrolled so that several slots' loads are in flight at once (the
+  // trip count is small and the merge is latency-bound otherwise)
+#pragma unroll 4
   for (int k = 0; k < ns; ++k) mx = fmaxf(mx, part_lse[(int64_t)(sb + k) * rows_pad + row]);
+#pragma unroll 4
   for (int k = 0; k < ns; ++k) {
     const float w = expf(part_lse[(int64_t)(sb + k) * rows_pad + row] - mx);
     wsum += w;
