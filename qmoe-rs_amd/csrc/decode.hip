@@ -24,8 +24,6 @@ namespace qmla {
 namespace {
 
 constexpr int kPlanThreads = 1024;
-constexpr int32_t kMaxPlanBatch = 8192;
-constexpr int32_t kMaxPlanBlocks = 8192;
 
 // Exclusive scan of n ints held in LDS (in place); returns the total.
 // Every thread of the block must call it.

@@ -94,6 +94,9 @@ struct DecodeArgs {
   float *part_lse;
   int32_t blocks;
 };
+// Largest batch and piece count one decode call plans for.
+constexpr int32_t kMaxPlanBatch = 8192;
+constexpr int32_t kMaxPlanBlocks = 8192;
 qmla_status launch_decode_f32(const DecodeArgs &a, hipStream_t stream);
 qmla_status launch_decode_mfma(const DecodeArgs &a, hipStream_t stream);
 bool decode_mfma_supported(int32_t rows, int32_t r, int32_t dr);

@@ -20,8 +20,11 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <vector>
+
+#include <rocblas/rocblas.h>
 
 #include "internal.hpp"
 
@@ -31,6 +34,8 @@ struct qmla_layer {
         *ln_b = nullptr, *wkvb = nullptr, *bkvb = nullptr, *wo = nullptr, *bo = nullptr;
   float *inv_freq = nullptr;  // [dr / 2], src/model.rs:56-58
   std::vector<void *> allocs;
+  rocblas_handle blas = nullptr;
+  mutable std::mutex blas_mu;
 };
 
 namespace qmla {
@@ -38,9 +43,11 @@ namespace qmla {
 namespace {
 
 // ------------------------------------------------------------ f32 GEMM
+// The projections are plain GEMMs and go to rocBLAS (full f32: no reduced-
+// precision math mode is set on the handle).
 // C[z][m][n] = sum_k A[z][m][k] * B[z][k][n] (+ bias[z][n]); B is read as
-// B[k][n] = Bt[n][k] when TRANS_B (the Linear layout W[out][in]).
-// 64x64 tiles, 256 threads, 4x4 outputs per thread.
+// B[k][n] = Bt[n][k] when trans_b (the Linear layout W[out][in]).  All
+// matrices are row-major with leading dimensions ld* and per-z strides s*.
 struct GemmArgs {
   const float *A;
   const float *B;
@@ -51,85 +58,45 @@ struct GemmArgs {
   int64_t sA, sB, sC, sBias;  // per-z strides
 };
 
-template <bool TRANS_B>
-__global__ __launch_bounds__(256) void k_gemm_f32(GemmArgs g) {
-  __shared__ float As[16][64 + 4];
-  __shared__ float Bs[16][64 + 4];
-  const int z = blockIdx.z;
-  const float *A = g.A + z * g.sA;
-  const float *B = g.B + z * g.sB;
-  float *C = g.C + z * g.sC;
-  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
-  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-  float acc[4][4] = {};
-  for (int k0 = 0; k0 < g.K; k0 += 16) {
-    for (int e = tid; e < 16 * 64; e += 256) {
-      const int kk = e & 15, mm = e >> 4;
-      const int m = m0 + mm, k = k0 + kk;
-      As[kk][mm] = (m < g.M && k < g.K) ? A[m * g.lda + k] : 0.f;
-    }
-    for (int e = tid; e < 16 * 64; e += 256) {
-      float x;
-      int kk, nn;
-      if (TRANS_B) {
-        kk = e & 15;
-        nn = e >> 4;
-      } else {
-        nn = e & 63;
-        kk = e >> 6;
-      }
-      const int n = n0 + nn, k = k0 + kk;
-      if (n < g.N && k < g.K)
-        x = TRANS_B ? B[n * g.ldb + k] : B[k * g.ldb + n];
-      else
-        x = 0.f;
-      Bs[kk][nn] = x;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int kk = 0; kk < 16; ++kk) {
-      float a[4], b[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = As[kk][ty * 4 + i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx * 4 + j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
-    }
-    __syncthreads();
-  }
-  const float *bias = g.bias ? g.bias + z * g.sBias : nullptr;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = m0 + ty * 4 + i;
-    if (m >= g.M) continue;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = n0 + tx * 4 + j;
-      if (n < g.N) C[m * g.ldc + n] = acc[i][j] + (bias ? bias[n] : 0.f);
-    }
-  }
+// C[z][m][n] = bias[z][n], ahead of a GEMM that accumulates with beta = 1.
+__global__ __launch_bounds__(256) void k_bias_fill(float *__restrict__ C,
+                                                   const float *__restrict__ bias, int N,
+                                                   int64_t ldc, int64_t sC, int64_t sBias) {
+  const int z = blockIdx.z, m = blockIdx.y;
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  if (n < N) C[z * sC + m * ldc + n] = bias[z * sBias + n];
 }
 
-qmla_status gemm(const GemmArgs &g, int batch, bool trans_b, hipStream_t s) {
+// Row-major C = A op(B) is column-major C^T = op(B)^T A^T: rocBLAS gets
+// (m, n, k) = (N, M, K) with B as its first operand.
+qmla_status gemm(const qmla_layer *L, const GemmArgs &g, int batch, bool trans_b, hipStream_t s) {
   if (g.M == 0 || g.N == 0) return QMLA_OK;
-  dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, batch), block(256);
-  QMLA_REQUIRE(grid.y <= 65535 && batch <= 65535, QMLA_ERR_SHAPE, "GEMM too large");
-  if (trans_b)
-    k_gemm_f32<true><<<grid, block, 0, s>>>(g);
-  else
-    k_gemm_f32<false><<<grid, block, 0, s>>>(g);
-  QMLA_LAUNCH_CHECK("k_gemm_f32");
+  QMLA_REQUIRE(g.M <= 65535 && batch <= 65535, QMLA_ERR_SHAPE, "GEMM too large");
+  float beta = 0.f;
+  if (g.bias) {
+    dim3 grid((g.N + 255) / 256, g.M, batch);
+    k_bias_fill<<<grid, dim3(256), 0, s>>>(g.C, g.bias, g.N, g.ldc, g.sC, g.sBias);
+    QMLA_LAUNCH_CHECK("k_bias_fill");
+    beta = 1.f;
+  }
+  const float one = 1.f;
+  std::lock_guard<std::mutex> lock(L->blas_mu);  // the handle's stream is set per call
+  rocblas_status st = rocblas_set_stream(L->blas, s);
+  if (st == rocblas_status_success)
+    st = rocblas_sgemm_strided_batched(
+        L->blas, trans_b ? rocblas_operation_transpose : rocblas_operation_none,
+        rocblas_operation_none, g.N, g.M, g.K, &one, g.B, (rocblas_int)g.ldb, g.sB, g.A,
+        (rocblas_int)g.lda, g.sA, &beta, g.C, (rocblas_int)g.ldc, g.sC, batch);
+  QMLA_REQUIRE(st == rocblas_status_success, QMLA_ERR_HIP, "rocBLAS sgemm: %s",
+               rocblas_status_to_string(st));
   return QMLA_OK;
 }
 
 // y = x W^T + b for x [M, K], W [N, K] (candle_nn::Linear)
-qmla_status linear(const float *x, int M, int K, const float *W, const float *b, int N, float *y,
-                   hipStream_t s) {
+qmla_status linear(const qmla_layer *L, const float *x, int M, int K, const float *W,
+                   const float *b, int N, float *y, hipStream_t s) {
   GemmArgs g{x, W, b, y, M, N, K, K, K, N, 0, 0, 0, 0};
-  return gemm(g, 1, true, s);
+  return gemm(L, g, 1, true, s);
 }
 
 __device__ inline float block_sum(float v, float *red) {
@@ -291,20 +258,20 @@ qmla_status check_layer_call(const qmla_layer *L, const float *xs, int32_t batch
   return QMLA_OK;
 }
 
+// Decode workspace for the largest piece count the decode may choose
+// (device CUs x pieces per CU), so the size does not creep up with the
+// context and a caller can size the workspace once per (batch, seq).
 size_t decode_bytes_for(const qmla_layer *L, const qmla_kv_cache *c, int32_t batch,
                         int32_t seq) {
-  // Pieces are chosen from the lengths after the append; the decode call in
-  // forward_with_cache sees exactly these lengths.
-  int64_t total = 0;
-  for (int32_t i = 0; i < batch; ++i) total += c->h_lens[i] + seq;
   int cus = device_cu_count();
   if (cus <= 0) cus = 256;
-  int64_t blocks = std::max<int64_t>(1, std::min<int64_t>((int64_t)cus * 4, (total + 255) / 256));
-  (void)L;
-  const int32_t rows = seq * L->cfg.heads;
-  return std::max(
-      decode_workspace_layout(batch, rows, L->cfg.kv_lora_rank, (int32_t)blocks, false).total,
-      decode_workspace_layout(batch, rows, L->cfg.kv_lora_rank, (int32_t)blocks, true).total);
+  const int32_t rows = seq * L->cfg.heads, r = L->cfg.kv_lora_rank, dr = L->cfg.qk_rope;
+  const bool mfma = c->dtype == QMLA_BF16 && decode_mfma_supported(rows, r, dr);
+  const int per_cu = mfma ? decode_mfma_blocks_per_cu(rows, r, dr) : 4;
+  const int32_t blocks = (int32_t)std::min<int64_t>((int64_t)cus * per_cu, kMaxPlanBlocks);
+  (void)batch;
+  return std::max(decode_workspace_layout(batch, rows, r, blocks, false).total,
+                  decode_workspace_layout(batch, rows, r, blocks, true).total);
 }
 
 }  // namespace
@@ -343,6 +310,10 @@ qmla_status qmla_layer_create(const qmla_layer_config *cfg, const float *wq, con
   qmla_layer *L = new (std::nothrow) qmla_layer();
   QMLA_REQUIRE(L, QMLA_ERR_OOM, "host allocation failed");
   L->cfg = g;
+  if (rocblas_create_handle(&L->blas) != rocblas_status_success) {
+    delete L;
+    return fail(QMLA_ERR_HIP, "rocBLAS handle creation failed");
+  }
   const int H = g.heads;
   struct W {
     float **dst;
@@ -389,6 +360,7 @@ qmla_status qmla_layer_create(const qmla_layer_config *cfg, const float *wq, con
   }
   if (st != QMLA_OK) {
     for (void *p : L->allocs) (void)hipFree(p);
+    (void)rocblas_destroy_handle(L->blas);
     delete L;
     return st;
   }
@@ -399,6 +371,7 @@ qmla_status qmla_layer_create(const qmla_layer_config *cfg, const float *wq, con
 qmla_status qmla_layer_destroy(qmla_layer *layer) {
   if (!layer) return QMLA_OK;
   for (void *p : layer->allocs) (void)hipFree(p);
+  if (layer->blas) (void)rocblas_destroy_handle(layer->blas);
   delete layer;
   return QMLA_OK;
 }
@@ -437,8 +410,8 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
   const int n = batch * seq;
   const int pos0 = cache->h_lens[0];
 
-  QMLA_TRY(linear(xs, n, g.hidden, L->wq, L->bq, H * (dn + dr), q, s));
-  QMLA_TRY(linear(xs, n, g.hidden, L->wkva, L->bkva, r + dr, kva, s));
+  QMLA_TRY(linear(L, xs, n, g.hidden, L->wq, L->bq, H * (dn + dr), q, s));
+  QMLA_TRY(linear(L, xs, n, g.hidden, L->wkva, L->bkva, r + dr, kva, s));
   k_latent_rows<<<dim3(n), dim3(256), 0, s>>>(kva, seq, r, dr, L->ln_w, L->ln_b, (float)g.ln_eps,
                                               L->inv_freq, (float)g.rope_mscale, pos0, rows);
   QMLA_LAUNCH_CHECK("k_latent_rows");
@@ -449,7 +422,7 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
   {
     GemmArgs a{qn, L->wkvb, nullptr, qlat, n, r, dn, (int64_t)H * dn, r, (int64_t)H * r,
                dn, (int64_t)(dn + dv) * r, r, 0};
-    QMLA_TRY(gemm(a, H, false, s));
+    QMLA_TRY(gemm(L, a, H, false, s));
   }
   QMLA_TRY(launch_cache_append(cache, rows, QMLA_F32, 0, batch, seq, s));
   qmla_decode_dims dd{batch, seq * H, r, dr};
@@ -460,9 +433,9 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
     GemmArgs a{olat, L->wkvb + (size_t)dn * r, L->bkvb ? L->bkvb + dn : nullptr, o, n, dv, r,
                (int64_t)H * r, r, (int64_t)H * dv, r, (int64_t)(dn + dv) * r, dv,
                (int64_t)(dn + dv)};
-    QMLA_TRY(gemm(a, H, true, s));
+    QMLA_TRY(gemm(L, a, H, true, s));
   }
-  QMLA_TRY(linear(o, n, H * dv, L->wo, L->bo, g.hidden, out, s));
+  QMLA_TRY(linear(L, o, n, H * dv, L->wo, L->bo, g.hidden, out, s));
   return QMLA_OK;
 }
 
@@ -490,8 +463,8 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
   hipStream_t s = as_stream(stream);
   const int n = batch * seq;
 
-  QMLA_TRY(linear(xs, n, g.hidden, L->wq, L->bq, H * (dn + dr), q, s));
-  QMLA_TRY(linear(xs, n, g.hidden, L->wkva, L->bkva, r + dr, kva, s));
+  QMLA_TRY(linear(L, xs, n, g.hidden, L->wq, L->bq, H * (dn + dr), q, s));
+  QMLA_TRY(linear(L, xs, n, g.hidden, L->wkva, L->bkva, r + dr, kva, s));
   k_latent_rows<<<dim3(n), dim3(256), 0, s>>>(kva, seq, r, dr, L->ln_w, L->ln_b, (float)g.ln_eps,
                                               L->inv_freq, (float)g.rope_mscale, 0, rows);
   QMLA_LAUNCH_CHECK("k_latent_rows");
@@ -502,7 +475,7 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
   {
     GemmArgs a{rows, L->wkvb, L->bkvb, kvb, n, H * (dn + dv), r, r + dr, r, (int64_t)H * (dn + dv),
                0, 0, 0, 0};
-    QMLA_TRY(gemm(a, 1, true, s));
+    QMLA_TRY(gemm(L, a, 1, true, s));
   }
   k_split_kv<<<dim3(n, H), dim3(128), 0, s>>>(kvb, seq, H, dn, dv, k, v);
   QMLA_LAUNCH_CHECK("k_split_kv");
@@ -514,7 +487,7 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
   QMLA_TRY(launch_prefill_f32(pd, qn, qr, k, kr, v, (float)g.softmax_scale, 1, ctx, s));
   k_merge_heads<<<dim3(n, H), dim3(128), 0, s>>>(ctx, seq, H, dv, o);
   QMLA_LAUNCH_CHECK("k_merge_heads");
-  QMLA_TRY(linear(o, n, H * dv, L->wo, L->bo, g.hidden, out, s));
+  QMLA_TRY(linear(L, o, n, H * dv, L->wo, L->bo, g.hidden, out, s));
   // the latent replacement of the KVCache returned at src/model.rs:250
   QMLA_TRY(launch_cache_append(cache, rows, QMLA_F32, 0, batch, seq, s));
   return QMLA_OK;
