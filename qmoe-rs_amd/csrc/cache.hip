@@ -142,6 +142,11 @@ qmla_status launch_cache_append(qmla_kv_cache *c, const void *rows, qmla_dtype r
         c->row_elems);
   }
   QMLA_LAUNCH_CHECK("k_cache_append");
+  return cache_advance(c, seq0, n_seqs, n_new, stream);
+}
+
+qmla_status cache_advance(qmla_kv_cache *c, int32_t seq0, int32_t n_seqs, int32_t n_new,
+                          hipStream_t stream) {
   k_cache_advance<<<dim3((n_seqs + 255) / 256), dim3(256), 0, stream>>>(c->d_lens, seq0, n_seqs,
                                                                         n_new);
   QMLA_LAUNCH_CHECK("k_cache_advance");

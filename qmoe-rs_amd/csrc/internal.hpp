@@ -122,6 +122,10 @@ qmla_status launch_prefill_bf16(const qmla_prefill_dims &d, const uint16_t *q_no
 qmla_status launch_cache_append(qmla_kv_cache *cache, const void *rows, qmla_dtype rows_dtype,
                                 int32_t seq0, int32_t n_seqs, int32_t n_new, hipStream_t stream);
 qmla_status check_append(const qmla_kv_cache *cache, int32_t seq0, int32_t n_seqs, int32_t n_new);
+// Lengths of sequences seq0 .. seq0 + n_seqs - 1 grow by n_new (device
+// table in stream order, host mirror now), after their rows were written.
+qmla_status cache_advance(qmla_kv_cache *cache, int32_t seq0, int32_t n_seqs, int32_t n_new,
+                          hipStream_t stream);
 // check_append, after growing the sequences that need it when the cache's
 // growth mode is on.
 qmla_status make_room(qmla_kv_cache *cache, int32_t seq0, int32_t n_seqs, int32_t n_new,

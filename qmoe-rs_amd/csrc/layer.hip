@@ -110,20 +110,36 @@ __device__ inline float block_sum(float v, float *red) {
   return t;
 }
 
-// Latent rows of new tokens: one block per token (b, i).
-//   rows[b,i] = [LayerNorm(kva[b,i,:r]) | rope(kva[b,i,r:], pos0 + i)]
-// LayerNorm as candle_nn::LayerNorm (src/model.rs:136): mean, biased
-// variance of the centred values, divide by sqrt(var + eps), weight, bias.
+// Latent rows of new tokens, written straight into the cache (the append of
+// src/model.rs:99-104 fused in): one block per token (b, i),
+//   row = [LayerNorm(kva[b,i,:r]) | rope(kva[b,i,r:], pos0 + i)]
+// goes to pool row offsets[b] + lens[b] + i in the cache dtype (bf16 by
+// round-to-nearest-even), and, when `rows` is not NULL, to rows[b,i] in f32.
+// The lengths advance afterwards (k_cache_advance).  LayerNorm as
+// candle_nn::LayerNorm (src/model.rs:136): mean, biased variance of the
+// centred values, divide by sqrt(var + eps), weight, bias.
+template <typename DstT>
 __global__ __launch_bounds__(256) void k_latent_rows(const float *__restrict__ kva, int s, int r,
                                                      int dr, const float *__restrict__ ln_w,
                                                      const float *__restrict__ ln_b, float eps,
                                                      const float *__restrict__ inv_freq,
                                                      float mscale, int pos0,
-                                                     float *__restrict__ rows) {
+                                                     float *__restrict__ rows,
+                                                     DstT *__restrict__ pool,
+                                                     const int64_t *__restrict__ offsets,
+                                                     const int32_t *__restrict__ lens) {
   __shared__ float red[8];
-  const int tok = blockIdx.x, i = tok % s;
+  const int tok = blockIdx.x, b = tok / s, i = tok % s;
   const float *x = kva + (int64_t)tok * (r + dr);
-  float *y = rows + (int64_t)tok * (r + dr);
+  float *y = rows ? rows + (int64_t)tok * (r + dr) : nullptr;
+  DstT *dst = pool + (offsets[b] + lens[b] + i) * (int64_t)(r + dr);
+  auto put = [&](int c, float v) {
+    if (y) y[c] = v;
+    if constexpr (sizeof(DstT) == 2)
+      dst[c] = f32_to_bf16_bits(v);
+    else
+      dst[c] = v;
+  };
   float sum = 0.f;
   for (int c = threadIdx.x; c < r; c += blockDim.x) sum += x[c];
   const float mean = block_sum(sum, red) / (float)r;
@@ -136,16 +152,34 @@ __global__ __launch_bounds__(256) void k_latent_rows(const float *__restrict__ k
   const float den = sqrtf(var + eps);
   for (int c = threadIdx.x; c < r; c += blockDim.x) {
     const float t = (x[c] - mean) / den * ln_w[c];
-    y[c] = ln_b ? t + ln_b[c] : t;
+    put(c, ln_b ? t + ln_b[c] : t);
   }
   const float pos = (float)(pos0 + i);
   for (int p = threadIdx.x; p < dr / 2; p += blockDim.x) {
     const float ang = pos * inv_freq[p];
     const float cs = cosf(ang) * mscale, sn = sinf(ang) * mscale;
     const float e = x[r + 2 * p], o = x[r + 2 * p + 1];
-    y[r + 2 * p] = e * cs - o * sn;
-    y[r + 2 * p + 1] = o * cs + e * sn;
+    put(r + 2 * p, e * cs - o * sn);
+    put(r + 2 * p + 1, o * cs + e * sn);
   }
+}
+
+// LayerNorm + RoPE of the n new tokens into the cache, then the lengths
+// advance (the cache call checked the room already).
+qmla_status latent_to_cache(const qmla_layer *L, const float *kva, int batch, int seq, int pos0,
+                            float *rows, qmla_kv_cache *cache, hipStream_t s) {
+  const auto &g = L->cfg;
+  const int n = batch * seq;
+  if (cache->dtype == QMLA_BF16)
+    k_latent_rows<uint16_t><<<dim3(n), dim3(256), 0, s>>>(
+        kva, seq, g.kv_lora_rank, g.qk_rope, L->ln_w, L->ln_b, (float)g.ln_eps, L->inv_freq,
+        (float)g.rope_mscale, pos0, rows, (uint16_t *)cache->rows, cache->d_offsets, cache->d_lens);
+  else
+    k_latent_rows<float><<<dim3(n), dim3(256), 0, s>>>(
+        kva, seq, g.kv_lora_rank, g.qk_rope, L->ln_w, L->ln_b, (float)g.ln_eps, L->inv_freq,
+        (float)g.rope_mscale, pos0, rows, (float *)cache->rows, cache->d_offsets, cache->d_lens);
+  QMLA_LAUNCH_CHECK("k_latent_rows");
+  return cache_advance(cache, 0, batch, seq, s);
 }
 
 // Split q [b*s, H, dn+dr] into q_nope and roped q_rope (src/model.rs:263-267
@@ -403,7 +437,7 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
   QMLA_REQUIRE(workspace && workspace_bytes >= w.total, QMLA_ERR_WORKSPACE,
                "workspace of %zu bytes < required %zu", workspace_bytes, w.total);
   char *ws = static_cast<char *>(workspace);
-  float *q = (float *)(ws + w.q), *kva = (float *)(ws + w.kva), *rows = (float *)(ws + w.rows);
+  float *q = (float *)(ws + w.q), *kva = (float *)(ws + w.kva);
   float *qn = (float *)(ws + w.qn), *qr = (float *)(ws + w.qr), *qlat = (float *)(ws + w.qlat);
   float *olat = (float *)(ws + w.olat), *o = (float *)(ws + w.o);
   hipStream_t s = as_stream(stream);
@@ -412,9 +446,7 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
 
   QMLA_TRY(linear(L, xs, n, g.hidden, L->wq, L->bq, H * (dn + dr), q, s));
   QMLA_TRY(linear(L, xs, n, g.hidden, L->wkva, L->bkva, r + dr, kva, s));
-  k_latent_rows<<<dim3(n), dim3(256), 0, s>>>(kva, seq, r, dr, L->ln_w, L->ln_b, (float)g.ln_eps,
-                                              L->inv_freq, (float)g.rope_mscale, pos0, rows);
-  QMLA_LAUNCH_CHECK("k_latent_rows");
+  QMLA_TRY(latent_to_cache(L, kva, batch, seq, pos0, nullptr, cache, s));
   k_split_rope_q<<<dim3(n, H), dim3(64), 0, s>>>(q, seq, H, dn, dr, L->inv_freq,
                                                 (float)g.rope_mscale, pos0, 0, qn, qr);
   QMLA_LAUNCH_CHECK("k_split_rope_q");
@@ -424,7 +456,6 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
                dn, (int64_t)(dn + dv) * r, r, 0};
     QMLA_TRY(gemm(L, a, H, false, s));
   }
-  QMLA_TRY(launch_cache_append(cache, rows, QMLA_F32, 0, batch, seq, s));
   qmla_decode_dims dd{batch, seq * H, r, dr};
   QMLA_TRY(qmla_decode_absorbed(&dd, cache, QMLA_F32, qlat, qr, g.softmax_scale, olat, nullptr,
                                 ws + w.dec, dec_bytes, stream));
@@ -465,9 +496,9 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
 
   QMLA_TRY(linear(L, xs, n, g.hidden, L->wq, L->bq, H * (dn + dr), q, s));
   QMLA_TRY(linear(L, xs, n, g.hidden, L->wkva, L->bkva, r + dr, kva, s));
-  k_latent_rows<<<dim3(n), dim3(256), 0, s>>>(kva, seq, r, dr, L->ln_w, L->ln_b, (float)g.ln_eps,
-                                              L->inv_freq, (float)g.rope_mscale, 0, rows);
-  QMLA_LAUNCH_CHECK("k_latent_rows");
+  // the latent replacement of the KVCache returned at src/model.rs:250 (the
+  // f32 rows also feed compute_kv below)
+  QMLA_TRY(latent_to_cache(L, kva, batch, seq, 0, rows, cache, s));
   k_split_rope_q<<<dim3(n, H), dim3(64), 0, s>>>(q, seq, H, dn, dr, L->inv_freq,
                                                 (float)g.rope_mscale, 0, 1, qn, qr);
   QMLA_LAUNCH_CHECK("k_split_rope_q");
@@ -488,8 +519,6 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
   k_merge_heads<<<dim3(n, H), dim3(128), 0, s>>>(ctx, seq, H, dv, o);
   QMLA_LAUNCH_CHECK("k_merge_heads");
   QMLA_TRY(linear(L, o, n, H * dv, L->wo, L->bo, g.hidden, out, s));
-  // the latent replacement of the KVCache returned at src/model.rs:250
-  QMLA_TRY(launch_cache_append(cache, rows, QMLA_F32, 0, batch, seq, s));
   return QMLA_OK;
 }
 
