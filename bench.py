@@ -16,7 +16,9 @@ Secondary lines (same JSON object, "secondary"): 16-head decode (batch 32,
 4096 + 1 tokens), causal prefill (batch 4, 2048 tokens, 16 heads) and chunked
 prefill (batch 8, 8192 cached + 512 new, 128 heads), the prefills in TFLOP/s
 of unmasked attention work (MHA form, dqk 192 + dv 128) against the
-2.5 PFLOP/s bf16 dense peak.
+2.5 PFLOP/s bf16 dense peak; and one full MLA layer decode step
+(forward_with_cache: projections, latent append, decode core, W_UV, o_proj)
+at V2-Lite head shapes, in tokens/s and weight + cache bytes per step.
 
 Inputs are generated on the device (seeded) before the timed region.  The
 decode caches rotate over replicas totalling >= 2 GB so consecutive steps
@@ -35,6 +37,7 @@ import math
 import os
 import sys
 import time
+import types
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "qmoe-rs_amd"))
@@ -166,6 +169,60 @@ class PrefillBench:
                 "wall_ms_per_step": wall, "gflop_per_step": self.flops / 1e9}
 
 
+class LayerDecodeBench:
+    """MlaAttention::forward_with_cache (src/model.rs:256-307), one new token
+    per sequence: f32 projections, LayerNorm + RoPE of the new latent rows
+    into a bf16 latent cache, the absorbed decode core, W_UV and o_proj.
+    V2-Lite head shapes (hidden 2048, 16 heads, dn 128, dr 64, dv 128,
+    r 512), batch 32, 4096 cached tokens per sequence (the cache grows by one
+    token per step); weights N(0, 0.02^2), activations N(0, 1), seeded."""
+
+    def __init__(self, stream, seed, batch=32, ctx=4096, hidden=2048, heads=16):
+        rng = np.random.default_rng(seed)
+        H, dn, dr, dv, r = heads, 128, 64, 128, 512
+
+        def nrm(*shape):
+            return (rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+
+        w = types.SimpleNamespace(hidden=hidden, heads=H, dn=dn, dr=dr, dv=dv, r=r, softmax_scale=None)
+        w.wq, w.bq = nrm(H * (dn + dr), hidden), nrm(H * (dn + dr))
+        w.wkva, w.bkva = nrm(r + dr, hidden), nrm(r + dr)
+        w.ln_w, w.ln_b = (1.0 + nrm(r)).astype(np.float32), nrm(r)
+        w.wkvb, w.bkvb = nrm(H * (dn + dv), r), nrm(H * (dn + dv))
+        w.wo, w.bo = nrm(hidden, H * dv), nrm(hidden)
+        self.layer = qmla.MlaLayer(w)
+        self.weight_bytes = 4 * (w.wq.size + w.wkva.size + w.wkvb.size + w.wo.size)
+        self.batch, self.ctx, self.stream = batch, ctx, stream
+        self.cache = qmla.KVCache([ctx + 512] * batch, r, dr, qmla.BF16)
+        tmp = qmla.DeviceBuffer(64 << 20)
+        fill_bf16(self.cache.describe().rows, batch * (ctx + 512) * ROW_ELEMS, seed + 1, tmp, stream)
+        stream.sync()
+        tmp.free()
+        self.cache.set_lengths([ctx] * batch, stream)
+        self.xs = qmla.DeviceBuffer(batch * hidden * 4)
+        qmla.check(qmla.lib().qmla_fill_normal_f32(self.xs.ptr, batch * hidden, seed + 2, 0.0, 1.0,
+                                                   qmla._sh(stream)))
+        self.out = qmla.DeviceBuffer(batch * hidden * 4)
+        self.ws_bytes = self.layer.workspace_bytes(self.cache, batch, 1)
+        self.ws = qmla.DeviceBuffer(self.ws_bytes)
+        stream.sync()
+
+    def step(self, i):
+        qmla.check(qmla.lib().qmla_layer_forward_with_cache(
+            self.layer.handle, self.xs.ptr, self.batch, 1, self.cache.handle, self.out.ptr, self.ws.ptr,
+            self.ws_bytes, qmla._sh(self.stream)))
+
+    def run(self, steps, warmup):
+        assert steps + warmup <= 512, "the cache has room for 512 new tokens per sequence"
+        wall, ev = time_steps(self.step, steps, warmup, self.stream)
+        t = ev * 1e-3
+        mean_ctx = self.ctx + warmup + (steps + 1) / 2.0
+        hbm = self.weight_bytes + self.batch * mean_ctx * ROW_BYTES
+        return {"tok_s": self.batch / t, "ms_per_step": ev, "wall_ms_per_step": wall,
+                "weight_bytes": self.weight_bytes, "bytes_per_step": hbm, "tb_s": hbm / t / 1e12,
+                "hbm_frac": hbm / t / 1e12 / (HBM_PEAK_GBS / 1e3)}
+
+
 def cpu_baseline(lens, heads, sample_seqs, min_seconds=10.0):
     """The oracle's absorbed-latent decode (the CPU restatement of the
     reference path), timed on the host cores on a bounded sample of the same
@@ -285,6 +342,13 @@ def main():
                                         **p5.run(max(3, args.steps // 4), max(1, args.warmup // 2))}
         log("chunked prefill", json.dumps(secondary["chunked_prefill"]))
         del p5
+        lb = LayerDecodeBench(stream, seed=51)
+        secondary["layer_decode_step"] = {
+            "workload": "MlaAttention forward_with_cache, hidden 2048, 16 heads, r 512, batch 32, "
+                        "4096 cached + 1, f32 weights, bf16 latent cache",
+            **lb.run(args.steps, args.warmup)}
+        log("layer decode step", json.dumps(secondary["layer_decode_step"]))
+        del lb
 
     cpu = None
     if not args.no_cpu_baseline:
