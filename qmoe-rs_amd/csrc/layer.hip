@@ -43,6 +43,7 @@ namespace qmla {
 namespace {
 
 // ------------------------------------------------------------ f32 GEMM
+constexpr int kSkinnyRows = 64;  // products with at most this many rows go split-K
 // The projections are plain GEMMs and go to rocBLAS (full f32: no reduced-
 // precision math mode is set on the handle).
 // C[z][m][n] = sum_k A[z][m][k] * B[z][k][n] (+ bias[z][n]); B is read as
@@ -92,9 +93,45 @@ qmla_status gemm(const qmla_layer *L, const GemmArgs &g, int batch, bool trans_b
   return QMLA_OK;
 }
 
-// y = x W^T + b for x [M, K], W [N, K] (candle_nn::Linear)
+// K slices for a skinny product (few rows, long K): rocBLAS tiles such a
+// GEMM over N only, which leaves most of the device idle (32-48 workgroups
+// for the decode-step projections).  Splitting K into S slices of >= 256
+// multiplies the grid by S; the slices' partial products are then summed.
+inline int split_k_slices(int M, int K) {
+  int S = 1;
+  if (M <= kSkinnyRows)
+    while (S < 16 && K % (2 * S) == 0 && K / (2 * S) >= 256) S *= 2;
+  return S;
+}
+
+// y[m][n] = bias[n] + sum_s part[s][m][n], in slice order (deterministic).
+__global__ __launch_bounds__(256) void k_split_k_sum(const float *__restrict__ part, int S,
+                                                     int64_t MN, int N,
+                                                     const float *__restrict__ bias,
+                                                     float *__restrict__ y) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= MN) return;
+  float acc = bias ? bias[i % N] : 0.f;
+  for (int s = 0; s < S; ++s) acc += part[s * MN + i];
+  y[i] = acc;
+}
+
+// y = x W^T + b for x [M, K], W [N, K] (candle_nn::Linear).  Skinny
+// products with room in `part` (S * M * N floats) go split-K.
 qmla_status linear(const qmla_layer *L, const float *x, int M, int K, const float *W,
-                   const float *b, int N, float *y, hipStream_t s) {
+                   const float *b, int N, float *y, hipStream_t s, float *part = nullptr,
+                   size_t part_elems = 0) {
+  const int S = split_k_slices(M, K);
+  if (S > 1 && part && (size_t)S * M * N <= part_elems) {
+    const int KS = K / S;
+    // slice z: part[z] = x[:, z KS : (z+1) KS] W[:, z KS : (z+1) KS]^T
+    GemmArgs g{x, W, nullptr, part, M, N, KS, K, K, N, KS, KS, (int64_t)M * N, 0};
+    QMLA_TRY(gemm(L, g, S, true, s));
+    const int64_t MN = (int64_t)M * N;
+    k_split_k_sum<<<dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, s>>>(part, S, MN, N, b, y);
+    QMLA_LAUNCH_CHECK("k_split_k_sum");
+    return QMLA_OK;
+  }
   GemmArgs g{x, W, b, y, M, N, K, K, K, N, 0, 0, 0, 0};
   return gemm(L, g, 1, true, s);
 }
@@ -241,7 +278,7 @@ __global__ __launch_bounds__(128) void k_merge_heads(const float *__restrict__ c
 inline size_t al(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct LayerWs {
-  size_t q, kva, rows, qn, qr, qlat, olat, o, dec, kvb, k, v, kr, ctx, total;
+  size_t q, kva, rows, qn, qr, qlat, olat, o, dec, kvb, k, v, kr, ctx, part, part_elems, total;
 };
 
 // Scratch carve-up shared by the size query and the two forward calls.
@@ -270,6 +307,11 @@ LayerWs layer_ws(const qmla_layer *L, const qmla_kv_cache *c, int32_t batch, int
   w.v = take(sizeof(float) * n * H * g.v_dim);
   w.kr = take(sizeof(float) * n * g.qk_rope + 4);
   w.ctx = take(sizeof(float) * n * H * g.v_dim);
+  // split-K partials of the skinny projections (16 slices at most)
+  const size_t widest = std::max<size_t>({(size_t)H * (g.qk_nope + g.qk_rope),
+                                          (size_t)(g.kv_lora_rank + g.qk_rope), (size_t)g.hidden});
+  w.part_elems = n <= (size_t)kSkinnyRows ? 16 * n * widest : 0;
+  w.part = take(sizeof(float) * (w.part_elems ? w.part_elems : 1));
   w.total = off;
   (void)c;
   return w;
@@ -440,12 +482,13 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
   float *q = (float *)(ws + w.q), *kva = (float *)(ws + w.kva);
   float *qn = (float *)(ws + w.qn), *qr = (float *)(ws + w.qr), *qlat = (float *)(ws + w.qlat);
   float *olat = (float *)(ws + w.olat), *o = (float *)(ws + w.o);
+  float *part = (float *)(ws + w.part);
   hipStream_t s = as_stream(stream);
   const int n = batch * seq;
   const int pos0 = cache->h_lens[0];
 
-  QMLA_TRY(linear(L, xs, n, g.hidden, L->wq, L->bq, H * (dn + dr), q, s));
-  QMLA_TRY(linear(L, xs, n, g.hidden, L->wkva, L->bkva, r + dr, kva, s));
+  QMLA_TRY(linear(L, xs, n, g.hidden, L->wq, L->bq, H * (dn + dr), q, s, part, w.part_elems));
+  QMLA_TRY(linear(L, xs, n, g.hidden, L->wkva, L->bkva, r + dr, kva, s, part, w.part_elems));
   QMLA_TRY(latent_to_cache(L, kva, batch, seq, pos0, nullptr, cache, s));
   k_split_rope_q<<<dim3(n, H), dim3(64), 0, s>>>(q, seq, H, dn, dr, L->inv_freq,
                                                 (float)g.rope_mscale, pos0, 0, qn, qr);
@@ -466,7 +509,7 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
                (int64_t)(dn + dv)};
     QMLA_TRY(gemm(L, a, H, true, s));
   }
-  QMLA_TRY(linear(L, o, n, H * dv, L->wo, L->bo, g.hidden, out, s));
+  QMLA_TRY(linear(L, o, n, H * dv, L->wo, L->bo, g.hidden, out, s, part, w.part_elems));
   return QMLA_OK;
 }
 
@@ -491,11 +534,12 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
   float *qn = (float *)(ws + w.qn), *qr = (float *)(ws + w.qr), *kvb = (float *)(ws + w.kvb);
   float *k = (float *)(ws + w.k), *v = (float *)(ws + w.v), *kr = (float *)(ws + w.kr);
   float *ctx = (float *)(ws + w.ctx), *o = (float *)(ws + w.o);
+  float *part = (float *)(ws + w.part);
   hipStream_t s = as_stream(stream);
   const int n = batch * seq;
 
-  QMLA_TRY(linear(L, xs, n, g.hidden, L->wq, L->bq, H * (dn + dr), q, s));
-  QMLA_TRY(linear(L, xs, n, g.hidden, L->wkva, L->bkva, r + dr, kva, s));
+  QMLA_TRY(linear(L, xs, n, g.hidden, L->wq, L->bq, H * (dn + dr), q, s, part, w.part_elems));
+  QMLA_TRY(linear(L, xs, n, g.hidden, L->wkva, L->bkva, r + dr, kva, s, part, w.part_elems));
   // the latent replacement of the KVCache returned at src/model.rs:250 (the
   // f32 rows also feed compute_kv below)
   QMLA_TRY(latent_to_cache(L, kva, batch, seq, 0, rows, cache, s));
@@ -518,7 +562,7 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
   QMLA_TRY(launch_prefill_f32(pd, qn, qr, k, kr, v, (float)g.softmax_scale, 1, ctx, s));
   k_merge_heads<<<dim3(n, H), dim3(128), 0, s>>>(ctx, seq, H, dv, o);
   QMLA_LAUNCH_CHECK("k_merge_heads");
-  QMLA_TRY(linear(L, o, n, H * dv, L->wo, L->bo, g.hidden, out, s));
+  QMLA_TRY(linear(L, o, n, H * dv, L->wo, L->bo, g.hidden, out, s, part, w.part_elems));
   return QMLA_OK;
 }
 
