@@ -13,12 +13,11 @@
 // of the P.V product, and V^T comes from the key-major tile through
 // ds_read_b64_tr_b16.  Each wave fits in half a SIMD's register file, so
 // two waves share a SIMD: waves 0-3 (group 0) and 4-7 (group 1), one of
-// each per SIMD.  The block advances in steps, a barrier before every
-// even one (one per tile); in every step one group computes S^T of a tile
-// (MFMA and LDS bound) while the other computes the softmax of its
-// previous S^T (VALU) and then the P.V of the tile before (MFMA), so one
-// wave's softmax runs under the other wave's MFMAs.  Group 1 runs one step
-// behind group 0.
+// each per SIMD.  The block advances in barrier-separated steps; in every
+// step one group computes S^T of a tile (MFMA and LDS bound) while the
+// other computes the softmax of its previous S^T (VALU) and then the P.V
+// of the tile before (MFMA), so one wave's softmax runs under the other
+// wave's MFMAs.  Group 1 runs one step behind group 0.
 //
 // The softmax keeps a lazy fixed reference per row (the first tile's
 // maximum; a block in which some probability exceeds kPOverflow redoes its
@@ -345,17 +344,16 @@ __device__ __forceinline__ bf16x8_t load_q_frag(const uint16_t *__restrict__ qn,
 
 // grid.x = batch * heads * n_qtiles (heaviest query tiles first when causal)
 //
-// Schedule.  Step k (0 <= k < 2 * ntb + 3) is local step k - g of a group-g
-// wave.  Local step 2j: S^T of tile j.  Local step 2j + 1: softmax of tile
-// j, then P.V of tile j - 1.  Tile j is therefore read last in step 2j + 2
-// (group 1's P.V), and the DMA of tile j + kPStages into its stage is
-// issued at step 2j + 5 (odd steps k >= 3 issue tile (k - 5) / 2 +
-// kPStages; the prologue issues tiles 0 .. kPStages - 2), after the barrier
-// of step 2j + 4.  Before step 2m every wave waits for its share of tile m
-// and then meets the others at a barrier, so tile m is complete in LDS for
-// both groups' S^T (steps 2m and 2m + 1).  Odd steps have no barrier: none
-// is needed for the ring, and without it the two groups absorb each
-// other's jitter within a tile.
+// Schedule.  Step k (0 <= k < 2 * ntb + 3, a barrier before each) is local
+// step k - g of a group-g wave.  Local step 2j: S^T of tile j.  Local step
+// 2j + 1: softmax of tile j, then P.V of tile j - 1.  Tile j is therefore
+// read last in global step 2j + 4 (group 1's P.V, its local step 2j + 3),
+// and the DMA of tile j + kPStages into its stage is issued in step 2j + 5
+// (odd steps k >= 3 issue tile (k - 5) / 2 + kPStages; the prologue issues
+// tiles 0 .. kPStages - 2): the barrier before step 2j + 5 is what keeps
+// that DMA behind the last read, so every step needs its barrier.  Before
+// step 2m every wave waits for its share of tile m, so tile m is complete
+// in LDS when group 0 reads it.
 template <int DN, int DR, int DV>
 __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
     const uint16_t *__restrict__ q_nope, const uint16_t *__restrict__ q_rope,
@@ -492,7 +490,7 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
       ptile_p<MASK>(s, sl2, m_ref, 0, half, vis_lim, l_run, t_max, pb);
     };
 
-    // Step k: vmcnt wait and barrier (even k).  At odd steps k >= 3, group 1
+    // Step k: vmcnt wait (even k), barrier.  At odd steps k >= 3, group 1
     // issues tile (k - 5) / 2 + kPStages, spread over its S^T MFMAs when it
     // has an S^T in that step.
     int k = 0;
@@ -506,9 +504,9 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
           wait_vmcnt<(kPStages - 3) * SH::MI>();
         else
           pwait_tiles<SH>(last - m, my_instr);
-        wait_lgkm<0>();
-        __builtin_amdgcn_s_barrier();
       }
+      wait_lgkm<0>();
+      __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
       ++k;
     };

@@ -86,7 +86,7 @@ def test_chunked_prefill_golden(qmla_gpu, golden, bf16):
 
 @pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("sq,sk,causal,krh", [(300, 300, True, 1), (257, 257, True, 3), (100, 333, False, 1),
-                                              (1, 1, True, 1), (65, 65, True, 1)])
+                                              (1, 1, True, 1), (65, 65, True, 1), (200, 200, True, 1)])
 def test_prefill_shapes_mla_dims(qmla_gpu, bf16, sq, sk, causal, krh):
     q = qmla_gpu
     arrs = inputs(2, 3, sq, sk, 128, 64, 128, krh, 100 + sq)
