@@ -243,3 +243,27 @@ def test_decode_bf16_growing_scores_restart(qmla_gpu, rows_m):
     assert err < TOL_BF16
     # |s| reaches tens of nats here, so bf16 rounding of q moves lse by ~0.1
     np.testing.assert_allclose(lse, rlse, atol=0.5)
+
+
+@pytest.mark.parametrize("rows_m,q_bf16", [(48, False), (64, True), (33, True), (128, False)])
+def test_decode_bf16_mixed_lengths_sweep(qmla_gpu, rows_m, q_bf16):
+    """Latent 512/64 with 33..128 query rows (the 2- and 4-wave kernels),
+    f32 and bf16 queries, lengths from 1 to a few tiles past a piece,
+    empty sequences in between, and several split counts."""
+    q = qmla_gpu
+    lens = [1, 0, 31, 32, 33, 700, 5000, 0, 64, 2049]
+    cache, rows, offs = make_cache(q, lens, 512, 64, q.BF16, 900 + rows_m, cap_extra=3)
+    b = len(lens)
+    ql, qr = O.normal((b, rows_m, 512), 901), O.normal((b, rows_m, 64), 902)
+    if q_bf16:
+        ql, qr = bf16_to_f32(bf16_bits(ql)), bf16_to_f32(bf16_bits(qr))
+    ref, rlse = O.decode_absorbed(ql, qr, rows, offs, np.asarray(lens, np.int32), 0.06)
+    for splits in (0, 7, 300):
+        out, lse = run(q, cache, ql, qr, 0.06, splits=splits, q_dtype=q.BF16 if q_bf16 else q.F32)
+        err = rel_err(out, ref)
+        print(f"rows={rows_m} q_bf16={q_bf16} splits={splits} rel_err={err:.2e}", flush=True)
+        assert np.isfinite(out).all()
+        assert err < TOL_BF16
+        empty = np.asarray(lens) == 0
+        assert np.all(out[empty] == 0) and np.all(np.isneginf(lse[empty]))
+        np.testing.assert_allclose(lse[~empty], rlse[~empty], atol=2e-2)

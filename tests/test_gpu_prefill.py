@@ -97,6 +97,26 @@ def test_prefill_shapes_mla_dims(qmla_gpu, bf16, sq, sk, causal, krh):
     assert err < (TOL_BF16 if bf16 else TOL_F32)
 
 
+def test_prefill_bf16_shape_sweep(qmla_gpu):
+    """Shapes that leave waves of a 256-row block without query rows (and
+    some DMA waves idle), partial last key tiles, one query row, chunks with
+    an offset and keys beyond the queries, non-causal and causal."""
+    q = qmla_gpu
+    cases = [  # b, h, sq, sk, q_offset, causal
+        (1, 2, 33, 33, 0, True), (1, 1, 97, 97, 0, True), (2, 1, 129, 129, 0, True),
+        (1, 3, 225, 225, 0, True), (1, 2, 1, 500, 0, False), (1, 2, 5, 300, 295, True),
+        (2, 2, 40, 1000, 960, True), (1, 9, 70, 70, 0, False), (3, 1, 256, 256, 0, True),
+        (1, 1, 300, 700, 400, True)]
+    for i, (b, h, sq, sk, off, causal) in enumerate(cases):
+        arrs = inputs(b, h, sq, sk, 128, 64, 128, 1, 800 + 10 * i)
+        out, used = gpu_prefill(q, arrs, 192 ** -0.5, causal, q_offset=off, bf16=True)
+        ref = O.fused_prefill_attn(*[np.asarray(u) for u in used], 192 ** -0.5, causal, q_offset=off)
+        err = rel_err(out, ref)
+        print(f"b={b} h={h} sq={sq} sk={sk} off={off} causal={causal} rel_err={err:.2e}", flush=True)
+        assert np.isfinite(out).all()
+        assert err < TOL_BF16, (b, h, sq, sk, off, causal, err)
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_prefill_bf16_growing_scores_restart(qmla_gpu, causal):
     """Keys drift along a direction every query shares, so the scores grow
