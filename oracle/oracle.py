@@ -24,6 +24,7 @@ _f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
 _u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
 _i64p = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
 
 
 def build(force: bool = False) -> str:
@@ -66,6 +67,10 @@ def lib():
             "orc_decode_absorbed_f64": (None, [_f32p, _f32p, _f32p, _i64p, _i32p, C.c_int, C.c_int, C.c_int,
                                                C.c_int, C.c_double, _f64p, C.c_void_p]),
             "orc_num_threads": (C.c_int, []),
+            "orc_fused_dequantize_and_dot": (C.c_float, [_u8p, C.c_size_t, _f32p, C.c_size_t, C.c_float]),
+            "orc_packed_forward": (None, [_u8p, _f32p, C.c_int, C.c_int, _f32p, C.c_int, _f32p]),
+            "orc_moe_forward": (None, [C.c_void_p, _f32p, C.c_int, _f32p, _u8p, _f32p, _u8p, _f32p, _u8p,
+                                       _f32p, _f32p, _i32p, _f32p]),
             "orc_set_num_threads": (None, [C.c_int]),
         }
         for name, (res, args) in sig.items():
@@ -402,3 +407,105 @@ def mla_forward_with_latent(L: MlaWeights, xs, latent):
     lib().orc_mla_forward_with_latent(C.byref(st), xs.ctypes.data, b, s, latent.ctypes.data, Tc,
                                       out.ctypes.data, rows.ctypes.data)
     return out, rows
+
+
+# --------------------------------------------------------------- 2-bit MoE
+# moe_oracle.c: fused_dequantize_and_dot / forward_simd / QMoELayer::forward
+# (src/simd.rs:6-45, src/tensor.rs:64-95, src/moe.rs:40-130).
+
+def fused_dequantize_and_dot(packed: np.ndarray, act: np.ndarray, scale: float) -> float:
+    p, a = _c(packed, np.uint8), _c(act)
+    return float(lib().orc_fused_dequantize_and_dot(p, p.size, a, a.size, scale))
+
+
+def packed_forward(packed: np.ndarray, scales: np.ndarray, out_f: int, in_f: int, x: np.ndarray) -> np.ndarray:
+    """out [batch, out_f] from packed [out_f, in_f // 4] and x [..., in_f]."""
+    x = _c(x)
+    batch = x.size // in_f
+    out = np.empty((batch, out_f), np.float32)
+    lib().orc_packed_forward(_c(packed, np.uint8), _c(scales), out_f, in_f, x, batch, out)
+    return out
+
+
+class _MoECfg(C.Structure):
+    _fields_ = [("num_experts", C.c_int), ("top_k", C.c_int), ("hidden_dim", C.c_int),
+                ("intermediate_dim", C.c_int)]
+
+
+@dataclass
+class MoEWeights:
+    """QMoELayer weights (src/moe.rs:23-28, :15-19): gate_weight [E, H] f32;
+    per-kind packed tensors stacked over experts: gate/up [E, I, H/4],
+    down [E, H, I/4] (uint8), scales gate/up [E, I], down [E, H]."""
+    num_experts: int
+    top_k: int
+    hidden_dim: int
+    intermediate_dim: int
+    gate_weight: np.ndarray
+    gate_packed: np.ndarray
+    gate_scales: np.ndarray
+    up_packed: np.ndarray
+    up_scales: np.ndarray
+    down_packed: np.ndarray
+    down_scales: np.ndarray
+
+    def cfg(self):
+        return _MoECfg(self.num_experts, self.top_k, self.hidden_dim, self.intermediate_dim)
+
+
+def moe_forward(W: MoEWeights, xs: np.ndarray, return_routing: bool = False):
+    """QMoELayer::forward: xs [seq, H] -> [seq, H] (+ routing [seq, top_k])."""
+    xs = _c(xs)
+    T = xs.shape[0]
+    out = np.empty((T, W.hidden_dim), np.float32)
+    idx = np.empty((T, max(W.top_k, 1)), np.int32)
+    wts = np.empty((T, max(W.top_k, 1)), np.float32)
+    cfg = W.cfg()
+    lib().orc_moe_forward(C.byref(cfg), xs, T, _c(W.gate_weight), _c(W.gate_packed, np.uint8),
+                          _c(W.gate_scales), _c(W.up_packed, np.uint8), _c(W.up_scales),
+                          _c(W.down_packed, np.uint8), _c(W.down_scales), out, idx, wts)
+    if return_routing:
+        return out, idx[:, :W.top_k], wts[:, :W.top_k]
+    return out
+
+
+def bench_packed_data(out_f: int, in_f: int):
+    """The reference benches' deterministic packed tensor
+    (benches/moe_layer.rs:11-29): bytes cycle 0x58, 0xA7, 0x2E, 0xE4 and
+    scale i = sin(0.05 i) + 1 (f32)."""
+    n = out_f * (in_f // 4)
+    packed = np.resize(np.array([0x58, 0xA7, 0x2E, 0xE4], np.uint8), n).reshape(out_f, in_f // 4)
+    i = np.arange(out_f, dtype=np.float32)
+    return packed, (np.sin(i * np.float32(0.05)) + np.float32(1.0)).astype(np.float32)
+
+
+def bench_moe_weights(num_experts: int, top_k: int, hidden: int, inter: int) -> MoEWeights:
+    """make_moe_layer of benches/moe_layer.rs:75-90 (every expert holds the
+    same deterministic pattern; gate_weight[i] = cos(0.07 i))."""
+    gp, gs = bench_packed_data(inter, hidden)
+    dp, ds = bench_packed_data(hidden, inter)
+    E = num_experts
+    i = np.arange(E * hidden, dtype=np.float32)
+    gw = np.cos(i * np.float32(0.07)).astype(np.float32).reshape(E, hidden)
+    rep = lambda a: np.ascontiguousarray(np.broadcast_to(a, (E,) + a.shape))
+    return MoEWeights(E, top_k, hidden, inter, gw, rep(gp), rep(gs), rep(gp), rep(gs), rep(dp), rep(ds))
+
+
+def bench_moe_input(tokens: int, hidden: int) -> np.ndarray:
+    """generate_input of benches/moe_layer.rs:68-73: sin(0.1 i) + 0.5."""
+    i = np.arange(tokens * hidden, dtype=np.float32)
+    return (np.sin(i * np.float32(0.1)) + np.float32(0.5)).astype(np.float32).reshape(tokens, hidden)
+
+
+def random_moe_weights(num_experts: int, top_k: int, hidden: int, inter: int, seed: int,
+                       gate_std: float = 0.05) -> MoEWeights:
+    """Seeded random packed experts: uniform codes 0..3 per weight, scales
+    U(0.005, 0.02), gate_weight ~ N(0, gate_std^2)."""
+    E = num_experts
+    r = lambda n, s: uniform_int(n, s, 0, 255).astype(np.uint8)
+    sc = lambda n, s: (0.005 + 0.015 * (uniform_int(n, s, 0, 1 << 20) / float(1 << 20))).astype(np.float32)
+    return MoEWeights(
+        E, top_k, hidden, inter, normal((E, hidden), seed, gate_std),
+        r(E * inter * (hidden // 4), seed + 1).reshape(E, inter, hidden // 4), sc(E * inter, seed + 2).reshape(E, inter),
+        r(E * inter * (hidden // 4), seed + 3).reshape(E, inter, hidden // 4), sc(E * inter, seed + 4).reshape(E, inter),
+        r(E * hidden * (inter // 4), seed + 5).reshape(E, hidden, inter // 4), sc(E * hidden, seed + 6).reshape(E, hidden))
