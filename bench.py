@@ -18,7 +18,9 @@ prefill (batch 8, 8192 cached + 512 new, 128 heads), the prefills in TFLOP/s
 of unmasked attention work (MHA form, dqk 192 + dv 128) against the
 2.5 PFLOP/s bf16 dense peak; and one full MLA layer decode step
 (forward_with_cache: projections, latent append, decode core, W_UV, o_proj)
-at V2-Lite head shapes, in tokens/s and weight + cache bytes per step.
+at V2-Lite head shapes, in tokens/s and weight + cache bytes per step; and the
+2-bit packed MoE layer forward at the reference bench's default sizes, in
+tokens/s and the active experts' packed bytes per step against 8 TB/s.
 
 Inputs are generated on the device (seeded) before the timed region.  The
 decode caches rotate over replicas totalling >= 2 GB so consecutive steps
@@ -223,6 +225,86 @@ class LayerDecodeBench:
                 "hbm_frac": hbm / t / 1e12 / (HBM_PEAK_GBS / 1e3)}
 
 
+def ref_bench_packed(out_f: int, in_f: int):
+    """The reference benches' packed tensor (benches/moe_layer.rs:11-29):
+    bytes cycling 0x58, 0xA7, 0x2E, 0xE4; scale i = sin(0.05 i) + 1."""
+    packed = np.resize(np.array([0x58, 0xA7, 0x2E, 0xE4], np.uint8), out_f * (in_f // 4))
+    i = np.arange(out_f, dtype=np.float32)
+    return packed.reshape(out_f, in_f // 4), (np.sin(i * np.float32(0.05)) + np.float32(1.0)).astype(np.float32)
+
+
+def ref_bench_moe(tokens=16, experts=32, top_k=4, hidden=2048, inter=1408):
+    """make_moe_layer + generate_input of benches/moe_layer.rs:31-90: every
+    expert holds the deterministic pattern above, gate_weight[i] =
+    cos(0.07 i), input[i] = sin(0.1 i) + 0.5."""
+    gp, gs = ref_bench_packed(inter, hidden)
+    dp, ds = ref_bench_packed(hidden, inter)
+    gw = np.cos(np.arange(experts * hidden, dtype=np.float32) * np.float32(0.07)).astype(np.float32)
+    xs = (np.sin(np.arange(tokens * hidden, dtype=np.float32) * np.float32(0.1)) + np.float32(0.5)).astype(np.float32)
+    return (gw.reshape(experts, hidden), [((gp, gs), (gp, gs), (dp, ds))] * experts,
+            xs.reshape(tokens, hidden))
+
+
+class MoEBench:
+    """QMoELayer::forward (src/moe.rs:40-130) at the reference bench's default
+    sizes (benches/moe_layer.rs:465-469): 16 tokens, 32 experts, top-4,
+    hidden 2048, intermediate 1408, 2-bit packed experts, f32 activations.
+    The layer is replicated (8 copies, 553 MB of packed weights) and the
+    steps rotate over the copies, so no step reads weights the 256 MB
+    Infinity Cache could still hold."""
+
+    def __init__(self, stream, replicas=8, tokens=16, experts=32, top_k=4, hidden=2048, inter=1408):
+        gw, ex, xs = ref_bench_moe(tokens, experts, top_k, hidden, inter)
+        cfg = qmla.MoEConfig(experts, top_k, hidden, inter)
+        self.layers = [qmla.QMoELayer(cfg, gw, ex) for _ in range(replicas)]
+        self.cfg, self.tokens, self.stream = cfg, tokens, stream
+        self.xs = qmla.DeviceBuffer.from_numpy(xs)
+        self.out = qmla.DeviceBuffer(tokens * hidden * 4)
+        self.idx = qmla.DeviceBuffer(tokens * top_k * 4)
+        self.ws_bytes = self.layers[0].workspace_bytes(tokens)
+        self.ws = qmla.DeviceBuffer(self.ws_bytes)
+        self.expert_bytes = 3 * inter * (hidden // 4) + 4 * (2 * inter + hidden)
+
+    def step(self, i):
+        self.layers[i % len(self.layers)].forward_device(self.xs, self.tokens, self.out, self.ws, self.ws_bytes,
+                                                         self.idx, None, self.stream)
+
+    def run(self, steps, warmup):
+        wall, ev = time_steps(self.step, steps, warmup, self.stream)
+        active = len(np.unique(self.idx.to_numpy(np.int32, (self.tokens, self.cfg.top_k), self.stream)))
+        c = self.cfg
+        hbm = active * self.expert_bytes + 4 * (c.num_experts * c.hidden_dim + 2 * self.tokens * c.hidden_dim)
+        t = ev * 1e-3
+        return {"tok_s": self.tokens / t, "ms_per_step": ev, "wall_ms_per_step": wall,
+                "active_experts": active, "bytes_per_step": hbm, "tb_s": hbm / t / 1e12,
+                "hbm_frac": hbm / t / 1e12 / (HBM_PEAK_GBS / 1e3), "replicas": len(self.layers)}
+
+
+def moe_cpu_baseline(min_seconds=5.0):
+    """The oracle's QMoELayer::forward restatement (single thread, like the
+    reference's loops in src/moe.rs:60-127) on the same 16-token input,
+    repeated for at least `min_seconds`."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O  # checker library, used here only as the CPU baseline
+
+    gw, ex, xs = ref_bench_moe()
+    (gp, gs), _, (dp, ds) = ex[0]
+    E = gw.shape[0]
+    rep = lambda a: np.ascontiguousarray(np.broadcast_to(a, (E,) + a.shape))
+    W = O.MoEWeights(E, 4, 2048, 1408, gw, rep(gp), rep(gs), rep(gp), rep(gs), rep(dp), rep(ds))
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.moe_forward(W, xs)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds:
+            break
+    per = dt / reps
+    return {"value": xs.shape[0] / per, "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"the full 16-token step x {reps} runs = {dt:.1f} s on 1 thread "
+                      f"({per * 1e3:.0f} ms per step); f32 C restatement (oracle/moe_oracle.c)"}
+
+
 def cpu_baseline(lens, heads, sample_seqs, min_seconds=10.0):
     """The oracle's absorbed-latent decode (the CPU restatement of the
     reference path), timed on the host cores on a bounded sample of the same
@@ -349,6 +431,19 @@ def main():
             **lb.run(args.steps, args.warmup)}
         log("layer decode step", json.dumps(secondary["layer_decode_step"]))
         del lb
+        mb = MoEBench(stream)
+        moe = mb.run(args.steps, args.warmup)
+        del mb
+        secondary["moe_layer"] = {
+            "workload": "QMoELayer forward, 16 tokens, 32 experts, top-4, hidden 2048, intermediate 1408, "
+                        "2-bit packed experts (reference bench pattern), f32 activations, int8 MFMA",
+            **moe,
+            "roofline": {"bound": "hbm", "achieved": moe["tb_s"] * 1e3, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": moe["hbm_frac"],
+                         "kernel": "whole qmla_moe_forward call (route, bin, quantize, gate/up, down, combine)",
+                         "bytes_per_launch": moe["bytes_per_step"]},
+            "cpu_baseline": None if args.no_cpu_baseline else moe_cpu_baseline()}
+        log("moe layer", json.dumps(secondary["moe_layer"]))
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -282,6 +282,58 @@ QMLA_API qmla_status qmla_layer_forward_prefill(const qmla_layer *layer, const f
                                        void *workspace, size_t workspace_bytes,
                                        qmla_stream stream);
 
+/* ------------------------------------ 2-bit packed MoE (tensor.rs, moe.rs)
+ * Packed format (src/simd.rs:20-31): an [out_features, in_features] tensor
+ * is out_features rows of in_features / 4 bytes; weight 4j + q of a row is
+ * bits 2q..2q+1 of byte j, a code c in 0..3 standing for the weight c - 1.
+ * All buffers are device memory.
+ *
+ * PackedQMoETensor::forward_simd (src/tensor.rs:64-95, forward_simd_raw
+ * :99-121): out[b][i] = (sum_k w_ik x[b][k]) * scales[i] for x
+ * [batch, in_features] f32, out [batch, out_features] f32.  Activations past
+ * 4 * (in_features / 4) are ignored, as in src/simd.rs:15.
+ * in_features a multiple of 128: int8 MFMA over an exact integer form of x
+ * (x rounded to 23 bits relative to each row's largest element, sums exact);
+ * other widths: f32 lane sums in the reference's order.  A row of x holding
+ * inf or NaN yields NaN outputs on the MFMA path.                          */
+QMLA_API qmla_status qmla_packed_forward_workspace_bytes(int32_t out_features, int32_t in_features,
+                                                int32_t batch, size_t *bytes);
+QMLA_API qmla_status qmla_packed_forward(const uint8_t *packed, const float *scales,
+                                int32_t out_features, int32_t in_features, const float *x,
+                                int32_t batch, float *out, void *workspace,
+                                size_t workspace_bytes, qmla_stream stream);
+
+/* MoEConfig (src/moe.rs:5-11). */
+typedef struct {
+  int32_t num_experts;
+  int32_t top_k;
+  int32_t hidden_dim;
+  int32_t intermediate_dim;
+} qmla_moe_config;
+
+/* QMoELayer::forward (src/moe.rs:40-130) for xs [seq_len, hidden] f32:
+ * gate logits xs . gate_weight^T (gate_weight [E, hidden] f32), the top_k
+ * experts by (logit descending, expert index ascending) -- the order of the
+ * reference's stable sort --, weights softmax-over-all-experts of their
+ * logits, SwiGLU experts
+ *   y_e(x) = down_e(swish(gate_e(x)) * up_e(x)),  swish(g) = g / (1 + e^-g)
+ * with packed gate/up [E, I, hidden/4], down [E, hidden, I/4] (expert e's
+ * PackedQMoETensor at offset e of each array) and scales gate/up [E, I],
+ * down [E, hidden]; out[t] = sum of weight * y_e(x_t) over the token's
+ * experts in ascending expert order.  top_experts / top_weights
+ * ([seq_len, top_k], nullable) receive the routing in rank order.
+ * num_experts == 0 or top_k == 0 gives zeros (src/moe.rs:46-48);
+ * top_k > num_experts is QMLA_ERR_SHAPE (the reference panics).          */
+QMLA_API qmla_status qmla_moe_workspace_bytes(const qmla_moe_config *cfg, int32_t seq_len,
+                                     size_t *bytes);
+QMLA_API qmla_status qmla_moe_forward(const qmla_moe_config *cfg, const float *xs, int32_t seq_len,
+                             const float *gate_weight, const uint8_t *gate_packed,
+                             const float *gate_scales, const uint8_t *up_packed,
+                             const float *up_scales, const uint8_t *down_packed,
+                             const float *down_scales, float *out, int32_t *top_experts,
+                             float *top_weights, void *workspace, size_t workspace_bytes,
+                             qmla_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -65,6 +65,11 @@ class LayerConfig(C.Structure):
         ("rope_mscale", C.c_double), ("softmax_scale", C.c_double), ("ln_eps", C.c_double)]
 
 
+class MoEConfig(C.Structure):
+    """MoEConfig (src/moe.rs:5-11)."""
+    _fields_ = [(n, C.c_int32) for n in ("num_experts", "top_k", "hidden_dim", "intermediate_dim")]
+
+
 # Every symbol include/qmla.h declares, with its ctypes signature.
 _vp, _i32, _sz, _d, _u64 = C.c_void_p, C.c_int32, C.c_size_t, C.c_double, C.c_uint64
 _st = C.c_int
@@ -110,6 +115,10 @@ SIGNATURES = {
     "qmla_layer_workspace_bytes": (_st, [_vp, _vp, _i32, _i32, C.POINTER(_sz)]),
     "qmla_layer_forward_with_cache": (_st, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "qmla_layer_forward_prefill": (_st, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
+    "qmla_packed_forward_workspace_bytes": (_st, [_i32, _i32, _i32, C.POINTER(_sz)]),
+    "qmla_packed_forward": (_st, [_vp, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _sz, _vp]),
+    "qmla_moe_workspace_bytes": (_st, [C.POINTER(MoEConfig), _i32, C.POINTER(_sz)]),
+    "qmla_moe_forward": (_st, [C.POINTER(MoEConfig), _vp, _i32] + [_vp] * 7 + [_vp, _vp, _vp, _vp, _sz, _vp]),
 }
 
 _lib = None
@@ -447,6 +456,105 @@ class MlaLayer:
             self.close()
         except Exception:
             pass
+
+
+# --------------------------------------------- tensor.rs / moe.rs mirror
+
+def packed_workspace_bytes(out_features: int, in_features: int, batch: int) -> int:
+    n = C.c_size_t()
+    check(lib().qmla_packed_forward_workspace_bytes(out_features, in_features, batch, C.byref(n)))
+    return n.value
+
+
+class PackedQMoETensor:
+    """PackedQMoETensor (src/tensor.rs:16-122) with its bytes and scales in
+    HBM: shape (out_features, in_features), in_features / 4 bytes a row."""
+
+    def __init__(self, packed, shape, scales):
+        out_f, in_f = shape
+        self.shape = (int(out_f), int(in_f))
+        p = np.ascontiguousarray(packed, np.uint8).reshape(-1)
+        sc = np.ascontiguousarray(scales, np.float32).reshape(-1)
+        if p.size < out_f * (in_f // 4) or sc.size < out_f:
+            raise QmlaError(2, "packed bytes or scales smaller than the shape")
+        self.data = DeviceBuffer.from_numpy(p)
+        self.scales = DeviceBuffer.from_numpy(sc)
+
+    @staticmethod
+    def from_bytes(packed, shape, scales) -> "PackedQMoETensor":
+        return PackedQMoETensor(packed, shape, scales)
+
+    def forward(self, x, batch: int, out, workspace=None, workspace_bytes: int = 0, stream=None):
+        """Device form: x [batch, in] f32 -> out [batch, out] f32 (buffers)."""
+        check(lib().qmla_packed_forward(self.data.ptr, self.scales.ptr, self.shape[0], self.shape[1], _p(x),
+                                        batch, _p(out), _p(workspace), workspace_bytes, _sh(stream)))
+
+    def forward_simd(self, x: np.ndarray) -> np.ndarray:
+        """forward_simd (src/tensor.rs:64-95): x [..., in] -> [..., out]."""
+        out_f, in_f = self.shape
+        x = np.ascontiguousarray(x, np.float32)
+        if in_f == 0 or x.size % in_f:
+            raise QmlaError(2, f"input size {x.size} is not a multiple of in_features {in_f}")
+        batch = x.size // in_f
+        bx = DeviceBuffer.from_numpy(x)
+        out = DeviceBuffer(batch * out_f * 4)
+        n = packed_workspace_bytes(out_f, in_f, batch)
+        ws = DeviceBuffer(n) if n else None
+        self.forward(bx, batch, out, ws, n)
+        check(lib().qmla_stream_synchronize(None))
+        return out.to_numpy(np.float32, x.shape[:-1] + (out_f,))
+
+
+class QMoELayer:
+    """QMoELayer (src/moe.rs:23-131).  experts: a list of (gate, up, down)
+    triples of (packed bytes, scales) host arrays, stacked into one HBM array
+    per kind."""
+
+    def __init__(self, config: MoEConfig, gate_weight: np.ndarray, experts):
+        self.config = config
+        E, H, I = config.num_experts, config.hidden_dim, config.intermediate_dim
+        if len(experts) != E:
+            raise QmlaError(2, f"{len(experts)} experts for num_experts {E}")
+        kinds = list(zip(*experts)) if E else [(), (), ()]
+        shapes = [(I, H), (I, H), (H, I)]
+        self.bufs = []
+        for kind, (o, i) in zip(kinds, shapes):
+            pk = np.zeros((max(E, 1), o, i // 4), np.uint8)
+            sc = np.zeros((max(E, 1), o), np.float32)
+            for e, (p, s_) in enumerate(kind):
+                pk[e] = np.asarray(p, np.uint8).reshape(o, i // 4)
+                sc[e] = np.asarray(s_, np.float32).reshape(o)
+            self.bufs += [DeviceBuffer.from_numpy(pk), DeviceBuffer.from_numpy(sc)]
+        self.gate_weight = DeviceBuffer.from_numpy(np.ascontiguousarray(gate_weight, np.float32).reshape(-1)
+                                                   if E else np.zeros(1, np.float32))
+
+    def workspace_bytes(self, seq_len: int) -> int:
+        n = C.c_size_t()
+        check(lib().qmla_moe_workspace_bytes(C.byref(self.config), seq_len, C.byref(n)))
+        return n.value
+
+    def forward_device(self, xs, seq_len: int, out, workspace, workspace_bytes: int, top_experts=None,
+                       top_weights=None, stream=None):
+        gp, gs, up, us, dp, ds = (b.ptr for b in self.bufs)
+        check(lib().qmla_moe_forward(C.byref(self.config), _p(xs), seq_len, self.gate_weight.ptr, gp, gs, up, us,
+                                     dp, ds, _p(out), _p(top_experts), _p(top_weights), _p(workspace),
+                                     workspace_bytes, _sh(stream)))
+
+    def forward(self, xs: np.ndarray, return_routing: bool = False):
+        """forward (src/moe.rs:40-130): xs [seq_len, hidden] -> [seq_len, hidden]."""
+        xs = np.ascontiguousarray(xs, np.float32)
+        T, H, k = xs.shape[0], self.config.hidden_dim, self.config.top_k
+        bx = DeviceBuffer.from_numpy(xs)
+        out = DeviceBuffer(T * H * 4)
+        n = self.workspace_bytes(T)
+        ws = DeviceBuffer(n)
+        ti, tw = DeviceBuffer(T * max(k, 1) * 4), DeviceBuffer(T * max(k, 1) * 4)
+        self.forward_device(bx, T, out, ws, n, ti, tw)
+        check(lib().qmla_stream_synchronize(None))
+        y = out.to_numpy(np.float32, (T, H))
+        if return_routing:
+            return y, ti.to_numpy(np.int32, (T, k)), tw.to_numpy(np.float32, (T, k))
+        return y
 
 
 # ------------------------------------------------------ HIP events (timing)
