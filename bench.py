@@ -30,6 +30,7 @@ on a bounded sample (>= 10 s), scaled to the full batch.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
        python bench.py --calibrate   (copy kernel for scaling PMC counters)
+       python bench.py --moe-only    (the MoE layer line alone, for profiling)
 """
 from __future__ import annotations
 
@@ -387,6 +388,8 @@ def main():
     ap.add_argument("--cpu-sample-seqs", type=int, default=32)
     ap.add_argument("--calibrate", action="store_true",
                     help="only run the copy kernel used to scale the PMC byte counters")
+    ap.add_argument("--moe-only", action="store_true",
+                    help="only run the 2-bit packed MoE layer line (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the decode path shards by batch "
@@ -398,6 +401,10 @@ def main():
     stream = qmla.Stream()
     if args.calibrate:
         copy_calibration(stream)
+        return
+    if args.moe_only:
+        mb = MoEBench(stream)
+        print(json.dumps({"moe_layer": mb.run(args.steps, args.warmup)}), flush=True)
         return
 
     lens = synth.v3_decode_lengths()

@@ -1,4 +1,4 @@
-"""ctypes binding of the CPU oracle (oracle/mla_oracle.c).
+"""ctypes binding of the CPU oracle (oracle/mla_oracle.c, oracle/moe_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() and
 by bench.py's cpu_baseline leg, as the checker.  The product library

@@ -38,6 +38,7 @@ typedef int i32x16_t __attribute__((ext_vector_type(16)));
 constexpr int kTokTile = 10;   // vectors per MFMA tile (3 digit columns each)
 constexpr int kSlab = 4096;    // codes of B staged in LDS at once (128 KB)
 constexpr int kMfmaWaves = 4;  // waves per block; each owns 32 rows
+constexpr int kMfmaThreads = 64 * kMfmaWaves;
 constexpr int kMaxExperts = 4096;
 constexpr int kMaxK = 1 << 20;
 
@@ -106,18 +107,17 @@ constexpr int kBadExp = 0x7fffffff;  // exponent marking a vector with inf/NaN
 // finds each vector's largest magnitude (its exponent e) unless the producer
 // handed it over (src_max), pass 2 writes the digits of each slab of K into
 // LDS in the lane order of the B operand and sums q per vector.
-// NG > 0: K = 128 NG in one slab, and every weight group of the wave is
-// requested at entry, before the passes, so the whole HBM latency overlaps
+// NG > 0: K = 128 NG in one slab with a compile-time ring of weight
+// groups, the first ones requested at entry so their HBM latency overlaps
 // the quantisation.  NG = 0: any K % 128 == 0, a ring of D groups in flight.
 template <int NMAT, int NG>
-__global__ __launch_bounds__(256) void k_packed_mfma(PackedArgs a) {
+__global__ __launch_bounds__(kMfmaThreads) void k_packed_mfma(PackedArgs a) {
   extern __shared__ __attribute__((aligned(16))) int8_t lds_b[];  // [chunk][h][32][16]
   __shared__ int64_t voff[kTokTile];
   __shared__ int vslot[kTokTile];
   __shared__ unsigned vmax[kTokTile];
   __shared__ int vexp[kTokTile];
   __shared__ unsigned long long vsum[kTokTile];
-  __shared__ float ostage[kMfmaWaves][kTokTile][32];  // epilogue transpose
   __shared__ unsigned bmax[kTokTile];
   TileInfo ti;
   if (!load_tile(a, ti)) return;
@@ -176,15 +176,15 @@ __global__ __launch_bounds__(256) void k_packed_mfma(PackedArgs a) {
     constexpr int U = 8;
     unsigned run = 0;
     int cur = -1;
-    for (int base = 0; base < items; base += 256 * U) {
+    for (int base = 0; base < items; base += kMfmaThreads * U) {
       u32x4_t v[U];
       int tt[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int i = min(base + tid + 256 * u, items - 1);
+        const int i = min(base + tid + kMfmaThreads * u, items - 1);
         const int tu = i / K4;
         v[u] = *reinterpret_cast<const u32x4_t *>(a.x + voff[tu] + 4 * (i - tu * K4));
-        tt[u] = base + tid + 256 * u < items ? tu : -1;
+        tt[u] = base + tid + kMfmaThreads * u < items ? tu : -1;
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -229,11 +229,11 @@ __global__ __launch_bounds__(256) void k_packed_mfma(PackedArgs a) {
       unsigned long long qs = 0;
       int cur = -1;
       constexpr int U2 = 2;  // items whose loads are issued together
-      for (int i0 = tid; i0 < items; i0 += 256 * U2) {
+      for (int i0 = tid; i0 < items; i0 += kMfmaThreads * U2) {
         floatx4_t f[U2][4];
 #pragma unroll
         for (int u = 0; u < U2; ++u) {
-          const int i = min(i0 + 256 * u, items - 1);
+          const int i = min(i0 + kMfmaThreads * u, items - 1);
           const int t = i % ti.ntok, r = i / ti.ntok;
           const int cg = (k0 >> 5) + (r >> 1);
           const float *src = a.x + voff[t] + 128 * (cg >> 2) + 64 * (r & 1) + 16 * (cg & 3);
@@ -242,7 +242,7 @@ __global__ __launch_bounds__(256) void k_packed_mfma(PackedArgs a) {
         }
 #pragma unroll
         for (int u = 0; u < U2; ++u) {
-          const int i = i0 + 256 * u;
+          const int i = i0 + kMfmaThreads * u;
           if (i >= items) break;
           const int t = i % ti.ntok, r = i / ti.ntok;
           const int h2 = r & 1, c = r >> 1;
@@ -277,7 +277,7 @@ __global__ __launch_bounds__(256) void k_packed_mfma(PackedArgs a) {
       if (cur >= 0) atomicAdd(&vsum[cur], qs);
       // columns of absent vectors and the two spare columns
       const int spare = 32 - 3 * ti.ntok;
-      for (int i = tid; i < spare * 2 * nch; i += 256) {
+      for (int i = tid; i < spare * 2 * nch; i += kMfmaThreads) {
         const int col = 3 * ti.ntok + i % spare, r = i / spare;
         *reinterpret_cast<i32x4_t *>(lds_b + ((r * 32 + col) << 4)) = i32x4_t{0, 0, 0, 0};
       }
@@ -345,53 +345,51 @@ __global__ __launch_bounds__(256) void k_packed_mfma(PackedArgs a) {
       }
     }
   }
-  // Idle waves (rows past M) stay to the end: the block barrier below.
-  // Column 3t + p of the accumulator holds digit plane p of vector t.
-  long long tot[NMAT][16];
+  // Epilogue.  The accumulators go through LDS (the B area, free once
+  // every wave is past its MFMAs) so that each lane finishes whole outputs:
+  // row rl = lane % 32 of the wave's 32, vectors lane / 32, + 2, ...  The
+  // three digit columns are combined once per output and each vector's 32
+  // rows leave as one 128-byte store.  Idle waves (rows past M) stay to the
+  // end for the block barriers.
+  __syncthreads();
+  int *accs = reinterpret_cast<int *>(lds_b) + wave * (NMAT * 16 * 64);
+  if (wave_ok) {
 #pragma unroll
-  for (int i = 0; i < NMAT; ++i)
+    for (int i = 0; i < NMAT; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int c0 = acc[i][r];
-      const int c1 = __shfl_down(c0, 1);
-      const int c2 = __shfl_down(c0, 2);
-      tot[i][r] = (long long)c0 + ((long long)c1 << 8) + ((long long)c2 << 16);
-    }
-  const int t = n / 3;
-  const bool owner = wave_ok && n - 3 * t == 0 && t < ti.ntok;
-  const int tc = min(t, ti.ntok - 1);
-  const int e = vexp[tc];
-  const long long qsum = (long long)vsum[tc];
-  const float *s0 = a.scale[0] + ti.expert * a.s_stride;
-  const float *s1 = a.scale[NMAT - 1] + ti.expert * a.s_stride;
-  uint32_t omax = 0;
-  if (owner) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int rl = 8 * (r >> 2) + 4 * h + (r & 3);
-      const int row = min(m0 + rl, a.M - 1);
-      float dot[NMAT];
-#pragma unroll
-      for (int i = 0; i < NMAT; ++i)
-        dot[i] = e == kBadExp ? __builtin_nanf("") : (float)ldexp((double)(tot[i][r] - qsum), -e);
-      float y;
-      if constexpr (NMAT == 1) {
-        y = dot[0] * s0[row];
-      } else {
-        const float g = dot[0] * s0[row];
-        const float u = dot[1] * s1[row];
-        y = (g * (1.0f / (1.0f + expf(-g)))) * u;
-      }
-      ostage[wave][t][rl] = y;
-      if (m0 + rl < a.M) omax = max(omax, __float_as_uint(y) & 0x7fffffffu);
-    }
+      for (int r = 0; r < 16; ++r) accs[(i * 16 + r) * 64 + lane] = acc[i][r];
   }
-  if (a.out_max && owner) atomicMax(&bmax[t], omax);  // LDS
-  // each vector's 32 rows leave as one 128-byte store (lanes 0..31); LDS
-  // operations of a wave complete in order, so the reads see the writes
-  if (wave_ok && lane < 32 && m0 + lane < a.M) {
-    for (int v = 0; v < ti.ntok; ++v)
-      a.out[(int64_t)vslot[v] * a.ld_out + m0 + lane] = ostage[wave][v][lane];
+  // accumulator element (row rl, column c) sits in register
+  // r = 4 (rl / 8) + rl % 4 of lane c + 32 ((rl / 4) % 2)
+  const int rl = lane & 31;
+  const int rr = 4 * (rl >> 3) + (rl & 3), lb = 32 * ((rl >> 2) & 1);
+  const int row = m0 + rl;
+  const bool row_live = wave_ok && row < a.M;
+  const int rowc = min(row, a.M - 1);
+  const float sc0 = a.scale[0][ti.expert * a.s_stride + rowc];
+  const float sc1 = a.scale[NMAT - 1][ti.expert * a.s_stride + rowc];
+  for (int t = lane >> 5; t < ti.ntok; t += 2) {
+    const int e = vexp[t];
+    const long long qsum = (long long)vsum[t];
+    float dot[NMAT];
+#pragma unroll
+    for (int i = 0; i < NMAT; ++i) {
+      const int *ar = accs + (i * 16 + rr) * 64 + lb + 3 * t;
+      const long long tot = (long long)ar[0] + ((long long)ar[1] << 8) + ((long long)ar[2] << 16);
+      dot[i] = e == kBadExp ? __builtin_nanf("") : (float)ldexp((double)(tot - qsum), -e);
+    }
+    float y;
+    if constexpr (NMAT == 1) {
+      y = dot[0] * sc0;
+    } else {
+      const float g = dot[0] * sc0;
+      const float u = dot[1] * sc1;
+      y = (g * (1.0f / (1.0f + expf(-g)))) * u;
+    }
+    if (row_live) {
+      a.out[(int64_t)vslot[t] * a.ld_out + row] = y;
+      if (a.out_max) atomicMax(&bmax[t], __float_as_uint(y) & 0x7fffffffu);  // LDS
+    }
   }
   if (a.out_max) {  // this block's partial maximum per vector, no global atomics
     __syncthreads();
@@ -439,10 +437,11 @@ __global__ __launch_bounds__(256) void k_packed_generic(PackedArgs a) {
 }
 
 // Gate logits, top-k and routing weights of one token per block
-// (src/moe.rs:51-82): logits over every expert (16 waves, one expert per
-// wave at a time, 8 independent 16-byte loads per lane in flight), rank by
-// (logit desc, index asc) -- the order of the reference's stable descending
-// sort -- softmax over all experts, top_k weights.
+// (src/moe.rs:51-82): logits over every expert (16 waves, two experts per
+// wave at a time with all their loads in flight together), rank by (logit
+// desc, index asc) -- the order of the reference's stable descending sort --,
+// softmax over all experts, top_k weights.  Also the largest |x| (f32 bits)
+// of the token, for the expert GEMVs' quantisation.
 __global__ __launch_bounds__(1024) void k_moe_route(const float *__restrict__ xs,
                                                     const float *__restrict__ gw, int E, int H,
                                                     int topk, int32_t *__restrict__ sel,
@@ -451,67 +450,79 @@ __global__ __launch_bounds__(1024) void k_moe_route(const float *__restrict__ xs
                                                     float *__restrict__ user_w,
                                                     uint32_t *__restrict__ xmax) {
   __shared__ float lg[kMaxExperts];
-  __shared__ float red[16];
-  __shared__ uint32_t bmax;
+  __shared__ float stat[2];
   const int t = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const float *x = xs + (int64_t)t * H;
-  // largest |x| (f32 bits) of the token for the expert GEMVs' quantisation
-  if (threadIdx.x == 0) bmax = 0;
-  __syncthreads();
-  {
-    uint32_t m = 0;
-    for (int k = threadIdx.x; k < H; k += 1024) m = max(m, __float_as_uint(x[k]) & 0x7fffffffu);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o));
-    if (lane == 0) atomicMax(&bmax, m);
-  }
   const bool vec = (H & 3) == 0 && (((uintptr_t)xs | (uintptr_t)gw) & 15) == 0;
-  for (int e = wave; e < E; e += 16) {
-    const float *w = gw + (int64_t)e * H;
-    float s = 0.f;
+  uint32_t xm = 0;
+  for (int e0 = wave; e0 < E; e0 += 32) {
+    const int e1 = e0 + 16;
+    const float *w0 = gw + (int64_t)e0 * H;
+    const float *w1 = gw + (int64_t)min(e1, E - 1) * H;
+    float s0 = 0.f, s1 = 0.f;
     if (vec) {
       const int H4 = H >> 2;
       constexpr int U = 8;
       for (int base = 0; base < H4; base += 64 * U) {
-        floatx4_t xv[U], wv[U];
+        floatx4_t xv[U], a0[U], a1[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           const int i = min(base + lane + 64 * u, H4 - 1);  // branch-free loads
           xv[u] = reinterpret_cast<const floatx4_t *>(x)[i];
-          wv[u] = reinterpret_cast<const floatx4_t *>(w)[i];
+          a0[u] = reinterpret_cast<const floatx4_t *>(w0)[i];
+          a1[u] = reinterpret_cast<const floatx4_t *>(w1)[i];
         }
 #pragma unroll
         for (int u = 0; u < U; ++u)
-          if (base + lane + 64 * u < H4)
-            s += xv[u][0] * wv[u][0] + xv[u][1] * wv[u][1] + xv[u][2] * wv[u][2] +
-                 xv[u][3] * wv[u][3];
+          if (base + lane + 64 * u < H4) {
+            s0 += xv[u][0] * a0[u][0] + xv[u][1] * a0[u][1] + xv[u][2] * a0[u][2] +
+                  xv[u][3] * a0[u][3];
+            s1 += xv[u][0] * a1[u][0] + xv[u][1] * a1[u][1] + xv[u][2] * a1[u][2] +
+                  xv[u][3] * a1[u][3];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xm = max(xm, __float_as_uint(xv[u][j]) & 0x7fffffffu);
+          }
       }
     } else {
-      for (int k = lane; k < H; k += 64) s += x[k] * w[k];
+      for (int k = lane; k < H; k += 64) {
+        s0 += x[k] * w0[k];
+        s1 += x[k] * w1[k];
+        xm = max(xm, __float_as_uint(x[k]) & 0x7fffffffu);
+      }
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
-    if (lane == 0) lg[e] = s;
+    for (int o = 32; o > 0; o >>= 1) {
+      s0 += __shfl_xor(s0, o);
+      s1 += __shfl_xor(s1, o);
+    }
+    if (lane == 0) {
+      lg[e0] = s0;
+      if (e1 < E) lg[e1] = s1;
+    }
+  }
+  if (wave == 0) {  // wave 0 read all of x in its first pass (E >= 1)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) xm = max(xm, (uint32_t)__shfl_xor((int)xm, o));
+    if (lane == 0) xmax[t] = xm;
   }
   __syncthreads();
-  float mx = -INFINITY;
-  for (int e = threadIdx.x; e < E; e += 1024) mx = fmaxf(mx, lg[e]);
+  if (wave == 0) {
+    float mx = -INFINITY;
+    for (int e = lane; e < E; e += 64) mx = fmaxf(mx, lg[e]);
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-  if (lane == 0) red[wave] = mx;
-  __syncthreads();
-  mx = red[0];
-  for (int i = 1; i < 16; ++i) mx = fmaxf(mx, red[i]);
-  __syncthreads();
-  float se = 0.f;
-  for (int e = threadIdx.x; e < E; e += 1024) se += expf(lg[e] - mx);
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    float se = 0.f;
+    for (int e = lane; e < E; e += 64) se += expf(lg[e] - mx);
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) se += __shfl_xor(se, o);
-  if (lane == 0) red[wave] = se;
+    for (int o = 32; o > 0; o >>= 1) se += __shfl_xor(se, o);
+    if (lane == 0) {
+      stat[0] = mx;
+      stat[1] = se;
+    }
+  }
   __syncthreads();
-  se = 0.f;
-  for (int i = 0; i < 16; ++i) se += red[i];
+  const float mx = stat[0], se = stat[1];
   // NaN logits rank as -inf, so the ranks stay a permutation of 0..E-1
   // and every (token, rank < top_k) entry is written exactly once.
   for (int e = threadIdx.x; e < E; e += 1024) {
@@ -530,7 +541,6 @@ __global__ __launch_bounds__(1024) void k_moe_route(const float *__restrict__ xs
       if (user_w) user_w[o] = w;
     }
   }
-  if (threadIdx.x == 0) xmax[t] = bmax;
 }
 
 // Exclusive prefix sum over a 1024-thread block (one value per thread).
@@ -640,7 +650,11 @@ bool mfma_ok(int32_t K) { return K > 0 && K % 128 == 0 && K <= kMaxK; }
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
-size_t mfma_lds_bytes(int32_t K) { return (size_t)std::min(K, kSlab) * 32; }
+// B operand slab, reused by the epilogue for the accumulators (4 waves x
+// NMAT x 16 registers x 64 lanes x 4 bytes)
+size_t mfma_lds_bytes(int32_t K, int nmat) {
+  return std::max((size_t)std::min(K, kSlab) * 32, (size_t)kMfmaWaves * nmat * 16 * 64 * 4);
+}
 
 int mfma_row_blocks(int32_t M) { return (M + 32 * kMfmaWaves - 1) / (32 * kMfmaWaves); }
 
@@ -648,10 +662,10 @@ constexpr int64_t kMaxTileGrid = 65535;  // grid y limit
 
 template <int NMAT, int NG>
 qmla_status launch_mfma(const PackedArgs &a, int64_t tile_grid, hipStream_t s) {
-  const size_t lds = mfma_lds_bytes(a.K);
+  const size_t lds = mfma_lds_bytes(a.K, NMAT);
   QMLA_TRY(ensure_dynamic_lds((const void *)k_packed_mfma<NMAT, NG>, lds));
   const dim3 grid(mfma_row_blocks(a.M), (unsigned)tile_grid);
-  hipLaunchKernelGGL((k_packed_mfma<NMAT, NG>), grid, dim3(256), lds, s, a);
+  hipLaunchKernelGGL((k_packed_mfma<NMAT, NG>), grid, dim3(kMfmaThreads), lds, s, a);
   QMLA_LAUNCH_CHECK("k_packed_mfma");
   return QMLA_OK;
 }
