@@ -155,6 +155,28 @@ def test_moe_forward_reference_bench_layer(qmla_gpu):
     check_moe(qmla_gpu, W, O.bench_moe_input(16, 2048), "reference bench layer")
 
 
+@pytest.mark.parametrize("E,k,H,I,T", [
+    (4, 2, 4352, 256, 3),     # hidden past one 4096-code LDS slab: ring path, two slabs
+    (1, 1, 128, 128, 1),      # one expert, one token
+    (3, 1, 512, 1152, 2)])    # intermediate 1152: ring path for the down GEMV
+def test_moe_forward_other_paths(qmla_gpu, E, k, H, I, T):
+    W = O.random_moe_weights(E, k, H, I, 3000 + H)
+    check_moe(qmla_gpu, W, O.normal((T, H), 3100 + T), f"E={E} k={k} H={H} I={I} T={T}")
+
+
+def test_moe_nonfinite_token_stays_in_its_row(qmla_gpu):
+    """A NaN activation poisons its own token's output only."""
+    q = qmla_gpu
+    W = O.random_moe_weights(8, 2, 256, 256, 41)
+    xs = O.normal((4, 256), 42)
+    xs[2, 5] = np.nan
+    out = moe_layer(q, W).forward(xs)
+    assert np.isnan(out[2]).all()
+    ref = O.moe_forward(W, xs)
+    keep = [0, 1, 3]
+    assert rel_err(out[keep], ref[keep]) < TOL
+
+
 def test_moe_ties_pick_lowest_indices(qmla_gpu):
     W = O.random_moe_weights(6, 2, 128, 128, 5)
     W.gate_weight[:] = 0.0
