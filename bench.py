@@ -447,7 +447,8 @@ def main():
             **moe,
             "roofline": {"bound": "hbm", "achieved": moe["tb_s"] * 1e3, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": moe["hbm_frac"],
-                         "kernel": "whole qmla_moe_forward call (route, bin, quantize, gate/up, down, combine)",
+                         "kernel": "whole qmla_moe_forward call (k_moe_route, k_moe_bin, k_packed_mfma gate/up "
+                                   "and down, k_moe_combine), HIP events on the launch stream",
                          "bytes_per_launch": moe["bytes_per_step"]},
             "cpu_baseline": None if args.no_cpu_baseline else moe_cpu_baseline()}
         log("moe layer", json.dumps(secondary["moe_layer"]))
