@@ -48,6 +48,20 @@ def test_packed_forward_fallback_is_bit_exact(qmla_gpu, out_f, in_f, batch):
     np.testing.assert_array_equal(got, O.packed_forward(p, s, out_f, in_f, x))
 
 
+def test_packed_forward_unaligned_input_uses_fallback(qmla_gpu):
+    """x not 16-byte aligned: the fallback kernel runs (bit-exact with the
+    oracle) instead of the MFMA kernel's 16-byte loads."""
+    q = qmla_gpu
+    p, s = rand_packed(64, 256, 31)
+    x = O.normal((3, 256), 32)
+    t = q.PackedQMoETensor.from_bytes(p, (64, 256), s)
+    buf = q.DeviceBuffer.from_numpy(np.concatenate([np.zeros(1, np.float32), x.reshape(-1)]))
+    out = q.DeviceBuffer(3 * 64 * 4)
+    t.forward(buf.ptr + 4, 3, out)
+    q.check(q.lib().qmla_stream_synchronize(None))
+    np.testing.assert_array_equal(out.to_numpy(np.float32, (3, 64)), O.packed_forward(p, s, 64, 256, x))
+
+
 def test_packed_forward_simd_kat(qmla_gpu):
     """src/simd.rs:51-65 through the device path."""
     t = qmla_gpu.PackedQMoETensor.from_bytes(np.array([[0x58]], np.uint8), (1, 4), np.array([1.5], np.float32))
