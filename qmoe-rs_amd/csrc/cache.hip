@@ -201,9 +201,11 @@ qmla_status qmla_cache_create(int32_t num_seqs, const int32_t *capacity, int32_t
   QMLA_REQUIRE(valid_dtype(dtype), QMLA_ERR_INVALID_ARG, "bad dtype %d", (int)dtype);
   QMLA_REQUIRE((kv_lora_rank + rope_dim) % 8 == 0, QMLA_ERR_UNSUPPORTED,
                "row width %d must be a multiple of 8", kv_lora_rank + rope_dim);
+  int device = 0;
+  QMLA_HIP(hipGetDevice(&device));
   qmla_kv_cache *c = new (std::nothrow) qmla_kv_cache();
   QMLA_REQUIRE(c, QMLA_ERR_OOM, "host allocation failed");
-  QMLA_HIP(hipGetDevice(&c->device));
+  c->device = device;
   c->num_seqs = num_seqs;
   c->r = kv_lora_rank;
   c->dr = rope_dim;
