@@ -31,6 +31,7 @@ on a bounded sample (>= 10 s), scaled to the full batch.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
        python bench.py --calibrate   (copy kernel for scaling PMC counters)
        python bench.py --moe-only    (the MoE layer line alone, for profiling)
+       python bench.py --layer-only  (the MLA layer decode step alone, for profiling)
 """
 from __future__ import annotations
 
@@ -390,6 +391,8 @@ def main():
                     help="only run the copy kernel used to scale the PMC byte counters")
     ap.add_argument("--moe-only", action="store_true",
                     help="only run the 2-bit packed MoE layer line (for profiling)")
+    ap.add_argument("--layer-only", action="store_true",
+                    help="only run the MLA layer decode step line (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the decode path shards by batch "
@@ -405,6 +408,10 @@ def main():
     if args.moe_only:
         mb = MoEBench(stream)
         print(json.dumps({"moe_layer": mb.run(args.steps, args.warmup)}), flush=True)
+        return
+    if args.layer_only:
+        lb = LayerDecodeBench(stream, seed=51)
+        print(json.dumps({"layer_decode_step": lb.run(args.steps, args.warmup)}), flush=True)
         return
 
     lens = synth.v3_decode_lengths()
