@@ -42,9 +42,6 @@ constexpr int kMfmaThreads = 64 * kMfmaWaves;
 constexpr int kMaxExperts = 4096;
 constexpr int kMaxK = 1 << 20;
 
-struct TileDesc {
-  int32_t expert, start, count, pad;
-};
 
 struct PackedArgs {
   const uint8_t *w[2];      // packed [experts][M][K / 4]
@@ -55,8 +52,8 @@ struct PackedArgs {
   const float *x;           // [vectors][ld_x] f32
   int64_t ld_x;
   int32_t src_div;          // source vector of slot s = s / src_div
-  const TileDesc *tiles;    // null: implicit tiles of kTokTile over `count` slots
-  const int32_t *ntiles;
+  const int2 *ebin;         // per expert {first bin position, pairs} (grid y = expert);
+                            //   null: grid y = tiles of kTokTile over `count` slots
   const int32_t *slots;     // bin position -> slot (null: identity)
   int32_t count;
   float *out;               // out[slot * ld_out + row]
@@ -71,16 +68,22 @@ struct TileInfo {
   int expert, start, ntok;
 };
 
-__device__ __forceinline__ bool load_tile(const PackedArgs &a, TileInfo &t) {
-  const int y = blockIdx.y;
-  if (a.tiles) {
-    if (y >= *a.ntiles) return false;
-    const TileDesc d = a.tiles[y];
-    t = TileInfo{d.expert, d.start, d.count};
+// The block's expert and its bin range [first, first + count): with bins,
+// grid y is the expert and the block walks all of its tiles; without, grid y
+// is one tile of the `count` slots.
+__device__ __forceinline__ int block_expert(const PackedArgs &a) {
+  return a.ebin ? (int)blockIdx.y : 0;
+}
+
+__device__ __forceinline__ void block_range(const PackedArgs &a, int &first, int &count) {
+  if (a.ebin) {
+    const int2 eb = a.ebin[blockIdx.y];
+    first = eb.x;
+    count = eb.y;
   } else {
-    t = TileInfo{0, y * kTokTile, min(kTokTile, a.count - y * kTokTile)};
+    first = blockIdx.y * kTokTile;
+    count = min(kTokTile, a.count - first);
   }
-  return t.ntok > 0;
 }
 
 template <int N>
@@ -102,7 +105,9 @@ constexpr int kBadExp = 0x7fffffff;  // exponent marking a vector with inf/NaN
 
 // Expert GEMV over one tile of vectors.  NMAT = 1: out = dot * scale.
 // NMAT = 2 (gate, up): out = swish(dot_0 * s_0) * (dot_1 * s_1)
-// (src/moe.rs:102-115).  Block: 4 waves x 32 rows; grid (row blocks, tiles).
+// (src/moe.rs:102-115).  Block: 4 waves x 32 rows; grid (row blocks,
+// experts) with each block walking its expert's tiles, or (row blocks,
+// tiles) without bins.
 // The block turns its <= 10 f32 vectors into digit planes itself: pass 1
 // finds each vector's largest magnitude (its exponent e) unless the producer
 // handed it over (src_max), pass 2 writes the digits of each slab of K into
@@ -119,8 +124,6 @@ __global__ __launch_bounds__(kMfmaThreads) void k_packed_mfma(PackedArgs a) {
   __shared__ int vexp[kTokTile];
   __shared__ unsigned long long vsum[kTokTile];
   __shared__ unsigned bmax[kTokTile];
-  TileInfo ti;
-  if (!load_tile(a, ti)) return;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, h = lane >> 5;
@@ -128,20 +131,40 @@ __global__ __launch_bounds__(kMfmaThreads) void k_packed_mfma(PackedArgs a) {
   const bool wave_ok = m0 < a.M;
   const bool row_ok = m0 + n < a.M;
   const int bpr = a.K >> 2;
+  const int expert = block_expert(a);
   const uint8_t *wp[NMAT];
 #pragma unroll
   for (int i = 0; i < NMAT; ++i)
-    wp[i] = a.w[i] + ti.expert * a.w_stride + (int64_t)(row_ok ? m0 + n : 0) * bpr + 16 * h;
+    wp[i] = a.w[i] + expert * a.w_stride + (int64_t)(row_ok ? m0 + n : 0) * bpr + 16 * h;
 
   // Loads are branch-free (rows past M read row 0, ring slots past the slab
   // re-read its last group; neither result is used) so that the compiler
-  // keeps them in flight instead of waiting behind each branch.
+  // keeps them in flight instead of waiting behind each branch.  The first
+  // groups are requested before the block knows its tokens: the expert is
+  // the grid position, so the weight stream starts while the bins are read.
   constexpr int D = 4;
   constexpr int PD = NMAT == 1 ? 8 : 6;  // groups in flight, fixed group count
   constexpr int NR = NG > 0 ? (NG < PD ? NG : PD) : D;
   u32x4_t ring[NR][NMAT];
-  {
-    const int ng0 = min(kSlab, a.K) >> 7;
+  const int ng0 = min(kSlab, a.K) >> 7;
+#pragma unroll
+  for (int d = 0; d < NR; ++d)
+#pragma unroll
+    for (int i = 0; i < NMAT; ++i)
+      ring[d][i] = gload16(wp[i] + (NG > 0 ? d : min(d, ng0 - 1)) * 32);
+
+  int first, count;
+  block_range(a, first, count);
+  if (count <= 0) {  // an expert no token chose: drain the requested groups
+    wait_vm<0>();
+    return;
+  }
+  for (int tt = 0; tt < count; tt += kTokTile) {
+  const TileInfo ti{expert, first + tt, min(kTokTile, count - tt)};
+  if (tt > 0) {
+    // next tile of the same expert: the LDS of the last one is free once
+    // every wave is past its epilogue; its weights come again (from L2)
+    __syncthreads();
 #pragma unroll
     for (int d = 0; d < NR; ++d)
 #pragma unroll
@@ -366,8 +389,8 @@ __global__ __launch_bounds__(kMfmaThreads) void k_packed_mfma(PackedArgs a) {
   const int row = m0 + rl;
   const bool row_live = wave_ok && row < a.M;
   const int rowc = min(row, a.M - 1);
-  const float sc0 = a.scale[0][ti.expert * a.s_stride + rowc];
-  const float sc1 = a.scale[NMAT - 1][ti.expert * a.s_stride + rowc];
+  const float sc0 = a.scale[0][expert * a.s_stride + rowc];
+  const float sc1 = a.scale[NMAT - 1][expert * a.s_stride + rowc];
   for (int t = lane >> 5; t < ti.ntok; t += 2) {
     const int e = vexp[t];
     const long long qsum = (long long)vsum[t];
@@ -395,6 +418,7 @@ __global__ __launch_bounds__(kMfmaThreads) void k_packed_mfma(PackedArgs a) {
     __syncthreads();
     if (tid < ti.ntok) a.out_max[(int64_t)vslot[tid] * gridDim.x + blockIdx.x] = bmax[tid];
   }
+  }  // tiles of the block
 }
 
 // Fallback for in_features that are not a multiple of 128: one thread per
@@ -402,11 +426,12 @@ __global__ __launch_bounds__(kMfmaThreads) void k_packed_mfma(PackedArgs a) {
 // separate multiply and add), so its results are those of the reference.
 template <int NMAT>
 __global__ __launch_bounds__(256) void k_packed_generic(PackedArgs a) {
-  TileInfo ti;
-  if (!load_tile(a, ti)) return;
+  int first, count;
+  block_range(a, first, count);
   const int row = blockIdx.x * 256 + threadIdx.x;
   if (row >= a.M) return;
   const int bpr = a.K >> 2;
+  const TileInfo ti{block_expert(a), first, count};
   for (int t = 0; t < ti.ntok; ++t) {
     const int pos = ti.start + t;
     const int slot = a.slots ? a.slots[pos] : pos;
@@ -561,11 +586,11 @@ __device__ long long block_scan1024(long long v, long long *tmp) {
 }
 
 // Token binning (src/moe.rs:56-82 expert_bins): per-expert counts, bin
-// offsets, tiles of <= kTokTile pairs and the pair -> slot list.  Order
-// within a bin does not change any result (each pair is computed alone).
+// offsets ({first, count} per expert) and the bin position -> slot list.
+// Order within a bin does not change any result (each pair is computed
+// alone).
 __global__ __launch_bounds__(1024) void k_moe_bin(const int32_t *__restrict__ sel, int npairs,
-                                                  int E, TileDesc *__restrict__ tiles,
-                                                  int32_t *__restrict__ ntiles,
+                                                  int E, int2 *__restrict__ ebin,
                                                   int32_t *__restrict__ pair_slot) {
   __shared__ int cnt[kMaxExperts];
   __shared__ int cur[kMaxExperts];
@@ -579,28 +604,23 @@ __global__ __launch_bounds__(1024) void k_moe_bin(const int32_t *__restrict__ se
   __syncthreads();
   // thread j owns experts 4j .. 4j + 3 (E <= 4096)
   long long mine = 0;
-  int c4[4], t4[4];
+  int c4[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = 4 * threadIdx.x + i;
     c4[i] = e < E ? cnt[e] : 0;
-    t4[i] = (c4[i] + kTokTile - 1) / kTokTile;
-    mine += (long long)c4[i] | ((long long)t4[i] << 32);
+    mine += c4[i];
   }
-  long long base = block_scan1024(mine, tmp);
-  int off = (int)(base & 0xffffffffLL), toff = (int)(base >> 32);
+  int off = (int)block_scan1024(mine, tmp);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = 4 * threadIdx.x + i;
     if (e < E) {
       cur[e] = off;
-      for (int j = 0; j < t4[i]; ++j)
-        tiles[toff + j] = TileDesc{e, off + j * kTokTile, min(kTokTile, c4[i] - j * kTokTile), 0};
+      ebin[e] = int2{off, c4[i]};
     }
     off += c4[i];
-    toff += t4[i];
   }
-  if (threadIdx.x == 1023) *ntiles = toff;
   __syncthreads();
   for (int p = threadIdx.x; p < npairs; p += 1024) {
     const int e = sel[p];
@@ -674,7 +694,7 @@ template <int NMAT>
 qmla_status launch_packed(const PackedArgs &a, int64_t tile_grid, bool mfma, hipStream_t s) {
   if (tile_grid <= 0 || a.M <= 0) return QMLA_OK;
   QMLA_REQUIRE(tile_grid <= kMaxTileGrid, QMLA_ERR_UNSUPPORTED,
-               "%lld vector tiles in one call (at most %lld)", (long long)tile_grid,
+               "grid of %lld tiles or experts (at most %lld)", (long long)tile_grid,
                (long long)kMaxTileGrid);
   if (mfma) {
     // whole-K prefetch for the common widths (NMAT x NG x 16 B a lane)
@@ -702,15 +722,13 @@ qmla_status check_packed_dims(int32_t out_f, int32_t in_f, int32_t batch) {
 }
 
 struct MoeWs {
-  size_t sel, selw, ntiles, tiles, slots, xmax, hmax, h, y, total;
-  int64_t tile_bound;
+  size_t sel, selw, ebin, slots, xmax, hmax, h, y, total;
 };
 
 MoeWs moe_ws(const qmla_moe_config &c, int32_t T) {
   const int64_t P = (int64_t)T * c.top_k;
   const int64_t H = c.hidden_dim, I = c.intermediate_dim;
   MoeWs w{};
-  w.tile_bound = P / kTokTile + std::min<int64_t>(c.num_experts, P);
   size_t o = 0;
   auto take = [&](size_t bytes) {
     const size_t at = o;
@@ -719,8 +737,7 @@ MoeWs moe_ws(const qmla_moe_config &c, int32_t T) {
   };
   w.sel = take(sizeof(int32_t) * P);
   w.selw = take(sizeof(float) * P);
-  w.ntiles = take(sizeof(int32_t));
-  w.tiles = take(sizeof(TileDesc) * w.tile_bound);
+  w.ebin = take(sizeof(int2) * c.num_experts);
   w.slots = take(sizeof(int32_t) * P);
   w.xmax = take(sizeof(uint32_t) * T);
   w.hmax = take(sizeof(uint32_t) * P * mfma_row_blocks(I));
@@ -822,16 +839,13 @@ qmla_status qmla_moe_forward(const qmla_moe_config *cfg, const float *xs, int32_
                    down_packed && down_scales,
                QMLA_ERR_INVALID_ARG, "null weight pointer");
   const MoeWs w = moe_ws(c, T);
-  QMLA_REQUIRE(w.tile_bound <= kMaxTileGrid, QMLA_ERR_UNSUPPORTED,
-               "seq_len x top_k too large for one call (%lld tiles)", (long long)w.tile_bound);
   QMLA_REQUIRE(workspace != nullptr && workspace_bytes >= w.total, QMLA_ERR_WORKSPACE,
                "workspace of %zu bytes, %zu needed", workspace_bytes, w.total);
   char *ws = static_cast<char *>(workspace);
   auto at = [&](size_t off) { return static_cast<void *>(ws + off); };
   int32_t *sel = static_cast<int32_t *>(at(w.sel));
   float *selw = static_cast<float *>(at(w.selw));
-  int32_t *ntiles = static_cast<int32_t *>(at(w.ntiles));
-  TileDesc *tiles = static_cast<TileDesc *>(at(w.tiles));
+  int2 *ebin = static_cast<int2 *>(at(w.ebin));
   int32_t *slots = static_cast<int32_t *>(at(w.slots));
   float *hbuf = static_cast<float *>(at(w.h));
   float *ybuf = static_cast<float *>(at(w.y));
@@ -842,8 +856,7 @@ qmla_status qmla_moe_forward(const qmla_moe_config *cfg, const float *xs, int32_
   hipLaunchKernelGGL(k_moe_route, dim3(T), dim3(1024), 0, s, xs, gate_weight, c.num_experts, H,
                      c.top_k, sel, selw, top_experts, top_weights, xmax);
   QMLA_LAUNCH_CHECK("k_moe_route");
-  hipLaunchKernelGGL(k_moe_bin, dim3(1), dim3(1024), 0, s, sel, P, c.num_experts, tiles, ntiles,
-                     slots);
+  hipLaunchKernelGGL(k_moe_bin, dim3(1), dim3(1024), 0, s, sel, P, c.num_experts, ebin, slots);
   QMLA_LAUNCH_CHECK("k_moe_bin");
 
   const bool fast_gu = mfma_ok(H) && aligned16(gate_packed) && aligned16(up_packed) &&
@@ -861,15 +874,14 @@ qmla_status qmla_moe_forward(const qmla_moe_config *cfg, const float *xs, int32_
   gu.x = xs;
   gu.ld_x = H;
   gu.src_div = c.top_k;
-  gu.tiles = tiles;
-  gu.ntiles = ntiles;
+  gu.ebin = ebin;
   gu.slots = slots;
   gu.out = hbuf;
   gu.ld_out = I;
   gu.src_max = xmax;
   gu.src_max_parts = 1;
   gu.out_max = fast_gu && fast_dn ? hmax : nullptr;
-  QMLA_TRY(launch_packed<2>(gu, w.tile_bound, fast_gu, s));
+  QMLA_TRY(launch_packed<2>(gu, c.num_experts, fast_gu, s));
 
   PackedArgs dn = gu;
   dn.w[0] = dn.w[1] = down_packed;
@@ -886,7 +898,7 @@ qmla_status qmla_moe_forward(const qmla_moe_config *cfg, const float *xs, int32_
   dn.src_max = fast_gu && fast_dn ? hmax : nullptr;
   dn.src_max_parts = mfma_row_blocks(I);
   dn.out_max = nullptr;
-  QMLA_TRY(launch_packed<1>(dn, w.tile_bound, fast_dn, s));
+  QMLA_TRY(launch_packed<1>(dn, c.num_experts, fast_dn, s));
 
   hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, s, ybuf,
                      sel, selw, T, c.top_k, H, out);
