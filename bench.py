@@ -363,10 +363,10 @@ def copy_calibration(stream, n=256 << 20, reps=4):
         f"({4 * n} bytes read, {2 * n} bytes written per launch)")
 
 
-def measured_traffic():
-    """HBM bytes per decode step from the committed rocprofv3 PMC summary
-    (counter reads scaled by the copy calibration), or None."""
-    path = os.path.join(ROOT, "profiles", "decode_v3_pmc.md")
+def measured_traffic(name="decode_v3_pmc.md"):
+    """HBM bytes per step from a committed rocprofv3 PMC summary (counter
+    reads scaled by the copy calibration), or None."""
+    path = os.path.join(ROOT, "profiles", name)
     try:
         with open(path) as f:
             for line in f:
@@ -453,7 +453,7 @@ def main():
                         "2-bit packed experts (reference bench pattern), f32 activations, int8 MFMA",
             **moe,
             "roofline": {"bound": "hbm", "achieved": moe["tb_s"] * 1e3, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": moe["hbm_frac"],
+                         "frac": moe["hbm_frac"], "traffic": measured_traffic("moe_layer_kernel_trace.md"),
                          "kernel": "whole qmla_moe_forward call (k_moe_route, k_moe_bin, k_packed_mfma gate/up "
                                    "and down, k_moe_combine), HIP events on the launch stream",
                          "bytes_per_launch": moe["bytes_per_step"]},
