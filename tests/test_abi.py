@@ -67,3 +67,23 @@ def test_oracle_library_builds_and_loads():
     import oracle
     oracle.build(force=False)
     assert oracle.lib().orc_tile_size(2049) == 16
+
+
+def test_packed_and_moe_argument_checks_without_a_device():
+    """qmla_packed_forward / qmla_moe_forward validate sizes on the host and
+    report their workspace (none for the packed GEMV) without a device."""
+    L = qmla.lib()
+    n = C.c_size_t(123)
+    assert L.qmla_packed_forward_workspace_bytes(64, 2048, 16, C.byref(n)) == 0 and n.value == 0
+    assert L.qmla_packed_forward_workspace_bytes(64, -4, 16, C.byref(n)) == 2
+    assert L.qmla_packed_forward_workspace_bytes(64, (1 << 20) + 4, 1, C.byref(n)) == 3
+    cfg = qmla.MoEConfig(32, 4, 2048, 1408)
+    assert L.qmla_moe_workspace_bytes(C.byref(cfg), 16, C.byref(n)) == 0
+    # routing, bins, h [64, 1408] and y [64, 2048] in f32 at least
+    assert n.value >= 4 * 64 * (1408 + 2048)
+    assert L.qmla_moe_workspace_bytes(C.byref(qmla.MoEConfig(4, 5, 64, 64)), 2, C.byref(n)) == 2
+    assert b"top_k" in L.qmla_last_error()
+    assert L.qmla_moe_workspace_bytes(C.byref(qmla.MoEConfig(5000, 2, 64, 64)), 2, C.byref(n)) == 3
+    assert L.qmla_moe_workspace_bytes(None, 2, C.byref(n)) == 1
+    # a zero-length call is a no-op that needs no pointers
+    assert L.qmla_moe_forward(C.byref(cfg), None, 0, *([None] * 11), 0, None) == 0
