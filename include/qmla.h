@@ -262,10 +262,13 @@ QMLA_API qmla_status qmla_layer_workspace_bytes(const qmla_layer *layer, const q
                                        int32_t batch, int32_t seq, size_t *bytes);
 /* MlaAttention::forward_with_cache, src/model.rs:256-307, over the latent
  * cache: xs [batch, seq, hidden] f32 device, out [batch, seq, hidden] f32.
- * Appends the seq new latent rows of sequences 0..batch-1 to the cache
- * (positions continue from each sequence's current length, which must be
- * equal across the batch as in the reference's uniform KVCache), then
- * attends all cached + new tokens without a mask (as :297-302).
+ * Appends the seq new latent rows of sequences 0..batch-1 to the cache and
+ * attends all cached + new tokens without a mask (as :297-302).  Lengths
+ * may differ across the batch (a ragged batch; the reference's KVCache is
+ * uniform, :259): sequence b's new tokens take RoPE positions len_b + i,
+ * read from the cache's device length table, so the call needs no host
+ * copy of the lengths.  Every argument, shape and workspace check runs
+ * before the cache is modified: a rejected call leaves it unchanged.
  * f32 cache: f32 throughout.  bf16 cache: the new rows are stored rounded
  * to bf16 and the attention core is the bf16 MFMA decode (kv_lora_rank /
  * rope 512/64, 128/32 or 64/16; other shapes return QMLA_ERR_UNSUPPORTED);
@@ -281,6 +284,29 @@ QMLA_API qmla_status qmla_layer_forward_prefill(const qmla_layer *layer, const f
                                        int32_t seq, qmla_kv_cache *cache, float *out,
                                        void *workspace, size_t workspace_bytes,
                                        qmla_stream stream);
+
+/* The public tensors of KVCache, src/model.rs:88-92 ({k, v, k_rope}, read
+ * and written directly by benches/attention.rs:68-70,256), rebuilt from the
+ * latent rows through the layer's kv_b_proj (compute_kv, :178-190):
+ *   k      [n_seqs, H, T, qk_nope]  = c W_UK^h^T + b_K^h
+ *   v      [n_seqs, H, T, v_dim]    = c W_UV^h^T + b_V^h
+ *   k_rope [n_seqs, H, T, qk_rope]  = the stored roped k_pe, broadcast to
+ *                                     every head (:217-219)
+ * for sequences seq0 .. seq0 + n_seqs - 1, which must share one length T
+ * (a KVCache tensor has one T; materialise a ragged cache one sequence at a
+ * time).  f32 device outputs; any of k, v, k_rope may be NULL to skip it.
+ * A bf16 cache needs a workspace of n_seqs * T * kv_lora_rank floats for
+ * the widened latent (the size query says so; an f32 cache needs none).
+ * The writes are O(T * H * (dn + dv + dr)) per sequence: this is the
+ * legacy path for callers that read the decompressed tensors, not the
+ * decode path. */
+QMLA_API qmla_status qmla_cache_materialise_workspace_bytes(const qmla_layer *layer,
+                                                   const qmla_kv_cache *cache, int32_t seq0,
+                                                   int32_t n_seqs, size_t *bytes);
+QMLA_API qmla_status qmla_cache_materialise(const qmla_layer *layer, const qmla_kv_cache *cache,
+                                   int32_t seq0, int32_t n_seqs, float *k, float *v,
+                                   float *k_rope, void *workspace, size_t workspace_bytes,
+                                   qmla_stream stream);
 
 /* ------------------------------------ 2-bit packed MoE (tensor.rs, moe.rs)
  * Packed format (src/simd.rs:20-31): an [out_features, in_features] tensor

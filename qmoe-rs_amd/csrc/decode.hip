@@ -312,6 +312,19 @@ qmla_status launch_decode_merge(int32_t batch, int32_t rows, int32_t r, DecodePl
   return QMLA_OK;
 }
 
+qmla_status decode_shape_supported(const qmla_kv_cache *c, int32_t rows) {
+  if (c->dtype == QMLA_BF16) {
+    QMLA_REQUIRE(decode_mfma_supported(rows, c->r, c->dr), QMLA_ERR_UNSUPPORTED,
+                 "bf16 decode for kv_lora_rank %d, rope %d", c->r, c->dr);
+    QMLA_REQUIRE(rows <= 65535 * 128, QMLA_ERR_SHAPE, "too many query rows");
+    return QMLA_OK;
+  }
+  QMLA_REQUIRE(c->r <= kF32Threads * kColsPerThread, QMLA_ERR_UNSUPPORTED,
+               "kv_lora_rank %d > %d", c->r, kF32Threads * kColsPerThread);
+  QMLA_REQUIRE(rows <= 65535, QMLA_ERR_SHAPE, "rows %d > 65535", rows);
+  return QMLA_OK;
+}
+
 qmla_status launch_decode_f32(const DecodeArgs &a, hipStream_t stream) {
   QMLA_REQUIRE(a.r <= kF32Threads * kColsPerThread, QMLA_ERR_UNSUPPORTED,
                "kv_lora_rank %d > %d", a.r, kF32Threads * kColsPerThread);

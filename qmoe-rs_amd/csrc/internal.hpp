@@ -100,6 +100,9 @@ constexpr int32_t kMaxPlanBlocks = 8192;
 qmla_status launch_decode_f32(const DecodeArgs &a, hipStream_t stream);
 qmla_status launch_decode_mfma(const DecodeArgs &a, hipStream_t stream);
 bool decode_mfma_supported(int32_t rows, int32_t r, int32_t dr);
+// Whether a decode with `rows` query rows per sequence over cache `c` has a
+// core (bf16 MFMA shapes, f32 width and row limits); checks no lengths.
+qmla_status decode_shape_supported(const qmla_kv_cache *c, int32_t rows);
 // Pieces per compute unit the MFMA decode kernel runs concurrently.
 bool decode_narrow_path(int32_t rows, int32_t r, int32_t dr);
 int decode_mfma_blocks_per_cu(int32_t rows, int32_t r, int32_t dr);

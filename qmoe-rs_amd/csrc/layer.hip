@@ -59,24 +59,30 @@ struct GemmArgs {
   int64_t sA, sB, sC, sBias;  // per-z strides
 };
 
-// C[z][m][n] = bias[z][n], ahead of a GEMM that accumulates with beta = 1.
+// C[z][m][n] = bias[z][n], ahead of a GEMM that accumulates with beta = 1
+// (grid: x over the M * N elements of one z, y over z).
 __global__ __launch_bounds__(256) void k_bias_fill(float *__restrict__ C,
-                                                   const float *__restrict__ bias, int N,
-                                                   int64_t ldc, int64_t sC, int64_t sBias) {
-  const int z = blockIdx.z, m = blockIdx.y;
-  const int n = blockIdx.x * 256 + threadIdx.x;
-  if (n < N) C[z * sC + m * ldc + n] = bias[z * sBias + n];
+                                                   const float *__restrict__ bias, int64_t MN,
+                                                   int N, int64_t ldc, int64_t sC,
+                                                   int64_t sBias) {
+  const int64_t z = blockIdx.y;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= MN) return;
+  const int64_t m = i / N, n = i % N;
+  C[z * sC + m * ldc + n] = bias[z * sBias + n];
 }
 
 // Row-major C = A op(B) is column-major C^T = op(B)^T A^T: rocBLAS gets
 // (m, n, k) = (N, M, K) with B as its first operand.
 qmla_status gemm(const qmla_layer *L, const GemmArgs &g, int batch, bool trans_b, hipStream_t s) {
   if (g.M == 0 || g.N == 0) return QMLA_OK;
-  QMLA_REQUIRE(g.M <= 65535 && batch <= 65535, QMLA_ERR_SHAPE, "GEMM too large");
+  const int64_t MN = (int64_t)g.M * g.N;
+  QMLA_REQUIRE(batch <= 65535 && (MN + 255) / 256 <= 0x7fffffff, QMLA_ERR_SHAPE,
+               "GEMM too large");
   float beta = 0.f;
   if (g.bias) {
-    dim3 grid((g.N + 255) / 256, g.M, batch);
-    k_bias_fill<<<grid, dim3(256), 0, s>>>(g.C, g.bias, g.N, g.ldc, g.sC, g.sBias);
+    dim3 grid((unsigned)((MN + 255) / 256), batch);
+    k_bias_fill<<<grid, dim3(256), 0, s>>>(g.C, g.bias, MN, g.N, g.ldc, g.sC, g.sBias);
     QMLA_LAUNCH_CHECK("k_bias_fill");
     beta = 1.f;
   }
@@ -149,7 +155,7 @@ __device__ inline float block_sum(float v, float *red) {
 
 // Latent rows of new tokens, written straight into the cache (the append of
 // src/model.rs:99-104 fused in): one block per token (b, i),
-//   row = [LayerNorm(kva[b,i,:r]) | rope(kva[b,i,r:], pos0 + i)]
+//   row = [LayerNorm(kva[b,i,:r]) | rope(kva[b,i,r:], lens[b] + i)]
 // goes to pool row offsets[b] + lens[b] + i in the cache dtype (bf16 by
 // round-to-nearest-even), and, when `rows` is not NULL, to rows[b,i] in f32.
 // The lengths advance afterwards (k_cache_advance).  LayerNorm as
@@ -160,8 +166,7 @@ __global__ __launch_bounds__(256) void k_latent_rows(const float *__restrict__ k
                                                      int dr, const float *__restrict__ ln_w,
                                                      const float *__restrict__ ln_b, float eps,
                                                      const float *__restrict__ inv_freq,
-                                                     float mscale, int pos0,
-                                                     float *__restrict__ rows,
+                                                     float mscale, float *__restrict__ rows,
                                                      DstT *__restrict__ pool,
                                                      const int64_t *__restrict__ offsets,
                                                      const int32_t *__restrict__ lens) {
@@ -169,7 +174,8 @@ __global__ __launch_bounds__(256) void k_latent_rows(const float *__restrict__ k
   const int tok = blockIdx.x, b = tok / s, i = tok % s;
   const float *x = kva + (int64_t)tok * (r + dr);
   float *y = rows ? rows + (int64_t)tok * (r + dr) : nullptr;
-  DstT *dst = pool + (offsets[b] + lens[b] + i) * (int64_t)(r + dr);
+  const int32_t len = lens[b];
+  DstT *dst = pool + (offsets[b] + len + i) * (int64_t)(r + dr);
   auto put = [&](int c, float v) {
     if (y) y[c] = v;
     if constexpr (sizeof(DstT) == 2)
@@ -191,7 +197,7 @@ __global__ __launch_bounds__(256) void k_latent_rows(const float *__restrict__ k
     const float t = (x[c] - mean) / den * ln_w[c];
     put(c, ln_b ? t + ln_b[c] : t);
   }
-  const float pos = (float)(pos0 + i);
+  const float pos = (float)(len + i);
   for (int p = threadIdx.x; p < dr / 2; p += blockDim.x) {
     const float ang = pos * inv_freq[p];
     const float cs = cosf(ang) * mscale, sn = sinf(ang) * mscale;
@@ -201,32 +207,35 @@ __global__ __launch_bounds__(256) void k_latent_rows(const float *__restrict__ k
   }
 }
 
-// LayerNorm + RoPE of the n new tokens into the cache, then the lengths
-// advance (the cache call checked the room already).
-qmla_status latent_to_cache(const qmla_layer *L, const float *kva, int batch, int seq, int pos0,
+// LayerNorm + RoPE of the n new tokens into the cache (sequence b's tokens
+// at positions lens[b] + i), then the lengths advance (the caller checked
+// the room already).
+qmla_status latent_to_cache(const qmla_layer *L, const float *kva, int batch, int seq,
                             float *rows, qmla_kv_cache *cache, hipStream_t s) {
   const auto &g = L->cfg;
   const int n = batch * seq;
   if (cache->dtype == QMLA_BF16)
     k_latent_rows<uint16_t><<<dim3(n), dim3(256), 0, s>>>(
         kva, seq, g.kv_lora_rank, g.qk_rope, L->ln_w, L->ln_b, (float)g.ln_eps, L->inv_freq,
-        (float)g.rope_mscale, pos0, rows, (uint16_t *)cache->rows, cache->d_offsets, cache->d_lens);
+        (float)g.rope_mscale, rows, (uint16_t *)cache->rows, cache->d_offsets, cache->d_lens);
   else
     k_latent_rows<float><<<dim3(n), dim3(256), 0, s>>>(
         kva, seq, g.kv_lora_rank, g.qk_rope, L->ln_w, L->ln_b, (float)g.ln_eps, L->inv_freq,
-        (float)g.rope_mscale, pos0, rows, (float *)cache->rows, cache->d_offsets, cache->d_lens);
+        (float)g.rope_mscale, rows, (float *)cache->rows, cache->d_offsets, cache->d_lens);
   QMLA_LAUNCH_CHECK("k_latent_rows");
   return cache_advance(cache, 0, batch, seq, s);
 }
 
 // Split q [b*s, H, dn+dr] into q_nope and roped q_rope (src/model.rs:263-267
-// and :199-203).  Output layouts are selected by `bhs`:
+// and :199-203); sequence b's token i sits at position lens[b] + i (its
+// cached length before this step's append).  Output layouts by `bhs`:
 //   bhs = 0: q_nope [b, s, H, dn], q_rope [b, s, H, dr]  (decode rows i*H + h)
 //   bhs = 1: q_nope [b, H, s, dn], q_rope [b, H, s, dr]  (prefill layout)
 __global__ __launch_bounds__(64) void k_split_rope_q(const float *__restrict__ q, int s, int H,
                                                       int dn, int dr,
                                                       const float *__restrict__ inv_freq,
-                                                      float mscale, int pos0, int bhs,
+                                                      float mscale,
+                                                      const int32_t *__restrict__ lens, int bhs,
                                                       float *__restrict__ q_nope,
                                                       float *__restrict__ q_rope) {
   const int tok = blockIdx.x, h = blockIdx.y;
@@ -234,7 +243,7 @@ __global__ __launch_bounds__(64) void k_split_rope_q(const float *__restrict__ q
   const float *src = q + ((int64_t)tok * H + h) * (dn + dr);
   const int64_t o = bhs ? ((int64_t)b * H + h) * s + i : (int64_t)tok * H + h;
   for (int c = threadIdx.x; c < dn; c += blockDim.x) q_nope[o * dn + c] = src[c];
-  const float pos = (float)(pos0 + i);
+  const float pos = (float)(lens[b] + i);
   for (int p = threadIdx.x; p < dr / 2; p += blockDim.x) {
     const float ang = pos * inv_freq[p];
     const float cs = cosf(ang) * mscale, sn = sinf(ang) * mscale;
@@ -273,6 +282,45 @@ __global__ __launch_bounds__(128) void k_merge_heads(const float *__restrict__ c
   const float *src = ctx + (((int64_t)b * H + h) * s + i) * dv;
   float *dst = o + ((int64_t)tok * H + h) * dv;
   for (int c = threadIdx.x; c < dv; c += blockDim.x) dst[c] = src[c];
+}
+
+// Materialising the reference KVCache (src/model.rs:86-105) from latent rows:
+// the c_kv part of sequence seq0 + b's first T rows as f32 [n, T, r] (the
+// A operand of the kv_b_proj GEMMs for a bf16 cache).
+template <typename SrcT>
+__global__ __launch_bounds__(256) void k_latent_c_f32(const SrcT *__restrict__ pool,
+                                                      const int64_t *__restrict__ offsets,
+                                                      int seq0, int T, int r, int dr,
+                                                      float *__restrict__ dst) {
+  const int t = blockIdx.x, b = blockIdx.y;
+  const SrcT *src = pool + (offsets[seq0 + b] + t) * (int64_t)(r + dr);
+  float *o = dst + ((int64_t)b * T + t) * r;
+  for (int c = threadIdx.x; c < r; c += blockDim.x) {
+    if constexpr (sizeof(SrcT) == 2)
+      o[c] = bf16_bits_to_f32(src[c]);
+    else
+      o[c] = src[c];
+  }
+}
+
+// k_rope [n, H, T, dr]: the stored (roped) k_pe of each token broadcast to
+// every head, as the reference's expand at src/model.rs:217-219 / :281-285.
+template <typename SrcT>
+__global__ __launch_bounds__(256) void k_broadcast_rope(const SrcT *__restrict__ pool,
+                                                        const int64_t *__restrict__ offsets,
+                                                        int seq0, int T, int H, int r, int dr,
+                                                        float *__restrict__ k_rope) {
+  const int t = blockIdx.x, b = blockIdx.y;
+  const SrcT *src = pool + (offsets[seq0 + b] + t) * (int64_t)(r + dr) + r;
+  for (int e = threadIdx.x; e < H * dr; e += blockDim.x) {
+    const int h = e / dr, c = e % dr;
+    float v;
+    if constexpr (sizeof(SrcT) == 2)
+      v = bf16_bits_to_f32(src[c]);
+    else
+      v = src[c];
+    k_rope[(((int64_t)b * H + h) * T + t) * dr + c] = v;
+  }
 }
 
 inline size_t al(size_t x) { return (x + 255) & ~size_t(255); }
@@ -327,11 +375,33 @@ qmla_status check_layer_call(const qmla_layer *L, const float *xs, int32_t batch
   QMLA_REQUIRE(c->r == L->cfg.kv_lora_rank && c->dr == L->cfg.qk_rope, QMLA_ERR_SHAPE,
                "cache latent dims (%d, %d) differ from the layer's (%d, %d)", c->r, c->dr,
                L->cfg.kv_lora_rank, L->cfg.qk_rope);
-  for (int32_t i = 1; i < batch; ++i)
-    QMLA_REQUIRE(c->h_lens[i] == c->h_lens[0], QMLA_ERR_SHAPE,
-                 "sequence lengths differ (%d vs %d): the layer API takes a uniform batch",
-                 c->h_lens[i], c->h_lens[0]);
+  QMLA_REQUIRE(c->dtype == QMLA_F32 || c->dtype == QMLA_BF16, QMLA_ERR_UNSUPPORTED,
+               "the layer needs an f32 or bf16 latent cache");
   return QMLA_OK;
+}
+
+// Sequences seq0 .. seq0 + n - 1 of one uniform length T (the reference's
+// KVCache holds one tensor per kind, so every sequence has the same T).
+qmla_status check_materialise(const qmla_layer *L, const qmla_kv_cache *c, int32_t seq0,
+                              int32_t n, int32_t *T) {
+  QMLA_REQUIRE(L && c, QMLA_ERR_INVALID_ARG, "NULL layer or cache");
+  QMLA_REQUIRE(n > 0 && seq0 >= 0 && seq0 + (int64_t)n <= c->num_seqs, QMLA_ERR_SHAPE,
+               "sequences [%d, %d) outside the cache's %d", seq0, seq0 + n, c->num_seqs);
+  QMLA_REQUIRE(c->r == L->cfg.kv_lora_rank && c->dr == L->cfg.qk_rope, QMLA_ERR_SHAPE,
+               "cache latent dims (%d, %d) differ from the layer's (%d, %d)", c->r, c->dr,
+               L->cfg.kv_lora_rank, L->cfg.qk_rope);
+  QMLA_REQUIRE(c->dtype == QMLA_F32 || c->dtype == QMLA_BF16, QMLA_ERR_UNSUPPORTED,
+               "bad cache dtype");
+  for (int32_t i = seq0 + 1; i < seq0 + n; ++i)
+    QMLA_REQUIRE(c->h_lens[i] == c->h_lens[seq0], QMLA_ERR_SHAPE,
+                 "sequence lengths differ (%d vs %d): a KVCache tensor has one length",
+                 c->h_lens[i], c->h_lens[seq0]);
+  *T = c->h_lens[seq0];
+  return QMLA_OK;
+}
+
+size_t materialise_ws_bytes(const qmla_kv_cache *c, int32_t n, int32_t T) {
+  return c->dtype == QMLA_BF16 ? sizeof(float) * (size_t)n * T * c->r : 0;
 }
 
 // Decode workspace for the largest piece count the decode may choose
@@ -468,16 +538,18 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
   QMLA_TRY(check_layer_call(L, xs, batch, seq, cache, out));
   // f32 cache: f32 decode core.  bf16 cache: the new rows are rounded to
   // bf16 on append and the core is the bf16 MFMA decode (q rounded to bf16,
-  // f32 accumulation) for the latent shapes it serves.
-  QMLA_REQUIRE(cache->dtype == QMLA_F32 || cache->dtype == QMLA_BF16, QMLA_ERR_UNSUPPORTED,
-               "the layer needs an f32 or bf16 latent cache");
-  QMLA_TRY(make_room(cache, 0, batch, seq, as_stream(stream)));
+  // f32 accumulation) for the latent shapes it serves.  Every check runs
+  // before the cache is touched: a rejected call leaves lengths, capacity
+  // and rows as they were.
   const auto &g = L->cfg;
   const int H = g.heads, dn = g.qk_nope, dr = g.qk_rope, dv = g.v_dim, r = g.kv_lora_rank;
+  QMLA_REQUIRE((int64_t)seq * H <= 0x7fffffff, QMLA_ERR_SHAPE, "seq x heads too large");
+  QMLA_TRY(decode_shape_supported(cache, seq * H));
   const size_t dec_bytes = decode_bytes_for(L, cache, batch, seq);
   const LayerWs w = layer_ws(L, cache, batch, seq, dec_bytes);
   QMLA_REQUIRE(workspace && workspace_bytes >= w.total, QMLA_ERR_WORKSPACE,
                "workspace of %zu bytes < required %zu", workspace_bytes, w.total);
+  QMLA_TRY(make_room(cache, 0, batch, seq, as_stream(stream)));
   char *ws = static_cast<char *>(workspace);
   float *q = (float *)(ws + w.q), *kva = (float *)(ws + w.kva);
   float *qn = (float *)(ws + w.qn), *qr = (float *)(ws + w.qr), *qlat = (float *)(ws + w.qlat);
@@ -485,14 +557,14 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
   float *part = (float *)(ws + w.part);
   hipStream_t s = as_stream(stream);
   const int n = batch * seq;
-  const int pos0 = cache->h_lens[0];
 
   QMLA_TRY(linear(L, xs, n, g.hidden, L->wq, L->bq, H * (dn + dr), q, s, part, w.part_elems));
   QMLA_TRY(linear(L, xs, n, g.hidden, L->wkva, L->bkva, r + dr, kva, s, part, w.part_elems));
-  QMLA_TRY(latent_to_cache(L, kva, batch, seq, pos0, nullptr, cache, s));
+  // q's positions are the lengths before this step's append (src/model.rs:267)
   k_split_rope_q<<<dim3(n, H), dim3(64), 0, s>>>(q, seq, H, dn, dr, L->inv_freq,
-                                                (float)g.rope_mscale, pos0, 0, qn, qr);
+                                                (float)g.rope_mscale, cache->d_lens, 0, qn, qr);
   QMLA_LAUNCH_CHECK("k_split_rope_q");
+  QMLA_TRY(latent_to_cache(L, kva, batch, seq, nullptr, cache, s));
   // q_lat[t, h, :] = q_nope[t, h, :] W_UK^h   (batched over heads)
   {
     GemmArgs a{qn, L->wkvb, nullptr, qlat, n, r, dn, (int64_t)H * dn, r, (int64_t)H * r,
@@ -518,17 +590,16 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
                                        void *workspace, size_t workspace_bytes,
                                        qmla_stream stream) {
   QMLA_TRY(check_layer_call(L, xs, batch, seq, cache, out));
-  QMLA_REQUIRE(cache->dtype == QMLA_F32 || cache->dtype == QMLA_BF16, QMLA_ERR_UNSUPPORTED,
-               "bad cache dtype");
-  QMLA_REQUIRE(cache->h_lens[0] == 0, QMLA_ERR_SHAPE,
-               "forward_prefill starts a sequence: cache lengths must be 0 (got %d)",
-               cache->h_lens[0]);
-  QMLA_TRY(make_room(cache, 0, batch, seq, as_stream(stream)));
+  for (int32_t i = 0; i < batch; ++i)
+    QMLA_REQUIRE(cache->h_lens[i] == 0, QMLA_ERR_SHAPE,
+                 "forward_prefill starts a sequence: cache length %d of sequence %d must be 0",
+                 cache->h_lens[i], i);
   const auto &g = L->cfg;
   const int H = g.heads, dn = g.qk_nope, dr = g.qk_rope, dv = g.v_dim, r = g.kv_lora_rank;
   const LayerWs w = layer_ws(L, cache, batch, seq, decode_bytes_for(L, cache, batch, seq));
   QMLA_REQUIRE(workspace && workspace_bytes >= w.total, QMLA_ERR_WORKSPACE,
                "workspace of %zu bytes < required %zu", workspace_bytes, w.total);
+  QMLA_TRY(make_room(cache, 0, batch, seq, as_stream(stream)));
   char *ws = static_cast<char *>(workspace);
   float *q = (float *)(ws + w.q), *kva = (float *)(ws + w.kva), *rows = (float *)(ws + w.rows);
   float *qn = (float *)(ws + w.qn), *qr = (float *)(ws + w.qr), *kvb = (float *)(ws + w.kvb);
@@ -540,12 +611,12 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
 
   QMLA_TRY(linear(L, xs, n, g.hidden, L->wq, L->bq, H * (dn + dr), q, s, part, w.part_elems));
   QMLA_TRY(linear(L, xs, n, g.hidden, L->wkva, L->bkva, r + dr, kva, s, part, w.part_elems));
+  k_split_rope_q<<<dim3(n, H), dim3(64), 0, s>>>(q, seq, H, dn, dr, L->inv_freq,
+                                                (float)g.rope_mscale, cache->d_lens, 1, qn, qr);
+  QMLA_LAUNCH_CHECK("k_split_rope_q");
   // the latent replacement of the KVCache returned at src/model.rs:250 (the
   // f32 rows also feed compute_kv below)
-  QMLA_TRY(latent_to_cache(L, kva, batch, seq, 0, rows, cache, s));
-  k_split_rope_q<<<dim3(n, H), dim3(64), 0, s>>>(q, seq, H, dn, dr, L->inv_freq,
-                                                (float)g.rope_mscale, 0, 1, qn, qr);
-  QMLA_LAUNCH_CHECK("k_split_rope_q");
+  QMLA_TRY(latent_to_cache(L, kva, batch, seq, rows, cache, s));
   // compute_kv on the LayerNorm'd latent (src/model.rs:178-190)
   {
     GemmArgs a{rows, L->wkvb, L->bkvb, kvb, n, H * (dn + dv), r, r + dr, r, (int64_t)H * (dn + dv),
@@ -563,6 +634,68 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
   k_merge_heads<<<dim3(n, H), dim3(128), 0, s>>>(ctx, seq, H, dv, o);
   QMLA_LAUNCH_CHECK("k_merge_heads");
   QMLA_TRY(linear(L, o, n, H * dv, L->wo, L->bo, g.hidden, out, s, part, w.part_elems));
+  return QMLA_OK;
+}
+
+qmla_status qmla_cache_materialise_workspace_bytes(const qmla_layer *layer,
+                                                   const qmla_kv_cache *cache, int32_t seq0,
+                                                   int32_t n_seqs, size_t *bytes) {
+  QMLA_REQUIRE(bytes, QMLA_ERR_INVALID_ARG, "bytes is NULL");
+  int32_t T = 0;
+  QMLA_TRY(check_materialise(layer, cache, seq0, n_seqs, &T));
+  *bytes = materialise_ws_bytes(cache, n_seqs, T);
+  return QMLA_OK;
+}
+
+qmla_status qmla_cache_materialise(const qmla_layer *L, const qmla_kv_cache *cache,
+                                   int32_t seq0, int32_t n_seqs, float *k, float *v,
+                                   float *k_rope, void *workspace, size_t workspace_bytes,
+                                   qmla_stream stream) {
+  int32_t T = 0;
+  QMLA_TRY(check_materialise(L, cache, seq0, n_seqs, &T));
+  const size_t need = materialise_ws_bytes(cache, n_seqs, T);
+  QMLA_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), QMLA_ERR_WORKSPACE,
+               "workspace of %zu bytes < required %zu", workspace_bytes, need);
+  if (T == 0) return QMLA_OK;
+  const auto &g = L->cfg;
+  const int H = g.heads, dn = g.qk_nope, dr = g.qk_rope, dv = g.v_dim, r = g.kv_lora_rank;
+  hipStream_t s = as_stream(stream);
+  QMLA_REQUIRE(n_seqs <= 65535, QMLA_ERR_SHAPE, "n_seqs %d > 65535", n_seqs);
+  const bool bf = cache->dtype == QMLA_BF16;
+  if (k_rope && dr > 0) {
+    if (bf)
+      k_broadcast_rope<uint16_t><<<dim3(T, n_seqs), dim3(256), 0, s>>>(
+          (const uint16_t *)cache->rows, cache->d_offsets, seq0, T, H, r, dr, k_rope);
+    else
+      k_broadcast_rope<float><<<dim3(T, n_seqs), dim3(256), 0, s>>>(
+          (const float *)cache->rows, cache->d_offsets, seq0, T, H, r, dr, k_rope);
+    QMLA_LAUNCH_CHECK("k_broadcast_rope");
+  }
+  if (!k && !v) return QMLA_OK;
+  float *lat = static_cast<float *>(workspace);
+  if (bf) {
+    k_latent_c_f32<uint16_t><<<dim3(T, n_seqs), dim3(256), 0, s>>>(
+        (const uint16_t *)cache->rows, cache->d_offsets, seq0, T, r, dr, lat);
+    QMLA_LAUNCH_CHECK("k_latent_c_f32");
+  }
+  // compute_kv (src/model.rs:178-190) per sequence, batched over heads:
+  //   k[b][h] = c_b W_UK^h^T + b_K^h,  v[b][h] = c_b W_UV^h^T + b_V^h
+  for (int32_t b = 0; b < n_seqs; ++b) {
+    const float *A = bf ? lat + (size_t)b * T * r
+                        : (const float *)cache->rows + cache->h_offsets[seq0 + b] * (r + dr);
+    const int64_t lda = bf ? r : r + dr;
+    if (k) {
+      GemmArgs a{A, L->wkvb, L->bkvb, k + (size_t)b * H * T * dn, T, dn, r, lda, r, dn,
+                 0, (int64_t)(dn + dv) * r, (int64_t)T * dn, (int64_t)(dn + dv)};
+      QMLA_TRY(gemm(L, a, H, true, s));
+    }
+    if (v) {
+      GemmArgs a{A, L->wkvb + (size_t)dn * r, L->bkvb ? L->bkvb + dn : nullptr,
+                 v + (size_t)b * H * T * dv, T, dv, r, lda, r, dv,
+                 0, (int64_t)(dn + dv) * r, (int64_t)T * dv, (int64_t)(dn + dv)};
+      QMLA_TRY(gemm(L, a, H, true, s));
+    }
+  }
   return QMLA_OK;
 }
 

@@ -115,6 +115,8 @@ SIGNATURES = {
     "qmla_layer_workspace_bytes": (_st, [_vp, _vp, _i32, _i32, C.POINTER(_sz)]),
     "qmla_layer_forward_with_cache": (_st, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "qmla_layer_forward_prefill": (_st, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
+    "qmla_cache_materialise_workspace_bytes": (_st, [_vp, _vp, _i32, _i32, C.POINTER(_sz)]),
+    "qmla_cache_materialise": (_st, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _sz, _vp]),
     "qmla_packed_forward_workspace_bytes": (_st, [_i32, _i32, _i32, C.POINTER(_sz)]),
     "qmla_packed_forward": (_st, [_vp, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _sz, _vp]),
     "qmla_moe_workspace_bytes": (_st, [C.POINTER(MoEConfig), _i32, C.POINTER(_sz)]),
@@ -445,6 +447,26 @@ class MlaLayer:
                                                wsb, None))
         check(lib().qmla_stream_synchronize(None))
         return out.to_numpy(np.float32, (b, s, self.hidden))
+
+    def materialise(self, cache: KVCache, seq0: int = 0, n_seqs: int | None = None):
+        """The reference KVCache's public tensors (src/model.rs:88-92) for
+        sequences seq0 .. seq0 + n_seqs - 1 of one length T, rebuilt through
+        kv_b_proj: (k [n, H, T, dn], v [n, H, T, dv], k_rope [n, H, T, dr])."""
+        n = cache.num_seqs - seq0 if n_seqs is None else n_seqs
+        nb = C.c_size_t()
+        check(lib().qmla_cache_materialise_workspace_bytes(self.handle, cache.handle, seq0, n, C.byref(nb)))
+        T = int(cache.lengths()[seq0])
+        c = self.cfg
+        H, dn, dv, dr = c.heads, c.qk_nope, c.v_dim, c.qk_rope
+        k = DeviceBuffer(n * H * T * dn * 4)
+        v = DeviceBuffer(n * H * T * dv * 4)
+        kr = DeviceBuffer(n * H * T * dr * 4)
+        ws = DeviceBuffer(nb.value) if nb.value else None
+        check(lib().qmla_cache_materialise(self.handle, cache.handle, seq0, n, k.ptr, v.ptr, kr.ptr, _p(ws),
+                                           nb.value, None))
+        check(lib().qmla_stream_synchronize(None))
+        return (k.to_numpy(np.float32, (n, H, T, dn)), v.to_numpy(np.float32, (n, H, T, dv)),
+                kr.to_numpy(np.float32, (n, H, T, dr)))
 
     def close(self):
         if self.handle:

@@ -87,3 +87,29 @@ def test_packed_and_moe_argument_checks_without_a_device():
     assert L.qmla_moe_workspace_bytes(None, 2, C.byref(n)) == 1
     # a zero-length call is a no-op that needs no pointers
     assert L.qmla_moe_forward(C.byref(cfg), None, 0, *([None] * 11), 0, None) == 0
+
+
+def test_layer_default_scales_match_the_reference_constructor():
+    """qmla_layer_default_scales restates MlaAttention::new's YaRN scales
+    (src/model.rs:160-173): rope_mscale = mscale(40, 1) / mscale(40, 0.707)
+    and softmax_scale = (dn + dr)^-1/2 * mscale(40, 0.707)^2, against the
+    closed-form constants (ln 40 = 3.6888794541139363)."""
+    L = qmla.lib()
+    for dn, dr, want in ((128, 64, 0.1147213868), (32, 16, 0.2294427736)):
+        cfg = qmla.LayerConfig(2048, 16, dn, dr, 128, 512, 0.0, 0.0, 0.0)
+        assert L.qmla_layer_default_scales(C.byref(cfg)) == 0
+        assert abs(cfg.rope_mscale - 1.0857263992) < 1e-9
+        assert abs(cfg.softmax_scale - want) < 1e-9
+        assert cfg.ln_eps == 1e-6
+    m = 0.1 * 0.707 * 3.6888794541139363 + 1.0
+    assert abs(m - 1.2608037767) < 1e-9
+    assert abs((0.1 * 3.6888794541139363 + 1.0) / m - 1.0857263992) < 1e-9
+    assert L.qmla_layer_default_scales(None) == 1
+
+
+def test_materialise_and_layer_calls_validate_without_a_device():
+    L = qmla.lib()
+    n = C.c_size_t()
+    assert L.qmla_cache_materialise_workspace_bytes(None, None, 0, 1, C.byref(n)) == 1
+    assert L.qmla_cache_materialise(None, None, 0, 1, None, None, None, None, 0, None) == 1
+    assert L.qmla_layer_forward_with_cache(None, None, 1, 1, None, None, None, 0, None) == 1

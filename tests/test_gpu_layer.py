@@ -76,10 +76,11 @@ def test_layer_argument_errors(qmla_gpu):
     q = qmla_gpu
     w, layer = c1_layer(q)
     cache = q.KVCache([4, 4], 64, 16, q.F32)
-    cache.set_lengths([1, 2])
-    with pytest.raises(q.QmlaError) as e:   # lengths differ across the batch
+    cache.set_lengths([3, 4])
+    with pytest.raises(q.QmlaError) as e:   # sequence 1 has no room for the new token
         layer.forward_with_cache(O.normal((2, 1, 512), 1), cache)
-    assert e.value.status == 2
+    assert e.value.status == 6
+    assert list(cache.lengths()) == [3, 4]
     cache.set_lengths([4, 4])
     with pytest.raises(q.QmlaError) as e:   # no room for the new token
         layer.forward_with_cache(O.normal((2, 1, 512), 1), cache)
@@ -118,3 +119,139 @@ def test_bf16_cache_prefill_then_decode(qmla_gpu, dims):
         print(f"dims={dims} step {step} rel_err={err:.2e}")
         assert err < 2e-2
     assert list(cache.lengths()) == [s + 3] * b
+
+
+def _ragged_cache(q, lens, r, dr, dtype, seed, spare=2):
+    """A cache whose sequences hold `lens` random latent rows (N(0,1); bf16
+    rounded for a bf16 cache) with `spare` free rows each; returns the cache
+    and the per-sequence f32 rows the oracle sees."""
+    lens = np.asarray(lens, np.int32)
+    cache = q.KVCache(lens + spare, r, dr, dtype)
+    total = int((lens + spare).sum())
+    pool = O.normal((total, r + dr), seed)
+    if dtype == q.BF16:
+        bits = O.to_bf16_bits(pool)
+        cache.write_pool(bits)
+        pool = O.bf16_bits_to_f32(bits)
+    else:
+        cache.write_pool(pool)
+    cache.set_lengths(lens)
+    offs = cache.offsets()
+    per_seq = [pool[offs[i]:offs[i] + lens[i]] for i in range(lens.size)]
+    return cache, per_seq
+
+
+@pytest.mark.parametrize("case", [
+    # (hidden, heads, dn, dr, dv, r, cache dtype, lengths, new tokens, tolerance)
+    ((512, 8, 32, 16, 32, 64), "f32", [4096, 32768, 300], 1, 1e-4),
+    ((512, 8, 32, 16, 32, 64), "f32", [1, 17000, 0], 2, 1e-4),
+    ((512, 16, 128, 64, 128, 512), "bf16", [300, 4097, 1], 1, 2e-2),
+], ids=["c1-dims-f32-4096-32768-300", "c1-dims-f32-two-tokens", "v2lite-dims-bf16-300-4097-1"])
+def test_ragged_layer_decode_at_real_positions(qmla_gpu, case):
+    """forward_with_cache over a ragged batch whose contexts reach 32768:
+    each sequence's new tokens take RoPE positions from its own length, and
+    every sequence's output and new cache rows equal a batch-1 run of the
+    reference's absorbed-latent step in the oracle at that position."""
+    q = qmla_gpu
+    dims, dt, lens, s, tol = case
+    hidden, H, dn, dr, dv, r = dims
+    w = O.MlaWeights.random(hidden, H, dn, dr, dv, r, seed=1200 + r)
+    layer = q.MlaLayer(w)
+    dtype = q.BF16 if dt == "bf16" else q.F32
+    cache, per_seq = _ragged_cache(q, lens, r, dr, dtype, 1201, spare=s)
+    xs = O.normal((len(lens), s, hidden), 1202)
+    out = layer.forward_with_cache(xs, cache)
+    assert list(cache.lengths()) == [n + s for n in lens]
+    pool = cache.read_rows()
+    if dtype == q.BF16:
+        pool = O.bf16_bits_to_f32(pool)
+    offs = cache.offsets()
+    for b, n in enumerate(lens):
+        lat = per_seq[b].reshape(1, n, r + dr)
+        ref, rows = O.mla_forward_with_latent(w, xs[b:b + 1], lat)
+        err = rel_err(out[b], ref[0])
+        row_err = rel_err(pool[offs[b] + n: offs[b] + n + s], rows[0])
+        print(f"{dt} seq {b} len {n}: out rel_err={err:.2e} new-row rel_err={row_err:.2e}")
+        assert err < tol
+        assert row_err < (1e-5 if dtype == q.F32 else 4e-3)
+
+
+def test_rejected_layer_call_leaves_the_cache_unchanged(qmla_gpu):
+    """A layer call that fails validation (unsupported bf16 decode shape,
+    short workspace) neither grows the cache nor appends rows."""
+    q = qmla_gpu
+    import ctypes as C
+    w = O.MlaWeights.random(256, 4, 32, 32, 32, 256, seed=1300)   # bf16 r 256 / dr 32: no MFMA core
+    layer = q.MlaLayer(w)
+    cache = q.KVCache([2, 2], 256, 32, q.BF16, grow=True)
+    cache.set_lengths([2, 2])
+    with pytest.raises(q.QmlaError) as e:
+        layer.forward_with_cache(O.normal((2, 1, 256), 1), cache)
+    assert e.value.status == 3
+    assert list(cache.lengths()) == [2, 2] and list(cache.capacity()) == [2, 2]
+    w2, layer2 = c1_layer(q)
+    cache2 = q.KVCache([2, 2], 64, 16, q.F32, grow=True)
+    cache2.set_lengths([2, 2])
+    x = q.DeviceBuffer.from_numpy(O.normal((2, 1, 512), 2))
+    out = q.DeviceBuffer(2 * 512 * 4)
+    need = layer2.workspace_bytes(cache2, 2, 1)
+    ws = q.DeviceBuffer(need)
+    st = q.lib().qmla_layer_forward_with_cache(layer2.handle, x.ptr, 2, 1, cache2.handle, out.ptr, ws.ptr,
+                                               need - 256, None)
+    assert st == 7
+    assert list(cache2.lengths()) == [2, 2] and list(cache2.capacity()) == [2, 2]
+    # with the full workspace the same call grows the cache and appends
+    st = q.lib().qmla_layer_forward_with_cache(layer2.handle, x.ptr, 2, 1, cache2.handle, out.ptr, ws.ptr,
+                                               need, None)
+    assert st == 0, q.lib().qmla_last_error()
+    q.check(q.lib().qmla_stream_synchronize(None))
+    assert list(cache2.lengths()) == [3, 3] and min(cache2.capacity()) >= 3
+    del C
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_materialised_cache_equals_the_reference_kvcache(qmla_gpu, dt):
+    """qmla_cache_materialise rebuilds KVCache {k, v, k_rope}
+    (src/model.rs:88-92): after forward_prefill and two decode steps, the
+    tensors equal the cache the reference's decompressed path returns."""
+    q = qmla_gpu
+    hidden, H, dn, dr, dv, r = (256, 4, 32, 16, 32, 64) if dt == "f32" else (512, 16, 128, 64, 128, 512)
+    w = O.MlaWeights.random(hidden, H, dn, dr, dv, r, seed=1400 + r)
+    layer = q.MlaLayer(w)
+    b, s = 2, 29
+    dtype = q.F32 if dt == "f32" else q.BF16
+    cache = q.KVCache([s + 2] * b, r, dr, dtype)
+    xs = O.normal((b, s, hidden), 1401)
+    layer.forward_prefill(xs, cache)
+    _, (k, v, kr) = O.mla_forward_prefill(w, xs)
+    for step in range(2):
+        x1 = O.normal((b, 1, hidden), 1410 + step)
+        layer.forward_with_cache(x1, cache)
+        _, (k, v, kr) = O.mla_forward_with_cache(w, x1, k, v, kr, return_cache=True)
+    gk, gv, gkr = layer.materialise(cache)
+    assert gk.shape == k.shape and gv.shape == v.shape and gkr.shape == kr.shape
+    if dtype == q.F32:
+        tol = 1e-4
+    else:
+        # the bf16 cache stores the latent rounded to bf16: compare with the
+        # oracle's decompression of exactly those rows (1e-4), and with the
+        # reference's f32 cache within the bf16 tolerance
+        pool = O.bf16_bits_to_f32(cache.read_rows())
+        offs = cache.offsets()
+        lat = np.stack([pool[offs[i]:offs[i] + s + 2] for i in range(b)])
+        ek, ev, ekr = O.decompress_cache(w, lat)
+        for got, ref in ((gk, ek), (gv, ev), (gkr, ekr)):
+            assert rel_err(got, ref) < 1e-4
+        tol = 2e-2
+    for name, got, ref in (("k", gk, k), ("v", gv, v), ("k_rope", gkr, kr)):
+        err = rel_err(got, ref)
+        print(f"{dt} {name} rel_err={err:.2e}")
+        assert err < tol
+    # one sequence of a ragged cache at a time; unequal lengths are refused
+    cache.set_lengths([s + 2, s])
+    k1, v1, kr1 = layer.materialise(cache, 1, 1)
+    assert k1.shape == (1, H, s, dn)
+    assert rel_err(k1[0], gk[1][:, :s]) < 1e-6
+    with pytest.raises(q.QmlaError) as e:
+        layer.materialise(cache, 0, 2)
+    assert e.value.status == 2
