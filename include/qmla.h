@@ -229,6 +229,25 @@ QMLA_API qmla_status qmla_decode_workspace_bytes_splits(const qmla_decode_dims *
                                                const qmla_kv_cache *cache, int32_t num_splits,
                                                size_t *bytes);
 
+/* Allocation-free form of qmla_decode_absorbed.  It has no counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, results and errors as qmla_decode_absorbed,
+ * without the workspace: the split partials live in a static device array
+ * of QMLA_DECODE_NOALLOC_SCRATCH_BYTES per GPU, held from the library's
+ * first use of that GPU until the process ends.  A call whose workspace
+ * (qmla_decode_workspace_bytes) would exceed that size returns
+ * QMLA_ERR_UNSUPPORTED before anything is launched; the 128-head,
+ * batch-64 decode over 256 compute units needs 84 MiB.  The call allocates
+ * nothing.  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams, other threads) race and must be
+ * serialised by the caller. */
+#define QMLA_DECODE_NOALLOC_SCRATCH_BYTES ((size_t)96 << 20)
+QMLA_API qmla_status qmla_decode_absorbed_noalloc(const qmla_decode_dims *dims,
+                                         const qmla_kv_cache *cache, qmla_dtype q_dtype,
+                                         const void *q_latent, const void *q_rope, double scale,
+                                         float *out_latent, float *out_lse, qmla_stream stream);
+
 /* --------------------------------------------- MLA layer (model.rs) -----
  * MlaAttention, src/model.rs:107-307, with device-resident weights.
  * Weights are given as host f32 arrays in the reference's Linear layout

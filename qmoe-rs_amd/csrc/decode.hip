@@ -15,7 +15,9 @@
 // (o / l, log-sum-exp) slot and k_decode_merge combines them.
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
+#include <mutex>
 
 #include "internal.hpp"
 
@@ -440,9 +442,65 @@ qmla_status decode_impl(const qmla_decode_dims *d, const qmla_kv_cache *c, qmla_
                              out_lse, s);
 }
 
+// ------------------------------------------- allocation-free decode -----
+// Scratch of qmla_decode_absorbed_noalloc: the decode workspace (plan or
+// per-sequence slot table, split partials and their log-sum-exp) lives in
+// this file-scope device array instead of a caller buffer.  Each device the
+// library runs on holds its own copy for the life of the process.  In host
+// code `scratch` names a host-side stand-in, never the device copy: the
+// device address comes from hipGetSymbolAddress, once per device, and only
+// that pointer is handed to kernels.  Nothing in it needs clearing: every
+// call writes each slot entry and partial it later reads.
+constexpr size_t kNoAllocScratchBytes = QMLA_DECODE_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void *> g_scratch_ptr[kMaxScratchDevices];
+std::mutex g_scratch_mu;
+
+// Device address of this device's scratch (resolved on the first call on
+// the device, with it current).
+qmla_status noalloc_scratch(void **out) {
+  int dev = 0;
+  QMLA_HIP(hipGetDevice(&dev));
+  QMLA_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, QMLA_ERR_UNSUPPORTED,
+               "device ordinal %d >= %d", dev, kMaxScratchDevices);
+  void *p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      QMLA_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+      QMLA_REQUIRE(p != nullptr, QMLA_ERR_HIP, "no device address for the decode scratch");
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return QMLA_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+qmla_status qmla_decode_absorbed_noalloc(const qmla_decode_dims *dims, const qmla_kv_cache *cache,
+                                         qmla_dtype q_dtype, const void *q_latent,
+                                         const void *q_rope, double scale, float *out_latent,
+                                         float *out_lse, qmla_stream stream) {
+  QMLA_TRY(validate_decode(dims, cache));
+  const int32_t blocks = choose_blocks(dims, cache, 0);
+  const size_t need = decode_workspace_layout(dims->batch, dims->rows, dims->kv_lora_rank, blocks,
+                                              cache->dtype == QMLA_BF16)
+                          .total;
+  QMLA_REQUIRE(need <= kNoAllocScratchBytes, QMLA_ERR_UNSUPPORTED,
+               "decode needs %zu bytes of scratch; the allocation-free entry point has %zu "
+               "(use qmla_decode_absorbed with a workspace)",
+               need, kNoAllocScratchBytes);
+  void *ws = nullptr;
+  QMLA_TRY(noalloc_scratch(&ws));
+  return decode_impl(dims, cache, q_dtype, q_latent, q_rope, scale, out_latent, out_lse, 0, ws,
+                     kNoAllocScratchBytes, stream);
+}
 
 qmla_status qmla_decode_workspace_bytes_splits(const qmla_decode_dims *dims,
                                                const qmla_kv_cache *cache, int32_t num_splits,

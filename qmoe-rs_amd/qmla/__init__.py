@@ -109,6 +109,7 @@ SIGNATURES = {
     "qmla_decode_absorbed": (_st, [C.POINTER(DecodeDims), _vp, _st, _vp, _vp, _d, _vp, _vp, _vp, _sz, _vp]),
     "qmla_decode_absorbed_splits": (_st, [C.POINTER(DecodeDims), _vp, _st, _vp, _vp, _d, _vp, _vp, _i32,
                                           _vp, _sz, _vp]),
+    "qmla_decode_absorbed_noalloc": (_st, [C.POINTER(DecodeDims), _vp, _st, _vp, _vp, _d, _vp, _vp, _vp]),
     "qmla_layer_default_scales": (_st, [C.POINTER(LayerConfig)]),
     "qmla_layer_create": (_st, [C.POINTER(LayerConfig)] + [_vp] * 10 + [C.POINTER(_vp)]),
     "qmla_layer_destroy": (_st, [_vp]),
