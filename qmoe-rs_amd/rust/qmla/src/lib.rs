@@ -1,0 +1,483 @@
+//! Safe wrappers of libqmla (raw bindings in `qmla-sys`).
+//!
+//! * [`DeviceBuffer`]: the HBM-resident buffers src/tensor.rs gains.
+//! * [`KVCache`]: the device latent cache that replaces KVCache
+//!   (src/model.rs:86-105), one `[c_kv | k_pe]` row per token with a ragged
+//!   length table.
+//! * [`MlaAttention`]: MlaAttention (src/model.rs:107-307) with device
+//!   weights; `forward_with_cache` / `forward_prefill` on device buffers.
+//! * [`fused_prefill_attn`], [`decode_absorbed`]: the attention cores.
+//! * [`PackedQMoETensor`], [`QMoELayer`]: src/tensor.rs:64-95 and
+//!   src/moe.rs:40-130 on the device.
+//!
+//! With the `candle` feature, [`attention_kernel`] and [`model`] keep the
+//! reference's candle signatures on top of these.
+use std::os::raw::c_void;
+use std::ptr;
+
+pub use qmla_sys as sys;
+use qmla_sys::*;
+
+#[cfg(feature = "candle")]
+pub mod attention_kernel;
+#[cfg(feature = "candle")]
+pub mod model;
+
+/// A failed library call: its status and message.
+#[derive(Debug, Clone)]
+pub struct Error {
+    pub status: qmla_status,
+    pub message: String,
+}
+
+impl std::fmt::Display for Error {
+    fn fmt(&self, f: &mut std::fmt::Formatter<'_>) -> std::fmt::Result {
+        write!(f, "qmla status {}: {}", self.status, self.message)
+    }
+}
+
+impl std::error::Error for Error {}
+
+pub type Result<T> = std::result::Result<T, Error>;
+
+fn ok(st: qmla_status) -> Result<()> {
+    if st == QMLA_OK {
+        Ok(())
+    } else {
+        Err(Error { status: st, message: last_error() })
+    }
+}
+
+/// Element types of device tensors (bf16 as u16 bit patterns).
+#[derive(Clone, Copy, Debug, PartialEq, Eq)]
+pub enum DType {
+    F32,
+    BF16,
+}
+
+impl DType {
+    pub fn raw(self) -> qmla_dtype {
+        match self {
+            DType::F32 => QMLA_F32,
+            DType::BF16 => QMLA_BF16,
+        }
+    }
+    pub fn size(self) -> usize {
+        match self {
+            DType::F32 => 4,
+            DType::BF16 => 2,
+        }
+    }
+}
+
+/// A HIP stream (null = the default stream).
+pub struct Stream {
+    raw: qmla_stream,
+    owned: bool,
+}
+
+impl Stream {
+    pub fn new() -> Result<Self> {
+        let mut raw: qmla_stream = ptr::null_mut();
+        ok(unsafe { qmla_stream_create(&mut raw) })?;
+        Ok(Stream { raw, owned: true })
+    }
+    pub fn default_stream() -> Self {
+        Stream { raw: ptr::null_mut(), owned: false }
+    }
+    pub fn raw(&self) -> qmla_stream {
+        self.raw
+    }
+    pub fn synchronize(&self) -> Result<()> {
+        ok(unsafe { qmla_stream_synchronize(self.raw) })
+    }
+}
+
+impl Drop for Stream {
+    fn drop(&mut self) {
+        if self.owned && !self.raw.is_null() {
+            unsafe {
+                qmla_stream_destroy(self.raw);
+            }
+        }
+    }
+}
+
+/// An HBM allocation (qmla_buffer_alloc / qmla_buffer_free).
+pub struct DeviceBuffer {
+    ptr: *mut c_void,
+    bytes: usize,
+}
+
+impl DeviceBuffer {
+    pub fn new(bytes: usize) -> Result<Self> {
+        let mut ptr: *mut c_void = ptr::null_mut();
+        ok(unsafe { qmla_buffer_alloc(bytes.max(1), &mut ptr) })?;
+        Ok(DeviceBuffer { ptr, bytes })
+    }
+    /// Zero-filled buffer.
+    pub fn zeros(bytes: usize, stream: &Stream) -> Result<Self> {
+        let b = DeviceBuffer::new(bytes)?;
+        ok(unsafe { qmla_memset_zero(b.ptr, b.bytes.max(1), stream.raw()) })?;
+        Ok(b)
+    }
+    /// Copy of a host slice (synchronous).
+    pub fn from_slice<T: Copy>(data: &[T], stream: &Stream) -> Result<Self> {
+        let bytes = std::mem::size_of_val(data);
+        let b = DeviceBuffer::new(bytes)?;
+        if bytes > 0 {
+            ok(unsafe { qmla_memcpy_h2d(b.ptr, data.as_ptr() as *const c_void, bytes, stream.raw()) })?;
+            stream.synchronize()?;
+        }
+        Ok(b)
+    }
+    /// Copies the first `out.len()` elements back to the host (synchronous).
+    pub fn copy_to<T: Copy>(&self, out: &mut [T], stream: &Stream) -> Result<()> {
+        let bytes = std::mem::size_of_val(out);
+        assert!(bytes <= self.bytes, "copy of {} bytes from a {}-byte buffer", bytes, self.bytes);
+        if bytes > 0 {
+            ok(unsafe { qmla_memcpy_d2h(out.as_mut_ptr() as *mut c_void, self.ptr, bytes, stream.raw()) })?;
+            stream.synchronize()?;
+        }
+        Ok(())
+    }
+    pub fn to_vec_f32(&self, n: usize, stream: &Stream) -> Result<Vec<f32>> {
+        let mut v = vec![0f32; n];
+        self.copy_to(&mut v, stream)?;
+        Ok(v)
+    }
+    pub fn ptr(&self) -> *const c_void {
+        self.ptr
+    }
+    pub fn ptr_mut(&mut self) -> *mut c_void {
+        self.ptr
+    }
+    pub fn bytes(&self) -> usize {
+        self.bytes
+    }
+}
+
+impl Drop for DeviceBuffer {
+    fn drop(&mut self) {
+        if !self.ptr.is_null() {
+            unsafe {
+                qmla_buffer_free(self.ptr);
+            }
+        }
+    }
+}
+
+/// The latent KV cache: sequence i holds its tokens' `[c_kv | k_pe]` rows
+/// in one contiguous range of an HBM pool, with a device length table.
+pub struct KVCache {
+    raw: *mut qmla_kv_cache,
+    num_seqs: usize,
+    kv_lora_rank: usize,
+    rope_dim: usize,
+    dtype: DType,
+}
+
+impl KVCache {
+    /// KVCache::new (src/model.rs:95-97): empty sequences with the given
+    /// capacities.  `grow` lets appends past a capacity grow it, as
+    /// Tensor::cat never runs out of room.
+    pub fn new(capacity: &[i32], kv_lora_rank: usize, rope_dim: usize, dtype: DType, grow: bool) -> Result<Self> {
+        let mut raw: *mut qmla_kv_cache = ptr::null_mut();
+        ok(unsafe {
+            qmla_cache_create(capacity.len() as i32, capacity.as_ptr(), kv_lora_rank as i32, rope_dim as i32,
+                              dtype.raw(), &mut raw)
+        })?;
+        let c = KVCache { raw, num_seqs: capacity.len(), kv_lora_rank, rope_dim, dtype };
+        if grow {
+            ok(unsafe { qmla_cache_set_growth(c.raw, 1) })?;
+        }
+        Ok(c)
+    }
+    pub fn raw(&self) -> *mut qmla_kv_cache {
+        self.raw
+    }
+    pub fn num_seqs(&self) -> usize {
+        self.num_seqs
+    }
+    pub fn dtype(&self) -> DType {
+        self.dtype
+    }
+    /// KVCache::append (src/model.rs:99-104): `n_new` rows for each of
+    /// sequences 0..n_seqs, `rows` [n_seqs, n_new, r + dr] on the device.
+    pub fn append(&mut self, rows: &DeviceBuffer, rows_dtype: DType, n_seqs: usize, n_new: usize,
+                  stream: &Stream) -> Result<()> {
+        let need = n_seqs * n_new * (self.kv_lora_rank + self.rope_dim) * rows_dtype.size();
+        assert!(rows.bytes() >= need, "rows buffer too small");
+        ok(unsafe {
+            qmla_cache_append(self.raw, rows.ptr(), rows_dtype.raw(), n_seqs as i32, n_new as i32, stream.raw())
+        })
+    }
+    /// Current lengths (`cache.k.dim(2)` per sequence, src/model.rs:259).
+    pub fn lengths(&self) -> Result<Vec<i32>> {
+        let mut v = vec![0i32; self.num_seqs];
+        ok(unsafe { qmla_cache_lengths(self.raw, v.as_mut_ptr()) })?;
+        Ok(v)
+    }
+    pub fn set_lengths(&mut self, lengths: &[i32], stream: &Stream) -> Result<()> {
+        assert_eq!(lengths.len(), self.num_seqs);
+        ok(unsafe { qmla_cache_set_lengths(self.raw, lengths.as_ptr(), stream.raw()) })
+    }
+    pub fn reserve(&mut self, min_capacity: &[i32], stream: &Stream) -> Result<()> {
+        assert_eq!(min_capacity.len(), self.num_seqs);
+        ok(unsafe { qmla_cache_reserve(self.raw, min_capacity.as_ptr(), stream.raw()) })
+    }
+    /// `#[derive(Clone)]` (src/model.rs:87) on a stream.
+    pub fn try_clone(&self, stream: &Stream) -> Result<Self> {
+        let mut raw: *mut qmla_kv_cache = ptr::null_mut();
+        ok(unsafe { qmla_cache_clone(self.raw, &mut raw, stream.raw()) })?;
+        Ok(KVCache {
+            raw,
+            num_seqs: self.num_seqs,
+            kv_lora_rank: self.kv_lora_rank,
+            rope_dim: self.rope_dim,
+            dtype: self.dtype,
+        })
+    }
+}
+
+impl Clone for KVCache {
+    fn clone(&self) -> Self {
+        self.try_clone(&Stream::default_stream()).expect("qmla_cache_clone")
+    }
+}
+
+impl Drop for KVCache {
+    fn drop(&mut self) {
+        if !self.raw.is_null() {
+            unsafe {
+                qmla_cache_destroy(self.raw);
+            }
+        }
+    }
+}
+
+/// Host f32 weights of one MlaAttention in the Linear layout ([out, in]
+/// weight, [out] bias): q_proj, kv_a_proj_with_mqa, kv_a_layernorm,
+/// kv_b_proj, o_proj (src/model.rs:107-146).
+pub struct MlaWeights<'a> {
+    pub wq: &'a [f32],
+    pub bq: Option<&'a [f32]>,
+    pub wkva: &'a [f32],
+    pub bkva: Option<&'a [f32]>,
+    pub ln_w: &'a [f32],
+    pub ln_b: Option<&'a [f32]>,
+    pub wkvb: &'a [f32],
+    pub bkvb: Option<&'a [f32]>,
+    pub wo: &'a [f32],
+    pub bo: Option<&'a [f32]>,
+}
+
+fn opt_ptr(b: Option<&[f32]>) -> *const f32 {
+    b.map_or(ptr::null(), |s| s.as_ptr())
+}
+
+/// MlaAttention with device-resident weights.
+pub struct MlaAttention {
+    raw: *mut qmla_layer,
+    pub config: qmla_layer_config,
+}
+
+impl MlaAttention {
+    /// The reference constructor's scales (src/model.rs:160-173) for these
+    /// dimensions.
+    pub fn default_config(hidden: usize, heads: usize, qk_nope: usize, qk_rope: usize, v_dim: usize,
+                          kv_lora_rank: usize) -> Result<qmla_layer_config> {
+        let mut cfg = qmla_layer_config {
+            hidden: hidden as i32,
+            heads: heads as i32,
+            qk_nope: qk_nope as i32,
+            qk_rope: qk_rope as i32,
+            v_dim: v_dim as i32,
+            kv_lora_rank: kv_lora_rank as i32,
+            ..Default::default()
+        };
+        ok(unsafe { qmla_layer_default_scales(&mut cfg) })?;
+        Ok(cfg)
+    }
+
+    pub fn new(config: qmla_layer_config, w: &MlaWeights) -> Result<Self> {
+        let mut raw: *mut qmla_layer = ptr::null_mut();
+        ok(unsafe {
+            qmla_layer_create(&config, w.wq.as_ptr(), opt_ptr(w.bq), w.wkva.as_ptr(), opt_ptr(w.bkva),
+                              w.ln_w.as_ptr(), opt_ptr(w.ln_b), w.wkvb.as_ptr(), opt_ptr(w.bkvb),
+                              w.wo.as_ptr(), opt_ptr(w.bo), &mut raw)
+        })?;
+        Ok(MlaAttention { raw, config })
+    }
+
+    pub fn workspace_bytes(&self, cache: &KVCache, batch: usize, seq: usize) -> Result<usize> {
+        let mut n = 0usize;
+        ok(unsafe { qmla_layer_workspace_bytes(self.raw, cache.raw, batch as i32, seq as i32, &mut n) })?;
+        Ok(n)
+    }
+
+    /// forward_with_cache (src/model.rs:256-307): xs [batch, seq, hidden]
+    /// -> out, appending the new tokens to sequences 0..batch of `cache`.
+    pub fn forward_with_cache(&self, xs: &DeviceBuffer, batch: usize, seq: usize, cache: &mut KVCache,
+                              out: &mut DeviceBuffer, workspace: &mut DeviceBuffer, stream: &Stream) -> Result<()> {
+        ok(unsafe {
+            qmla_layer_forward_with_cache(self.raw, xs.ptr() as *const f32, batch as i32, seq as i32, cache.raw,
+                                          out.ptr_mut() as *mut f32, workspace.ptr_mut(), workspace.bytes(),
+                                          stream.raw())
+        })
+    }
+
+    /// forward_prefill (src/model.rs:193-253) into empty sequences.
+    pub fn forward_prefill(&self, xs: &DeviceBuffer, batch: usize, seq: usize, cache: &mut KVCache,
+                           out: &mut DeviceBuffer, workspace: &mut DeviceBuffer, stream: &Stream) -> Result<()> {
+        ok(unsafe {
+            qmla_layer_forward_prefill(self.raw, xs.ptr() as *const f32, batch as i32, seq as i32, cache.raw,
+                                       out.ptr_mut() as *mut f32, workspace.ptr_mut(), workspace.bytes(),
+                                       stream.raw())
+        })
+    }
+
+    /// The public tensors of the reference KVCache (src/model.rs:88-92),
+    /// rebuilt through kv_b_proj for sequences seq0..seq0 + n of one length
+    /// T: (k [n, H, T, dn], v [n, H, T, dv], k_rope [n, H, T, dr]) in f32.
+    pub fn materialise(&self, cache: &KVCache, seq0: usize, n: usize, stream: &Stream)
+                       -> Result<(DeviceBuffer, DeviceBuffer, DeviceBuffer, usize)> {
+        let mut ws_bytes = 0usize;
+        ok(unsafe {
+            qmla_cache_materialise_workspace_bytes(self.raw, cache.raw, seq0 as i32, n as i32, &mut ws_bytes)
+        })?;
+        let t = cache.lengths()?[seq0] as usize;
+        let c = &self.config;
+        let (h, dn, dv, dr) = (c.heads as usize, c.qk_nope as usize, c.v_dim as usize, c.qk_rope as usize);
+        let mut k = DeviceBuffer::new(4 * n * h * t * dn)?;
+        let mut v = DeviceBuffer::new(4 * n * h * t * dv)?;
+        let mut kr = DeviceBuffer::new(4 * n * h * t * dr)?;
+        let mut ws = DeviceBuffer::new(ws_bytes)?;
+        ok(unsafe {
+            qmla_cache_materialise(self.raw, cache.raw, seq0 as i32, n as i32, k.ptr_mut() as *mut f32,
+                                   v.ptr_mut() as *mut f32, kr.ptr_mut() as *mut f32, ws.ptr_mut(), ws_bytes,
+                                   stream.raw())
+        })?;
+        stream.synchronize()?;
+        Ok((k, v, kr, t))
+    }
+}
+
+impl Drop for MlaAttention {
+    fn drop(&mut self) {
+        if !self.raw.is_null() {
+            unsafe {
+                qmla_layer_destroy(self.raw);
+            }
+        }
+    }
+}
+
+/// fused_prefill_attn (src/attention_kernel.rs:64-107) on device tensors
+/// q_nope [b,h,sq,dn], q_rope [b,h,sq,dr], k [b,h,sk,dn],
+/// k_rope [b,krh,sk,dr], v [b,h,sk,dv] -> out [b,h,sq,dv].
+pub fn fused_prefill_attn(dims: &qmla_prefill_dims, dtype: DType, q_nope: &DeviceBuffer, q_rope: &DeviceBuffer,
+                          k: &DeviceBuffer, k_rope: &DeviceBuffer, v: &DeviceBuffer, scale: f64, causal: bool,
+                          out: &mut DeviceBuffer, stream: &Stream) -> Result<()> {
+    ok(unsafe {
+        qmla_fused_prefill_attn(dims, dtype.raw(), q_nope.ptr(), q_rope.ptr(), k.ptr(), k_rope.ptr(), v.ptr(),
+                                scale, causal as i32, out.ptr_mut(), stream.raw())
+    })
+}
+
+/// Absorbed-latent decode over sequences 0..dims.batch of `cache`
+/// (attention core of forward_with_cache, src/model.rs:294-303).
+pub fn decode_absorbed(dims: &qmla_decode_dims, cache: &KVCache, q_dtype: DType, q_latent: &DeviceBuffer,
+                       q_rope: &DeviceBuffer, scale: f64, out_latent: &mut DeviceBuffer,
+                       out_lse: Option<&mut DeviceBuffer>, workspace: &mut DeviceBuffer,
+                       stream: &Stream) -> Result<()> {
+    let lse = out_lse.map_or(ptr::null_mut(), |b| b.ptr_mut() as *mut f32);
+    ok(unsafe {
+        qmla_decode_absorbed(dims, cache.raw, q_dtype.raw(), q_latent.ptr(), q_rope.ptr(), scale,
+                             out_latent.ptr_mut() as *mut f32, lse, workspace.ptr_mut(), workspace.bytes(),
+                             stream.raw())
+    })
+}
+
+pub fn decode_workspace_bytes(dims: &qmla_decode_dims, cache: &KVCache) -> Result<usize> {
+    let mut n = 0usize;
+    ok(unsafe { qmla_decode_workspace_bytes(dims, cache.raw, &mut n) })?;
+    Ok(n)
+}
+
+/// PackedQMoETensor (src/tensor.rs:16-122) with its bytes and scales in HBM.
+pub struct PackedQMoETensor {
+    data: DeviceBuffer,
+    scales: DeviceBuffer,
+    pub out_features: usize,
+    pub in_features: usize,
+}
+
+impl PackedQMoETensor {
+    pub fn from_bytes(packed: &[u8], out_features: usize, in_features: usize, scales: &[f32],
+                      stream: &Stream) -> Result<Self> {
+        assert!(packed.len() >= out_features * (in_features / 4) && scales.len() >= out_features);
+        Ok(PackedQMoETensor {
+            data: DeviceBuffer::from_slice(packed, stream)?,
+            scales: DeviceBuffer::from_slice(scales, stream)?,
+            out_features,
+            in_features,
+        })
+    }
+    /// forward_simd (src/tensor.rs:64-95): x [batch, in] -> out [batch, out].
+    pub fn forward(&self, x: &DeviceBuffer, batch: usize, out: &mut DeviceBuffer, stream: &Stream) -> Result<()> {
+        let mut n = 0usize;
+        ok(unsafe {
+            qmla_packed_forward_workspace_bytes(self.out_features as i32, self.in_features as i32, batch as i32,
+                                                &mut n)
+        })?;
+        let mut ws = DeviceBuffer::new(n)?;
+        ok(unsafe {
+            qmla_packed_forward(self.data.ptr() as *const u8, self.scales.ptr() as *const f32,
+                                self.out_features as i32, self.in_features as i32, x.ptr() as *const f32,
+                                batch as i32, out.ptr_mut() as *mut f32, ws.ptr_mut(), n, stream.raw())
+        })
+    }
+}
+
+/// QMoELayer (src/moe.rs:23-131): gate weight and every expert's packed
+/// gate/up/down stacked per kind in HBM.
+pub struct QMoELayer {
+    pub config: qmla_moe_config,
+    gate_weight: DeviceBuffer,
+    packed: [DeviceBuffer; 3],
+    scales: [DeviceBuffer; 3],
+}
+
+impl QMoELayer {
+    /// `packed[k]` / `scales[k]` for k = gate, up, down: [E, I, H/4] /
+    /// [E, I], [E, I, H/4] / [E, I], [E, H, I/4] / [E, H].
+    pub fn new(config: qmla_moe_config, gate_weight: &[f32], packed: [&[u8]; 3], scales: [&[f32]; 3],
+               stream: &Stream) -> Result<Self> {
+        Ok(QMoELayer {
+            config,
+            gate_weight: DeviceBuffer::from_slice(gate_weight, stream)?,
+            packed: [DeviceBuffer::from_slice(packed[0], stream)?, DeviceBuffer::from_slice(packed[1], stream)?,
+                     DeviceBuffer::from_slice(packed[2], stream)?],
+            scales: [DeviceBuffer::from_slice(scales[0], stream)?, DeviceBuffer::from_slice(scales[1], stream)?,
+                     DeviceBuffer::from_slice(scales[2], stream)?],
+        })
+    }
+    pub fn workspace_bytes(&self, seq_len: usize) -> Result<usize> {
+        let mut n = 0usize;
+        ok(unsafe { qmla_moe_workspace_bytes(&self.config, seq_len as i32, &mut n) })?;
+        Ok(n)
+    }
+    /// forward (src/moe.rs:40-130): xs [seq_len, hidden] -> out.
+    pub fn forward(&self, xs: &DeviceBuffer, seq_len: usize, out: &mut DeviceBuffer, workspace: &mut DeviceBuffer,
+                   stream: &Stream) -> Result<()> {
+        ok(unsafe {
+            qmla_moe_forward(&self.config, xs.ptr() as *const f32, seq_len as i32,
+                             self.gate_weight.ptr() as *const f32, self.packed[0].ptr() as *const u8,
+                             self.scales[0].ptr() as *const f32, self.packed[1].ptr() as *const u8,
+                             self.scales[1].ptr() as *const f32, self.packed[2].ptr() as *const u8,
+                             self.scales[2].ptr() as *const f32, out.ptr_mut() as *mut f32, ptr::null_mut(),
+                             ptr::null_mut(), workspace.ptr_mut(), workspace.bytes(), stream.raw())
+        })
+    }
+}
