@@ -74,22 +74,32 @@ def fill_bf16(dst_ptr: int, n: int, seed: int, tmp: qmla.DeviceBuffer, stream):
         done += m
 
 
+STATS = {}  # per-step event statistics of the last time_steps call
+
+
 def time_steps(step, steps: int, warmup: int, stream):
-    """Runs warmup steps, then times exactly `steps` back-to-back steps with
-    one HIP event pair on the launch stream (synchronised on both sides).
-    Returns (wall ms per step, event ms per step)."""
+    """Runs warmup steps, then times exactly `steps` back-to-back steps on
+    the launch stream (synchronised on both sides): one HIP event is recorded
+    before the first step and after every step, so the K steps give K
+    per-step durations (median, p10, p90 in STATS) and the first-to-last
+    event span gives the mean.  Returns (wall ms per step, event ms per
+    step)."""
     for i in range(warmup):
         step(i)
     stream.sync()
-    e0, e1 = qmla.Event(), qmla.Event()
+    ev = [qmla.Event() for _ in range(steps + 1)]
     t0 = time.perf_counter()
-    e0.record(stream)
+    ev[0].record(stream)
     for i in range(steps):
         step(warmup + i)
-    e1.record(stream)
+        ev[i + 1].record(stream)
     stream.sync()
     wall = (time.perf_counter() - t0) * 1e3 / steps
-    return wall, e0.elapsed_ms(e1) / steps
+    per = np.array([ev[i].elapsed_ms(ev[i + 1]) for i in range(steps)])
+    STATS.clear()
+    STATS.update({"p10_ms": float(np.percentile(per, 10)), "median_ms": float(np.median(per)),
+                  "p90_ms": float(np.percentile(per, 90)), "min_ms": float(per.min()), "max_ms": float(per.max())})
+    return wall, ev[0].elapsed_ms(ev[-1]) / steps
 
 
 class DecodeBench:
@@ -139,6 +149,7 @@ class DecodeBench:
             "bytes_per_step": self.cache_bytes,
             "tokens": self.tokens,
             "replicas": self.replicas,
+            "step_ms": dict(STATS),
         }
 
 
@@ -170,7 +181,8 @@ class PrefillBench:
         wall, ev = time_steps(self.step, steps, warmup, self.stream)
         tf = self.flops / (ev * 1e-3) / 1e12
         return {"tflops": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS, "ms_per_step": ev,
-                "wall_ms_per_step": wall, "gflop_per_step": self.flops / 1e9}
+                "wall_ms_per_step": wall, "gflop_per_step": self.flops / 1e9,
+                "tflops_at_median": self.flops / (STATS["median_ms"] * 1e-3) / 1e12, "step_ms": dict(STATS)}
 
 
 class LayerDecodeBench:
@@ -224,7 +236,7 @@ class LayerDecodeBench:
         hbm = self.weight_bytes + self.batch * mean_ctx * ROW_BYTES
         return {"tok_s": self.batch / t, "ms_per_step": ev, "wall_ms_per_step": wall,
                 "weight_bytes": self.weight_bytes, "bytes_per_step": hbm, "tb_s": hbm / t / 1e12,
-                "hbm_frac": hbm / t / 1e12 / (HBM_PEAK_GBS / 1e3)}
+                "hbm_frac": hbm / t / 1e12 / (HBM_PEAK_GBS / 1e3), "step_ms": dict(STATS)}
 
 
 def ref_bench_packed(out_f: int, in_f: int):
@@ -279,7 +291,8 @@ class MoEBench:
         t = ev * 1e-3
         return {"tok_s": self.tokens / t, "ms_per_step": ev, "wall_ms_per_step": wall,
                 "active_experts": active, "bytes_per_step": hbm, "tb_s": hbm / t / 1e12,
-                "hbm_frac": hbm / t / 1e12 / (HBM_PEAK_GBS / 1e3), "replicas": len(self.layers)}
+                "hbm_frac": hbm / t / 1e12 / (HBM_PEAK_GBS / 1e3), "replicas": len(self.layers),
+                "step_ms": dict(STATS)}
 
 
 def moe_cpu_baseline(min_seconds=5.0):
@@ -302,7 +315,7 @@ def moe_cpu_baseline(min_seconds=5.0):
         if dt >= min_seconds:
             break
     per = dt / reps
-    return {"value": xs.shape[0] / per, "unit": "tok/s", "cores": 1, "kind": "port",
+    return {"value": xs.shape[0] / per, "unit": "tok/s", "cores": 1, "kind": "port", "cpu_model": cpu_model(),
             "sample": f"the full 16-token step x {reps} runs = {dt:.1f} s on 1 thread "
                       f"({per * 1e3:.0f} ms per step); f32 C restatement (oracle/moe_oracle.c)"}
 
@@ -339,7 +352,7 @@ def cpu_baseline(lens, heads, sample_seqs, min_seconds=10.0):
     per1, reps1 = timed(one, 1, min_seconds / 4)
     full1 = per1 * total / float(one.sum())
     O.set_num_threads(threads)
-    return {"value": len(lens) / full, "unit": "tok/s", "cores": threads, "kind": "port",
+    return {"value": len(lens) / full, "unit": "tok/s", "cores": threads, "kind": "port", "cpu_model": cpu_model(),
             "sample": f"first {len(sample)} of {len(lens)} sequences ({int(sample.sum())} of {int(total)} tokens, "
                       f"{heads} heads) x {reps} runs = {per * reps:.1f} s on {threads} threads; scaled by token "
                       f"count to the full batch ({full * 1e3:.0f} ms per step); absorbed-latent f32 C restatement "
@@ -347,6 +360,81 @@ def cpu_baseline(lens, heads, sample_seqs, min_seconds=10.0):
             "single_thread": {"value": len(lens) / full1, "unit": "tok/s", "cores": 1,
                               "sample": f"sequence 0 ({int(one.sum())} tokens) x {reps1} runs = "
                                         f"{per1 * reps1:.1f} s; {full1:.1f} s per full step"}}
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def blas_threads() -> int:
+    try:
+        import threadpoolctl
+        return max([int(i.get("num_threads", 1)) for i in threadpoolctl.threadpool_info()
+                    if i.get("user_api") == "blas"] or [1])
+    except Exception:
+        return 1
+
+
+def _repeat(fn, min_seconds):
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds:
+            return dt / reps, reps
+
+
+def cpu_baseline_v2lite(sample_seqs=4, batch=32, heads=16, ctx=4096, min_seconds=5.0):
+    """The reference's decode attention in its own (decompressed) form on
+    the host: for each step, KVCache::append's cat of the cache along T and
+    scores / softmax / @ v over the per-head f32 K, V, k_rope
+    (src/model.rs:291-303), numpy with the matmuls on BLAS.  Bounded sample:
+    `sample_seqs` of the `batch` sequences, scaled by sequence count."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O  # checker library, used here only as the CPU baseline
+
+    b = sample_seqs
+    k, v = O.normal((b, heads, ctx, 128), 61), O.normal((b, heads, ctx, 128), 62)
+    kr = O.normal((b, heads, ctx, 64), 63)
+    kn, vn, krn = O.normal((b, heads, 1, 128), 64), O.normal((b, heads, 1, 128), 65), O.normal((b, heads, 1, 64), 66)
+    qn, qr = O.normal((b, heads, 1, 128), 67), O.normal((b, heads, 1, 64), 68)
+    per, reps = _repeat(lambda: O.blas_decode_step(qn, qr, k, v, kr, kn, vn, krn, SCALE), min_seconds)
+    full = per * batch / b
+    th = blas_threads()
+    return {"value": batch / full, "unit": "tok/s", "cores": th, "kind": "port", "cpu_model": cpu_model(),
+            "sample": f"{b} of {batch} sequences x {reps} steps = {per * reps:.1f} s; scaled by sequence count "
+                      f"({full * 1e3:.0f} ms per step); the reference's decompressed form (f32 per-head K/V/k_rope "
+                      f"[b,16,4097,d], cache cat + scores + softmax + @v, src/model.rs:291-303) in numpy on "
+                      f"{th} BLAS threads (oracle.blas_decode_step)"}
+
+
+def cpu_baseline_prefill(min_seconds=5.0):
+    """The reference's tiled fused_prefill_attn (src/attention_kernel.rs:64-107)
+    on the host at the causal workload's shapes (f32, numpy with BLAS
+    matmuls): one of the 4 sequences (16 heads x 2048 tokens), scaled by 4."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O  # checker library, used here only as the CPU baseline
+
+    s = 2048
+    qn, qr = O.normal((1, 16, s, 128), 71), O.normal((1, 16, s, 64), 72)
+    k, kr, v = O.normal((1, 16, s, 128), 73), O.normal((1, 16, s, 64), 74), O.normal((1, 16, s, 128), 75)
+    per, reps = _repeat(lambda: O.blas_fused_prefill_attn(qn, qr, k, kr, v, SCALE, True), min_seconds)
+    full = per * 4
+    flops = 4 * 16 * (s * (s + 1) // 2) * 2 * (192 + 128)
+    th = blas_threads()
+    return {"value": flops / full / 1e12, "unit": "TFLOP/s", "cores": th, "kind": "port", "cpu_model": cpu_model(),
+            "sample": f"1 of 4 sequences (16 heads x 2048 tokens) x {reps} runs = {per * reps:.1f} s; scaled by 4 "
+                      f"({full * 1e3:.0f} ms per call); the reference's tiled form (query tiles of "
+                      f"{O.tile_size(s)}, full-row softmax, per-head k_rope) in numpy on {th} BLAS threads "
+                      f"(oracle.blas_fused_prefill_attn); unmasked-pair flops as the GPU line"}
 
 
 def copy_calibration(stream, n=256 << 20, reps=4):
@@ -393,6 +481,8 @@ def main():
                     help="only run the 2-bit packed MoE layer line (for profiling)")
     ap.add_argument("--layer-only", action="store_true",
                     help="only run the MLA layer decode step line (for profiling)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only run the two prefill lines (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the decode path shards by batch "
@@ -413,6 +503,14 @@ def main():
         lb = LayerDecodeBench(stream, seed=51)
         print(json.dumps({"layer_decode_step": lb.run(args.steps, args.warmup)}), flush=True)
         return
+    if args.prefill_only:
+        res = {}
+        for name, dims in (("causal_prefill", (4, 16, 2048, 2048, 0)), ("chunked_prefill", (8, 128, 512, 8704, 8192))):
+            pb = PrefillBench(*dims, stream, seed=31 if name == "causal_prefill" else 41)
+            res[name] = pb.run(args.steps, args.warmup)
+            del pb
+        print(json.dumps(res), flush=True)
+        return
 
     lens = synth.v3_decode_lengths()
     log(f"v3 decode: batch {len(lens)}, {int(lens.sum())} tokens, {int(lens.sum()) * ROW_BYTES / 1e9:.3f} GB latent")
@@ -426,16 +524,20 @@ def main():
     if not args.no_secondary:
         d2 = DecodeBench(np.full(32, 4097, np.int32), 16, stream, seed=21)
         secondary["v2lite_decode"] = {"workload": "16 heads, batch 32, 4096 cached + 1, bf16 latent", **d2.run(args.steps, args.warmup)}
+        if not args.no_cpu_baseline:
+            secondary["v2lite_decode"]["cpu_baseline"] = cpu_baseline_v2lite()
         log("v2lite decode", json.dumps(secondary["v2lite_decode"]))
         del d2
         p3 = PrefillBench(4, 16, 2048, 2048, 0, stream, seed=31)
         secondary["causal_prefill"] = {"workload": "batch 4, 2048 tokens, 16 heads, dn 128 dr 64 dv 128, bf16, causal",
                                        **p3.run(args.steps, args.warmup)}
+        if not args.no_cpu_baseline:
+            secondary["causal_prefill"]["cpu_baseline"] = cpu_baseline_prefill()
         log("causal prefill", json.dumps(secondary["causal_prefill"]))
         del p3
         p5 = PrefillBench(8, 128, 512, 8704, 8192, stream, seed=41)
         secondary["chunked_prefill"] = {"workload": "batch 8, 8192 cached + 512 new, 128 heads, bf16, causal in chunk",
-                                        **p5.run(max(3, args.steps // 4), max(1, args.warmup // 2))}
+                                        **p5.run(args.steps, max(1, args.warmup // 2))}
         log("chunked prefill", json.dumps(secondary["chunked_prefill"]))
         del p5
         lb = LayerDecodeBench(stream, seed=51)
@@ -486,6 +588,7 @@ def main():
             "batch": int(len(lens)), "heads": 128, "kv_lora_rank": 512, "rope_dim": 64,
             "tokens": main_res["tokens"], "cache_replicas": main_res["replicas"],
         },
+        "step_ms": main_res["step_ms"],
         "hbm_gbs": main_res["hbm_gbs"],
         "hbm_frac": main_res["hbm_frac"],
         "roofline": {

@@ -252,6 +252,59 @@ def decode_absorbed(q_lat, q_rope, cache, offsets, lens, scale: float, f64: bool
     return out, lse
 
 
+# ------------------------------------- the reference's op sequence (BLAS) --
+# numpy restatements that keep the reference's tensor operations in its
+# order, with the matmuls on numpy's BLAS (OpenBLAS, multithreaded) as
+# candle's are on OpenBLAS sgemm (Cargo.toml:36).  They exist to time the
+# reference's CPU path as a baseline; tests pin them to the C oracle.
+
+MASK_NEG = np.float32(-1e18)
+
+
+def _softmax_last(x: np.ndarray) -> np.ndarray:
+    """candle_nn::ops::softmax over the last dim: max-subtract, exp, sum, divide."""
+    m = x.max(axis=-1, keepdims=True)
+    e = np.exp(x - m)
+    return e / e.sum(axis=-1, keepdims=True)
+
+
+def blas_fused_prefill_attn(q_nope, q_rope, k, k_rope, v, scale: float, causal: bool, q_offset: int = 0):
+    """fused_prefill_attn, src/attention_kernel.rs:64-107: per query tile of
+    tile_size(S) rows, scores = (q_nope k^T + q_rope k_rope^T) * scale
+    (:89-92), the causal mask of make_causal_mask (:14-31, :94-98), softmax
+    (:100), @ v (:101), tiles concatenated (:106).  k_rope [b, 1 or h, S, dr]."""
+    q_nope, q_rope, k, k_rope, v = (np.asarray(x, np.float32) for x in (q_nope, q_rope, k, k_rope, v))
+    sq, sk = q_nope.shape[2], k.shape[2]
+    tile = tile_size(sq)
+    kt = np.ascontiguousarray(np.swapaxes(k, 2, 3))        # k.transpose(2, 3).contiguous() (:76)
+    krt = np.ascontiguousarray(np.swapaxes(k_rope, 2, 3))  # (:77)
+    cols = np.arange(sk)
+    outs = []
+    for t0 in range(0, sq, tile):
+        t1 = min(t0 + tile, sq)
+        sc = (np.matmul(q_nope[:, :, t0:t1], kt) + np.matmul(q_rope[:, :, t0:t1], krt)) * np.float32(scale)
+        if causal:
+            rows = q_offset + np.arange(t0, t1)
+            sc = sc + np.where(rows[:, None] < cols[None, :], MASK_NEG, np.float32(0))
+        outs.append(np.matmul(_softmax_last(sc).astype(np.float32), v))
+    return np.concatenate(outs, axis=2)
+
+
+def blas_decode_step(q_nope, q_rope, k, v, k_rope, k_new, v_new, k_rope_new, scale: float):
+    """The attention part of MlaAttention::forward_with_cache,
+    src/model.rs:291-303, over the decompressed cache: KVCache::append
+    (:99-104, a cat along T that copies the cache), the rope keys re-joined
+    (:294-295), scores q_nope k^T + q_rope k_rope^T over every cached token,
+    scale, softmax, @ v (no mask, :297-302).  Shapes [b, H, T, d]; the new
+    token tensors [b, H, s, d].  Returns (context [b, H, s, dv], new k, v, k_rope)."""
+    k = np.concatenate([k, k_new], axis=2)
+    v = np.concatenate([v, v_new], axis=2)
+    k_rope = np.concatenate([k_rope, k_rope_new], axis=2)
+    sc = np.matmul(q_nope, np.swapaxes(k, 2, 3)) + np.matmul(q_rope, np.swapaxes(k_rope, 2, 3))
+    sc = sc * np.float32(scale)
+    return np.matmul(_softmax_last(sc).astype(np.float32), v), k, v, k_rope
+
+
 def num_threads() -> int:
     return lib().orc_num_threads()
 

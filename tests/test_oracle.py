@@ -289,3 +289,27 @@ def test_prefill_layer_equals_manual_composition():
     lat0 = np.zeros((2, 0, 40), np.float32)
     dec1, _ = O.mla_forward_with_latent(L, xs[:, :1], lat0)
     assert rel_err(out1, dec1) < 1e-5
+
+
+def test_blas_restatements_equal_the_c_oracle():
+    """The numpy/BLAS restatements of the reference's op sequence (used to
+    time the reference's CPU path) agree with the C oracle: the tiled
+    prefill (tile boundaries at 64 / 32 / 16 rows), with and without a
+    causal offset, and the decode step over a decompressed cache equals the
+    unmasked oracle attention over the appended cache."""
+    for (b, h, s, krh, off, causal) in ((1, 2, 70, 1, 0, True), (2, 3, 1100, 3, 0, True),
+                                        (1, 2, 40, 1, 300, True), (1, 1, 33, 1, 0, False)):
+        sk = s + off
+        qn, qr = O.normal((b, h, s, 32), 1), O.normal((b, h, s, 16), 2)
+        k, kr, v = O.normal((b, h, sk, 32), 3), O.normal((b, krh, sk, 16), 4), O.normal((b, h, sk, 24), 5)
+        ref = O.fused_prefill_attn(qn, qr, k, kr, v, 0.15, causal, q_offset=off)
+        got = O.blas_fused_prefill_attn(qn, qr, k, kr, v, 0.15, causal, q_offset=off)
+        assert np.abs(got - ref).max() <= 2e-5 * np.abs(ref).max()
+    b, H, T, s = 2, 4, 300, 1
+    k, v, kr = O.normal((b, H, T, 32), 6), O.normal((b, H, T, 24), 7), O.normal((b, H, T, 16), 8)
+    kn, vn, krn = O.normal((b, H, s, 32), 9), O.normal((b, H, s, 24), 10), O.normal((b, H, s, 16), 11)
+    qn, qr = O.normal((b, H, s, 32), 12), O.normal((b, H, s, 16), 13)
+    ctx, k2, v2, kr2 = O.blas_decode_step(qn, qr, k, v, kr, kn, vn, krn, 0.2)
+    assert k2.shape == (b, H, T + s, 32) and np.array_equal(k2[:, :, T:], kn)
+    ref = O.fused_prefill_attn(qn, qr, k2, kr2, v2, 0.2, False)
+    assert np.abs(ctx - ref).max() <= 2e-5 * np.abs(ref).max()
