@@ -58,8 +58,9 @@ __device__ int32_t block_exclusive_scan(int32_t *a, int32_t n, int32_t *tmp) {
 // One block builds the segment list.  LDS: P[batch] prefix, S[batch] slot
 // base, C[blocks] segment counts, tmp[kPlanThreads].
 __global__ __launch_bounds__(kPlanThreads) void k_decode_plan(const int32_t *__restrict__ lens,
-                                                              int32_t batch, int32_t blocks,
-                                                              int32_t chunk, DecodePlanView plan) {
+                                                              int32_t pending, int32_t batch,
+                                                              int32_t blocks, int32_t chunk,
+                                                              DecodePlanView plan) {
   extern __shared__ int32_t sm[];
   int32_t *P = sm;               // [batch + 1]
   int32_t *S = P + batch + 1;    // [batch]
@@ -67,7 +68,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_decode_plan(const int32_t *__r
   int32_t *tmp = C + blocks + 1; // [kPlanThreads]
   const int tid = threadIdx.x;
 
-  for (int b = tid; b < batch; b += kPlanThreads) P[b] = lens[b];
+  for (int b = tid; b < batch; b += kPlanThreads) P[b] = lens[b] + pending;
   __syncthreads();
   const int32_t N = block_exclusive_scan(P, batch, tmp);
   if (tid == 0) P[batch] = N;
@@ -235,8 +236,11 @@ __global__ __launch_bounds__(256) void k_decode_merge(int32_t rows, int32_t r, D
                                                        const float *__restrict__ part_o,
                                                        const float *__restrict__ part_lse,
                                                        float *__restrict__ out,
-                                                       float *__restrict__ out_lse) {
+                                                       float *__restrict__ out_lse,
+                                                       int32_t *__restrict__ adv_lens, int32_t adv) {
   const int b = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
+  // lengths grow by the pending tokens the decode attended (it has finished)
+  if (adv_lens && m == 0 && tid == 0) adv_lens[b] += adv;
   const int32_t n = plan.seq_nslots[b];
   const int64_t qrow = (int64_t)b * rows + m;
   if (n == 1) return;
@@ -296,20 +300,22 @@ DecodePlanView decode_plan_view(void *ws, int32_t batch, int32_t blocks) {
   return v;
 }
 
-qmla_status launch_decode_plan(const qmla_kv_cache *cache, int32_t batch, int32_t blocks,
-                               int32_t chunk, DecodePlanView plan, hipStream_t stream) {
+qmla_status launch_decode_plan(const qmla_kv_cache *cache, int32_t pending, int32_t batch,
+                               int32_t blocks, int32_t chunk, DecodePlanView plan,
+                               hipStream_t stream) {
   size_t lds = sizeof(int32_t) * ((size_t)batch + 1 + batch + blocks + 1 + kPlanThreads);
-  k_decode_plan<<<dim3(1), dim3(kPlanThreads), lds, stream>>>(cache->d_lens, batch, blocks, chunk,
-                                                             plan);
+  k_decode_plan<<<dim3(1), dim3(kPlanThreads), lds, stream>>>(cache->d_lens, pending, batch,
+                                                             blocks, chunk, plan);
   QMLA_LAUNCH_CHECK("k_decode_plan");
   return QMLA_OK;
 }
 
 qmla_status launch_decode_merge(int32_t batch, int32_t rows, int32_t r, DecodePlanView plan,
                                 const float *part_o, const float *part_lse, float *out,
-                                float *out_lse, hipStream_t stream) {
+                                float *out_lse, int32_t *adv_lens, int32_t adv,
+                                hipStream_t stream) {
   k_decode_merge<<<dim3(batch, rows), dim3(256), 0, stream>>>(rows, r, plan, part_o, part_lse,
-                                                             out, out_lse);
+                                                             out, out_lse, adv_lens, adv);
   QMLA_LAUNCH_CHECK("k_decode_merge");
   return QMLA_OK;
 }
@@ -401,6 +407,16 @@ qmla_status decode_impl(const qmla_decode_dims *d, const qmla_kv_cache *c, qmla_
   QMLA_REQUIRE(q_rope || d->rope_dim == 0, QMLA_ERR_INVALID_ARG, "NULL q_rope");
   QMLA_REQUIRE(splits >= 0, QMLA_ERR_INVALID_ARG, "negative split count");
   QMLA_REQUIRE(std::isfinite(scale), QMLA_ERR_INVALID_ARG, "non-finite scale");
+  return decode_launch(d, c, q_dtype, q_latent, q_rope, scale, out, out_lse, splits, ws, ws_bytes,
+                       0, false, as_stream(stream));
+}
+
+}  // namespace
+
+qmla_status qmla::decode_launch(const qmla_decode_dims *d, const qmla_kv_cache *c,
+                                qmla_dtype q_dtype, const void *q_latent, const void *q_rope,
+                                double scale, float *out, float *out_lse, int32_t splits, void *ws,
+                                size_t ws_bytes, int32_t pending, bool advance, hipStream_t s) {
   const int32_t blocks = choose_blocks(d, c, splits);
   const bool mfma = c->dtype == QMLA_BF16;
   if (mfma)
@@ -410,14 +426,13 @@ qmla_status decode_impl(const qmla_decode_dims *d, const qmla_kv_cache *c, qmla_
   DecodeWorkspace lay = decode_workspace_layout(d->batch, d->rows, d->kv_lora_rank, blocks, mfma);
   QMLA_REQUIRE(ws != nullptr && ws_bytes >= lay.total, QMLA_ERR_WORKSPACE,
                "workspace of %zu bytes < required %zu", ws_bytes, lay.total);
-  hipStream_t s = as_stream(stream);
   DecodePlanView plan{};
   if (!mfma) {
     plan = decode_plan_view(ws, d->batch, blocks);
     int64_t total = 0;
     for (int32_t i = 0; i < d->batch; ++i) total += c->h_lens[i];
     int32_t chunk = (int32_t)std::max<int64_t>(1, (total + blocks - 1) / blocks);
-    QMLA_TRY(launch_decode_plan(c, d->batch, blocks, chunk, plan, s));
+    QMLA_TRY(launch_decode_plan(c, pending, d->batch, blocks, chunk, plan, s));
   }
   DecodeArgs a;
   a.cache = c;
@@ -436,11 +451,15 @@ qmla_status decode_impl(const qmla_decode_dims *d, const qmla_kv_cache *c, qmla_
   a.part_o = reinterpret_cast<float *>(static_cast<char *>(ws) + lay.part_o_off);
   a.part_lse = reinterpret_cast<float *>(static_cast<char *>(ws) + lay.part_lse_off);
   a.blocks = blocks;
+  a.pending = pending;
+  a.advance = advance;
   if (mfma) return launch_decode_mfma(a, s);  // decode + merge
   QMLA_TRY(launch_decode_f32(a, s));
   return launch_decode_merge(d->batch, d->rows, d->kv_lora_rank, plan, a.part_o, a.part_lse, out,
-                             out_lse, s);
+                             out_lse, advance ? c->d_lens : nullptr, pending, s);
 }
+
+namespace {
 
 // ------------------------------------------- allocation-free decode -----
 // Scratch of qmla_decode_absorbed_noalloc: the decode workspace (plan or

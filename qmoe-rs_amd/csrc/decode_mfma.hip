@@ -569,13 +569,13 @@ __device__ int32_t lds_exscan(int32_t *a, int32_t n, int32_t *tmp) {
 // virtual stream, sequence b occupies [P[b], P[b + 1]) with its real
 // tokens at [P[b] + seg_tokens, P[b + 1]).
 template <int NT>
-__device__ void plan_round(const int32_t *__restrict__ lens, int32_t batch, int32_t from,
-                           int32_t seg_tokens, int32_t *scratch, SegDesc *list, int32_t *meta,
-                           int2 *__restrict__ seq_info) {
+__device__ void plan_round(const int32_t *__restrict__ lens, int32_t pending, int32_t batch,
+                           int32_t from, int32_t seg_tokens, int32_t *scratch, SegDesc *list,
+                           int32_t *meta, int2 *__restrict__ seq_info) {
   const int tid = threadIdx.x;
   const int blocks = gridDim.x, piece = blockIdx.x;
   int32_t *P = scratch, *SB = scratch + batch + 1, *tmp = SB + batch + 1;
-  for (int b = tid; b < batch; b += NT) P[b] = lens[b] + seg_tokens;
+  for (int b = tid; b < batch; b += NT) P[b] = lens[b] + pending + seg_tokens;
   __syncthreads();
   const int32_t N = lds_exscan<NT>(P, batch, tmp);
   if (tid == 0) P[batch] = N;
@@ -631,7 +631,8 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
     const uint8_t *__restrict__ pool, const int64_t *__restrict__ offsets,
     const int32_t *__restrict__ lens, int32_t batch, const QT *__restrict__ q_lat,
     const QT *__restrict__ q_rope, int32_t rows, float scale_log2, int32_t seg_tokens,
-    int2 *__restrict__ seq_info, float *__restrict__ part_o, float *__restrict__ part_lse) {
+    int32_t pending, int2 *__restrict__ seq_info, float *__restrict__ part_o,
+    float *__restrict__ part_lse) {
   using SH = DecodeShape<R, DR>;
   using PS = PvSplit<R, NW>;
   static_assert(NSTAGE >= 3, "the pipelined loop keeps two stages resident");
@@ -683,7 +684,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
 
   int32_t next_seq = 0;
   do {
-  plan_round<NW * 64>(lens, batch, next_seq, seg_tokens, (int32_t *)ring_raw, seg_list, seg_meta,
+  plan_round<NW * 64>(lens, pending, batch, next_seq, seg_tokens, (int32_t *)ring_raw, seg_list, seg_meta,
                       seq_info);
   const int32_t nseg = __builtin_amdgcn_readfirstlane(seg_meta[0]);
   next_seq = __builtin_amdgcn_readfirstlane(seg_meta[1]);
@@ -880,8 +881,12 @@ template <int R>
 __global__ __launch_bounds__(256) void k_decode_merge_frag(
     int32_t rows, int32_t row_blocks, const int2 *__restrict__ seq_info,
     const float *__restrict__ part_o, const float *__restrict__ part_lse, float *__restrict__ out,
-    float *__restrict__ out_lse) {
+    float *__restrict__ out_lse, int32_t *__restrict__ adv_lens, int32_t adv, int32_t adv_n) {
   constexpr int CB = R / 32;
+  // lengths that the decode read as lens + pending become lens + pending
+  // here, after the decode kernel (which read them) has finished
+  if (adv_lens && blockIdx.x == 0 && blockIdx.y == 0)
+    for (int i = threadIdx.x; i < adv_n; i += blockDim.x) adv_lens[i] += adv;
   __shared__ float tile[4][32][33];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int cb = blockIdx.y * 4 + wave;
@@ -994,7 +999,8 @@ __global__ __launch_bounds__(256) void k_decode_narrow(
     const uint8_t *__restrict__ pool, const int64_t *__restrict__ offsets,
     const int32_t *__restrict__ lens, int32_t batch, const QT *__restrict__ q_lat,
     const QT *__restrict__ q_rope, int32_t rows, float scale_log2, int32_t seg_tokens,
-    int2 *__restrict__ seq_info, float *__restrict__ part_o, float *__restrict__ part_lse) {
+    int32_t pending, int2 *__restrict__ seq_info, float *__restrict__ part_o,
+    float *__restrict__ part_lse) {
   using SH = DecodeShape<R, DR>;
   constexpr int NW = 4, NSTAGE = kNarrowStages;
   constexpr int KQ = SH::KSTEPS / NW;  // k-steps of this wave's S^T quarter
@@ -1054,7 +1060,7 @@ __global__ __launch_bounds__(256) void k_decode_narrow(
 
   int32_t next_seq = 0;
   do {
-  plan_round<NW * 64>(lens, batch, next_seq, seg_tokens, (int32_t *)ring_raw, seg_list, seg_meta,
+  plan_round<NW * 64>(lens, pending, batch, next_seq, seg_tokens, (int32_t *)ring_raw, seg_list, seg_meta,
                       seq_info);
   const int32_t nseg = __builtin_amdgcn_readfirstlane(seg_meta[0]);
   next_seq = __builtin_amdgcn_readfirstlane(seg_meta[1]);
@@ -1290,8 +1296,9 @@ template <int R>
 qmla_status launch_merge(const DecodeArgs &a, hipStream_t stream) {
   const int row_blocks = (a.rows + 31) / 32;
   dim3 mgrid((unsigned)(a.batch * row_blocks), (R / 32 + 3) / 4);
-  k_decode_merge_frag<R><<<mgrid, dim3(256), 0, stream>>>(a.rows, row_blocks, a.seq_info,
-                                                          a.part_o, a.part_lse, a.out, a.out_lse);
+  k_decode_merge_frag<R><<<mgrid, dim3(256), 0, stream>>>(
+      a.rows, row_blocks, a.seq_info, a.part_o, a.part_lse, a.out, a.out_lse,
+      a.advance ? a.cache->d_lens : nullptr, a.pending, a.batch);
   QMLA_LAUNCH_CHECK("k_decode_merge_frag");
   return QMLA_OK;
 }
@@ -1310,13 +1317,13 @@ qmla_status launch_shape(const DecodeArgs &a, hipStream_t stream) {
     QMLA_TRY(ensure_dynamic_lds((const void *)k, lds));
     k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, a.cache->d_lens, a.batch,
                                     (const uint16_t *)a.q_lat, (const uint16_t *)a.q_rope, a.rows,
-                                    sl2, seg_tokens, a.seq_info, a.part_o, a.part_lse);
+                                    sl2, seg_tokens, a.pending, a.seq_info, a.part_o, a.part_lse);
   } else {
     auto k = k_decode_mfma<R, DR, NW, NSTAGE, float>;
     QMLA_TRY(ensure_dynamic_lds((const void *)k, lds));
     k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, a.cache->d_lens, a.batch,
                                     (const float *)a.q_lat, (const float *)a.q_rope, a.rows, sl2,
-                                    seg_tokens, a.seq_info, a.part_o, a.part_lse);
+                                    seg_tokens, a.pending, a.seq_info, a.part_o, a.part_lse);
   }
   QMLA_LAUNCH_CHECK("k_decode_mfma");
   return launch_merge<R>(a, stream);
@@ -1334,13 +1341,13 @@ qmla_status launch_narrow(const DecodeArgs &a, hipStream_t stream) {
     QMLA_TRY(ensure_dynamic_lds((const void *)k, lds));
     k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, a.cache->d_lens, a.batch,
                                     (const uint16_t *)a.q_lat, (const uint16_t *)a.q_rope, a.rows,
-                                    sl2, seg_tokens, a.seq_info, a.part_o, a.part_lse);
+                                    sl2, seg_tokens, a.pending, a.seq_info, a.part_o, a.part_lse);
   } else {
     auto k = k_decode_narrow<R, DR, float>;
     QMLA_TRY(ensure_dynamic_lds((const void *)k, lds));
     k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, a.cache->d_lens, a.batch,
                                     (const float *)a.q_lat, (const float *)a.q_rope, a.rows, sl2,
-                                    seg_tokens, a.seq_info, a.part_o, a.part_lse);
+                                    seg_tokens, a.pending, a.seq_info, a.part_o, a.part_lse);
   }
   QMLA_LAUNCH_CHECK("k_decode_narrow");
   return launch_merge<R>(a, stream);

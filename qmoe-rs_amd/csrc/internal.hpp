@@ -72,11 +72,21 @@ DecodeWorkspace decode_workspace_layout(int32_t batch, int32_t rows, int32_t r, 
                                         bool mfma);
 DecodePlanView decode_plan_view(void *ws, int32_t batch, int32_t blocks);
 
-qmla_status launch_decode_plan(const qmla_kv_cache *cache, int32_t batch, int32_t blocks,
-                               int32_t chunk, DecodePlanView plan, hipStream_t stream);
+qmla_status launch_decode_plan(const qmla_kv_cache *cache, int32_t pending, int32_t batch,
+                               int32_t blocks, int32_t chunk, DecodePlanView plan,
+                               hipStream_t stream);
+// The decode of qmla_decode_absorbed[_splits] with `pending` tokens per
+// sequence already written past the device lengths (see DecodeArgs); with
+// `advance` the lengths grow by `pending` once the merge has run.  The
+// caller has validated the shapes; the host length mirror is the caller's.
+qmla_status decode_launch(const qmla_decode_dims *d, const qmla_kv_cache *c, qmla_dtype q_dtype,
+                          const void *q_latent, const void *q_rope, double scale, float *out,
+                          float *out_lse, int32_t splits, void *ws, size_t ws_bytes,
+                          int32_t pending, bool advance, hipStream_t stream);
 qmla_status launch_decode_merge(int32_t batch, int32_t rows, int32_t r, DecodePlanView plan,
                                 const float *part_o, const float *part_lse, float *out,
-                                float *out_lse, hipStream_t stream);
+                                float *out_lse, int32_t *adv_lens, int32_t adv,
+                                hipStream_t stream);
 
 // Attention cores (decode_f32.hip / decode_mfma.hip).
 struct DecodeArgs {
@@ -93,6 +103,11 @@ struct DecodeArgs {
   float *part_o;
   float *part_lse;
   int32_t blocks;
+  // Tokens already written past each of the batch's device lengths (the
+  // layer's new rows): the decode attends lens + pending tokens, and with
+  // `advance` the merge then adds pending to the lengths.
+  int32_t pending;
+  bool advance;
 };
 // Largest batch and piece count one decode call plans for.
 constexpr int32_t kMaxPlanBatch = 8192;
@@ -117,6 +132,46 @@ qmla_status launch_prefill_bf16(const qmla_prefill_dims &d, const uint16_t *q_no
                                 const uint16_t *q_rope, const uint16_t *k,
                                 const uint16_t *k_rope, const uint16_t *v, float scale,
                                 int causal, uint16_t *out, hipStream_t stream);
+
+// Skinny projections (skinny_gemm.hip): y[m][n] = sum_k x[m][k] W[n][k]
+// (+ bias[n]) for M <= 32 token rows, per z (a head) with z-strides; W in
+// the fragment-major bf16 hi/lo layout of skinny_pack.  Epilogue modes:
+constexpr int kSkinnyFinal = 0;  // y[z sy + m ldy + n]
+constexpr int kSkinnyQkv = 1;    // [q_proj | kv_a_proj_with_mqa] -> q_nope, roped q_rope, kva
+constexpr int kSkinnyPackB = 2;  // y: the next product's B operand, k = z sy + n (2 KB per 16 k)
+struct SkinnyGemmArgs {
+  const void *w_frag;  // fragment-major bf16 hi/lo weights (skinny_pack)
+  const float *x;      // [Z][M][K]: row stride ldx, z-stride sx; or, with
+  int64_t ldx, sx;     // x_packed, a PACKB output (Z = 1)
+  bool x_packed;
+  const float *bias;   // [Z][N], z-stride sb, or null
+  int64_t sb;
+  float *y;            // FINAL: [Z][M][N], row stride ldy, z-stride sy
+  int64_t ldy, sy;
+  int M, N, K, Z;
+  int mode;
+  // QKV: token m of this launch is token m0 + m of the call, sequence
+  // (m0 + m) / seq, position lens[seq] + (m0 + m) % seq.
+  int m0, seq, heads, dn, dr;
+  float *q_nope;  // [tokens][heads][dn]
+  float *q_rope;  // [tokens][heads][dr]
+  float *kva;     // [tokens][kva_ld]
+  int64_t kva_ld;
+  const int32_t *lens;
+  const float *inv_freq;
+  float mscale;
+};
+struct LatentRowsArgs;
+int skinny_waves(int K);
+// Fragment-major hi/lo packing of W [Z][N][K] (row stride ldw, z-stride sw,
+// f32, host memory) into out (skinny_frag_bytes(N, K, Z) bytes).
+size_t skinny_frag_bytes(int N, int K, int Z);
+void skinny_pack(const float *W, int64_t ldw, int64_t sw, int N, int K, int Z, uint8_t *out);
+bool skinny_supported(int M, int K);
+// With `rows`, the launch also writes the latent cache rows of n_rows new
+// tokens (latent_rows.hpp) in extra blocks.
+qmla_status launch_skinny_gemm(const SkinnyGemmArgs &a, hipStream_t stream,
+                               const LatentRowsArgs *rows = nullptr, int n_rows = 0);
 
 // Cache row writer shared by the cache API and the layer: copies/converts
 // n_seqs x n_new rows (row-major [n_seqs, n_new, row_elems]) into sequences

@@ -26,13 +26,23 @@
 
 #include <rocblas/rocblas.h>
 
-#include "internal.hpp"
+#include "latent_rows.hpp"
 
 struct qmla_layer {
   qmla_layer_config cfg{};
   float *wq = nullptr, *bq = nullptr, *wkva = nullptr, *bkva = nullptr, *ln_w = nullptr,
         *ln_b = nullptr, *wkvb = nullptr, *bkvb = nullptr, *wo = nullptr, *bo = nullptr;
   float *inv_freq = nullptr;  // [dr / 2], src/model.rs:56-58
+  // Fragment-major bf16 hi/lo halves of the decode-step projections
+  // (skinny_gemm.hip), packed from:
+  //   w1   [H(dn+dr) + r + dr][hidden]  q_proj rows, then kv_a_proj_with_mqa rows
+  //   wuk  [H][r][dn]                   W_UK^h transposed (kv_b rows h(dn+dv) .. +dn)
+  //   wuv  [H][dv][r]                   W_UV^h (kv_b rows h(dn+dv)+dn .. +dv)
+  //   wo   [hidden][H dv]               o_proj
+  void *w1f = nullptr, *wukf = nullptr, *wuvf = nullptr, *wof = nullptr;
+  float *b1 = nullptr;   // [bq | bkva]
+  float *buv = nullptr;  // [H][dv]: b_V^h
+  bool skinny = false;   // the split weights exist (every K a multiple of 16)
   std::vector<void *> allocs;
   rocblas_handle blas = nullptr;
   mutable std::mutex blas_mu;
@@ -154,57 +164,31 @@ __device__ inline float block_sum(float v, float *red) {
 }
 
 // Latent rows of new tokens, written straight into the cache (the append of
-// src/model.rs:99-104 fused in): one block per token (b, i),
-//   row = [LayerNorm(kva[b,i,:r]) | rope(kva[b,i,r:], lens[b] + i)]
-// goes to pool row offsets[b] + lens[b] + i in the cache dtype (bf16 by
-// round-to-nearest-even), and, when `rows` is not NULL, to rows[b,i] in f32.
-// The lengths advance afterwards (k_cache_advance).  LayerNorm as
-// candle_nn::LayerNorm (src/model.rs:136): mean, biased variance of the
-// centred values, divide by sqrt(var + eps), weight, bias.
-template <typename DstT>
-__global__ __launch_bounds__(256) void k_latent_rows(const float *__restrict__ kva, int s, int r,
-                                                     int dr, const float *__restrict__ ln_w,
-                                                     const float *__restrict__ ln_b, float eps,
-                                                     const float *__restrict__ inv_freq,
-                                                     float mscale, float *__restrict__ rows,
-                                                     DstT *__restrict__ pool,
-                                                     const int64_t *__restrict__ offsets,
-                                                     const int32_t *__restrict__ lens) {
-  __shared__ float red[8];
-  const int tok = blockIdx.x, b = tok / s, i = tok % s;
-  const float *x = kva + (int64_t)tok * (r + dr);
-  float *y = rows ? rows + (int64_t)tok * (r + dr) : nullptr;
-  const int32_t len = lens[b];
-  DstT *dst = pool + (offsets[b] + len + i) * (int64_t)(r + dr);
-  auto put = [&](int c, float v) {
-    if (y) y[c] = v;
-    if constexpr (sizeof(DstT) == 2)
-      dst[c] = f32_to_bf16_bits(v);
-    else
-      dst[c] = v;
-  };
-  float sum = 0.f;
-  for (int c = threadIdx.x; c < r; c += blockDim.x) sum += x[c];
-  const float mean = block_sum(sum, red) / (float)r;
-  float sq = 0.f;
-  for (int c = threadIdx.x; c < r; c += blockDim.x) {
-    const float d = x[c] - mean;
-    sq += d * d;
-  }
-  const float var = block_sum(sq, red) / (float)r;
-  const float den = sqrtf(var + eps);
-  for (int c = threadIdx.x; c < r; c += blockDim.x) {
-    const float t = (x[c] - mean) / den * ln_w[c];
-    put(c, ln_b ? t + ln_b[c] : t);
-  }
-  const float pos = (float)(len + i);
-  for (int p = threadIdx.x; p < dr / 2; p += blockDim.x) {
-    const float ang = pos * inv_freq[p];
-    const float cs = cosf(ang) * mscale, sn = sinf(ang) * mscale;
-    const float e = x[r + 2 * p], o = x[r + 2 * p + 1];
-    put(r + 2 * p, e * cs - o * sn);
-    put(r + 2 * p + 1, o * cs + e * sn);
-  }
+// src/model.rs:99-104 fused in): one block per token (latent_rows.hpp).
+__global__ __launch_bounds__(256) void k_latent_rows(LatentRowsArgs a) {
+  extern __shared__ float lds[];  // latent_row_lds_bytes(r, dr)
+  latent_row(a, blockIdx.x, lds);
+}
+
+LatentRowsArgs latent_rows_args(const qmla_layer *L, const float *kva, int seq, float *rows,
+                                qmla_kv_cache *cache) {
+  const auto &g = L->cfg;
+  LatentRowsArgs a{};
+  a.kva = kva;
+  a.s = seq;
+  a.r = g.kv_lora_rank;
+  a.dr = g.qk_rope;
+  a.ln_w = L->ln_w;
+  a.ln_b = L->ln_b;
+  a.eps = (float)g.ln_eps;
+  a.inv_freq = L->inv_freq;
+  a.mscale = (float)g.rope_mscale;
+  a.pool = cache->rows;
+  a.bf16 = cache->dtype == QMLA_BF16;
+  a.offsets = cache->d_offsets;
+  a.lens = cache->d_lens;
+  a.rows = rows;
+  return a;
 }
 
 // LayerNorm + RoPE of the n new tokens into the cache (sequence b's tokens
@@ -212,16 +196,9 @@ __global__ __launch_bounds__(256) void k_latent_rows(const float *__restrict__ k
 // the room already).
 qmla_status latent_to_cache(const qmla_layer *L, const float *kva, int batch, int seq,
                             float *rows, qmla_kv_cache *cache, hipStream_t s) {
-  const auto &g = L->cfg;
-  const int n = batch * seq;
-  if (cache->dtype == QMLA_BF16)
-    k_latent_rows<uint16_t><<<dim3(n), dim3(256), 0, s>>>(
-        kva, seq, g.kv_lora_rank, g.qk_rope, L->ln_w, L->ln_b, (float)g.ln_eps, L->inv_freq,
-        (float)g.rope_mscale, rows, (uint16_t *)cache->rows, cache->d_offsets, cache->d_lens);
-  else
-    k_latent_rows<float><<<dim3(n), dim3(256), 0, s>>>(
-        kva, seq, g.kv_lora_rank, g.qk_rope, L->ln_w, L->ln_b, (float)g.ln_eps, L->inv_freq,
-        (float)g.rope_mscale, rows, (float *)cache->rows, cache->d_offsets, cache->d_lens);
+  k_latent_rows<<<dim3(batch * seq), dim3(256),
+                  latent_row_lds_bytes(L->cfg.kv_lora_rank, L->cfg.qk_rope), s>>>(
+      latent_rows_args(L, kva, seq, rows, cache));
   QMLA_LAUNCH_CHECK("k_latent_rows");
   return cache_advance(cache, 0, batch, seq, s);
 }
@@ -323,6 +300,88 @@ __global__ __launch_bounds__(256) void k_broadcast_rope(const SrcT *__restrict__
   }
 }
 
+// Builds and uploads the fragment-major split projection weights of the
+// decode step (once, at layer creation).
+qmla_status make_skinny_weights(qmla_layer *L, const float *wq, const float *bq,
+                                const float *wkva, const float *bkva, const float *wkvb,
+                                const float *bkvb, const float *wo) {
+  const auto &g = L->cfg;
+  const int H = g.heads, dn = g.qk_nope, dr = g.qk_rope, dv = g.v_dim, r = g.kv_lora_rank;
+  const int hid = g.hidden, nq = H * (dn + dr), nk = r + dr;
+  auto upload = [&](const void *src, size_t bytes, void **dst) -> qmla_status {
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) return fail(QMLA_ERR_OOM, "weight allocation failed");
+    L->allocs.push_back(p);
+    *dst = p;
+    if (hipMemcpy(p, src, bytes, hipMemcpyHostToDevice) != hipSuccess)
+      return fail(QMLA_ERR_HIP, "weight upload failed");
+    return QMLA_OK;
+  };
+  auto put = [&](const float *W, int64_t ldw, int64_t sw, int N, int K, int Z,
+                 void **dst) -> qmla_status {
+    std::vector<uint8_t> frag(skinny_frag_bytes(N, K, Z));
+    skinny_pack(W, ldw, sw, N, K, Z, frag.data());
+    return upload(frag.data(), frag.size(), dst);
+  };
+  std::vector<float> w((size_t)(nq + nk) * hid);
+  std::memcpy(w.data(), wq, sizeof(float) * nq * hid);
+  std::memcpy(w.data() + (size_t)nq * hid, wkva, sizeof(float) * nk * hid);
+  QMLA_TRY(put(w.data(), hid, 0, nq + nk, hid, 1, &L->w1f));
+  std::vector<float> b(nq + nk, 0.f);
+  if (bq) std::memcpy(b.data(), bq, sizeof(float) * nq);
+  if (bkva) std::memcpy(b.data() + nq, bkva, sizeof(float) * nk);
+  QMLA_TRY(upload(b.data(), b.size() * 4, (void **)&L->b1));
+  // W_UK^h transposed: wuk[h][i][d] = wkvb[h (dn + dv) + d][i]
+  w.assign((size_t)H * r * dn, 0.f);
+  for (int h = 0; h < H; ++h)
+    for (int d = 0; d < dn; ++d)
+      for (int i = 0; i < r; ++i)
+        w[((size_t)h * r + i) * dn + d] = wkvb[((size_t)h * (dn + dv) + d) * r + i];
+  QMLA_TRY(put(w.data(), dn, (int64_t)r * dn, r, dn, H, &L->wukf));
+  // W_UV^h = kv_b rows h (dn + dv) + dn .. + dv, and its bias b_V^h
+  QMLA_TRY(put(wkvb + (size_t)dn * r, r, (int64_t)(dn + dv) * r, dv, r, H, &L->wuvf));
+  b.assign((size_t)H * dv, 0.f);
+  if (bkvb)
+    for (int h = 0; h < H; ++h)
+      for (int i = 0; i < dv; ++i) b[(size_t)h * dv + i] = bkvb[(size_t)h * (dn + dv) + dn + i];
+  QMLA_TRY(upload(b.data(), b.size() * 4, (void **)&L->buv));
+  QMLA_TRY(put(wo, (int64_t)H * dv, 0, hid, H * dv, 1, &L->wof));
+  L->skinny = true;
+  return QMLA_OK;
+}
+
+// The decode step runs its projections on the skinny kernel when every
+// product has a K the kernel takes and the token count is small.
+bool use_skinny(const qmla_layer *L, int n) {
+  const auto &g = L->cfg;
+  return L->skinny && n <= kSkinnyRows && skinny_supported(32, g.hidden) &&
+         skinny_supported(32, g.qk_nope) && skinny_supported(32, g.kv_lora_rank) &&
+         skinny_supported(32, g.heads * g.v_dim);
+}
+
+// Arguments of a skinny product y = x W^T (+ bias) with the FINAL store:
+// x [Z][M][K] (row stride ldx, z-stride sx), y [Z][M][N] (ldy, sy).
+SkinnyGemmArgs skinny_args(const void *w_frag, const float *x, int64_t ldx, int64_t sx,
+                           const float *bias, int64_t sb, float *y, int64_t ldy, int64_t sy,
+                           int M, int N, int K, int Z) {
+  SkinnyGemmArgs a{};
+  a.w_frag = w_frag;
+  a.x = x;
+  a.ldx = ldx;
+  a.sx = sx;
+  a.bias = bias;
+  a.sb = sb;
+  a.y = y;
+  a.ldy = ldy;
+  a.sy = sy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.Z = Z;
+  a.mode = kSkinnyFinal;
+  return a;
+}
+
 inline size_t al(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct LayerWs {
@@ -348,7 +407,9 @@ LayerWs layer_ws(const qmla_layer *L, const qmla_kv_cache *c, int32_t batch, int
   w.qr = take(sizeof(float) * n * H * g.qk_rope + 4);
   w.qlat = take(sizeof(float) * n * H * g.kv_lora_rank);
   w.olat = take(sizeof(float) * n * H * g.kv_lora_rank);
-  w.o = take(sizeof(float) * n * H * g.v_dim);
+  // o: [n][H dv] f32, or o_proj's packed B operand of 32 token rows (the
+  // same 4 bytes per element, 32 rows at least)
+  w.o = take(sizeof(float) * std::max<size_t>(n, 32) * H * g.v_dim);
   w.dec = take(dec_bytes);
   w.kvb = take(sizeof(float) * n * H * (g.qk_nope + g.v_dim));
   w.k = take(sizeof(float) * n * H * g.qk_nope);
@@ -504,6 +565,9 @@ qmla_status qmla_layer_create(const qmla_layer_config *cfg, const float *wq, con
     if (p) L->allocs.push_back(p);
     L->inv_freq = static_cast<float *>(p);
   }
+  if (st == QMLA_OK && g.hidden % 16 == 0 && g.qk_nope % 16 == 0 && g.kv_lora_rank % 16 == 0 &&
+      (g.heads * g.v_dim) % 16 == 0)
+    st = make_skinny_weights(L, wq, bq, wkva, bkva, wkvb, bkvb, wo);
   if (st != QMLA_OK) {
     for (void *p : L->allocs) (void)hipFree(p);
     (void)rocblas_destroy_handle(L->blas);
@@ -557,6 +621,62 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
   float *part = (float *)(ws + w.part);
   hipStream_t s = as_stream(stream);
   const int n = batch * seq;
+
+  if (use_skinny(L, n)) {
+    // The projections on the skinny MFMA kernel, 32 token rows per launch;
+    // six dependent launches for one new token per sequence:
+    //   q_proj | kv_a (q split and roped in the epilogue) -> W_UK absorption
+    //   with the new latent cache rows in extra blocks -> decode core ->
+    //   merge (+ length advance) -> W_UV -> o_proj
+    for (int m0 = 0; m0 < n; m0 += 32) {
+      SkinnyGemmArgs a = skinny_args(L->w1f, xs + (size_t)m0 * g.hidden, g.hidden, 0, L->b1, 0,
+                                     nullptr, 0, 0, std::min(32, n - m0), H * (dn + dr) + r + dr,
+                                     g.hidden, 1);
+      a.mode = kSkinnyQkv;
+      a.m0 = m0;
+      a.seq = seq;
+      a.heads = H;
+      a.dn = dn;
+      a.dr = dr;
+      a.q_nope = qn;
+      a.q_rope = qr;
+      a.kva = kva;
+      a.kva_ld = r + dr;
+      a.lens = cache->d_lens;
+      a.inv_freq = L->inv_freq;
+      a.mscale = (float)g.rope_mscale;
+      QMLA_TRY(launch_skinny_gemm(a, s));
+    }
+    // q_lat[t, h, :] = W_UK^h^T q_nope[t, h, :]   (z = head), and the latent
+    // rows [LayerNorm(c) | rope(k_pe)] of the n new tokens into the cache
+    const LatentRowsArgs rows = latent_rows_args(L, kva, seq, nullptr, cache);
+    for (int m0 = 0; m0 < n; m0 += 32)
+      QMLA_TRY(launch_skinny_gemm(
+          skinny_args(L->wukf, qn + (size_t)m0 * H * dn, (int64_t)H * dn, dn, nullptr, 0,
+                      qlat + (size_t)m0 * H * r, (int64_t)H * r, r, std::min(32, n - m0), r, dn,
+                      H),
+          s, m0 == 0 ? &rows : nullptr, n));
+    // the new rows sit past the device lengths: the decode attends
+    // lens + seq tokens and its merge advances the lengths
+    for (int32_t i = 0; i < batch; ++i) cache->h_lens[i] += seq;
+    qmla_decode_dims dd{batch, seq * H, r, dr};
+    QMLA_TRY(decode_launch(&dd, cache, QMLA_F32, qlat, qr, g.softmax_scale, olat, nullptr, 0,
+                           ws + w.dec, dec_bytes, seq, true, s));
+    // o[t, h, :] = W_UV^h o_lat[t, h, :] + b_V^h, written as o_proj's
+    // packed B operand (32 token rows x H dv: 4 (H dv) bytes), then o_proj
+    for (int m0 = 0; m0 < n; m0 += 32) {
+      const int M = std::min(32, n - m0);
+      SkinnyGemmArgs uv = skinny_args(L->wuvf, olat + (size_t)m0 * H * r, (int64_t)H * r, r,
+                                      L->buv, dv, o, 0, dv, M, dv, r, H);
+      uv.mode = kSkinnyPackB;
+      QMLA_TRY(launch_skinny_gemm(uv, s));
+      SkinnyGemmArgs op = skinny_args(L->wof, o, 0, 0, L->bo, 0, out + (size_t)m0 * g.hidden,
+                                      g.hidden, 0, M, g.hidden, H * dv, 1);
+      op.x_packed = true;
+      QMLA_TRY(launch_skinny_gemm(op, s));
+    }
+    return QMLA_OK;
+  }
 
   QMLA_TRY(linear(L, xs, n, g.hidden, L->wq, L->bq, H * (dn + dr), q, s, part, w.part_elems));
   QMLA_TRY(linear(L, xs, n, g.hidden, L->wkva, L->bkva, r + dr, kva, s, part, w.part_elems));

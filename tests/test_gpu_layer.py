@@ -255,3 +255,29 @@ def test_materialised_cache_equals_the_reference_kvcache(qmla_gpu, dt):
     with pytest.raises(q.QmlaError) as e:
         layer.materialise(cache, 0, 2)
     assert e.value.status == 2
+
+
+@pytest.mark.parametrize("batch,seq,dt", [(40, 1, "f32"), (1, 1, "f32"), (3, 12, "bf16")],
+                         ids=["40x1-f32-two-chunks", "1x1-f32", "3x12-bf16"])
+def test_decode_step_projections_at_v2lite_width(qmla_gpu, batch, seq, dt):
+    """forward_with_cache at V2-Lite widths (hidden 2048, 16 heads, dn 128,
+    dr 64, dv 128, r 512).  With at most 64 new tokens the projections run
+    on the skinny bf16 hi/lo MFMA kernel, 32 token rows per launch (40 rows:
+    two launches); the result equals the oracle's absorbed-latent step (f32
+    throughout) within 1e-4 for an f32 cache, 2e-2 for a bf16 cache."""
+    q = qmla_gpu
+    hidden, H, dn, dr, dv, r = 2048, 16, 128, 64, 128, 512
+    w = O.MlaWeights.random(hidden, H, dn, dr, dv, r, seed=1500)
+    layer = q.MlaLayer(w)
+    dtype = q.F32 if dt == "f32" else q.BF16
+    lens = [97 + 13 * (i % 5) for i in range(batch)]
+    cache, per_seq = _ragged_cache(q, lens, r, dr, dtype, 1501, spare=seq)
+    xs = O.normal((batch, seq, hidden), 1502)
+    out = layer.forward_with_cache(xs, cache)
+    tol = 1e-4 if dtype == q.F32 else 2e-2
+    worst = 0.0
+    for b, n in enumerate(lens):
+        ref, _ = O.mla_forward_with_latent(w, xs[b:b + 1], per_seq[b].reshape(1, n, r + dr))
+        worst = max(worst, rel_err(out[b], ref[0]))
+    print(f"batch {batch} seq {seq} {dt}: worst rel_err={worst:.2e}")
+    assert worst < tol
