@@ -238,11 +238,11 @@ QMLA_API qmla_status qmla_decode_workspace_bytes_splits(const qmla_decode_dims *
  * first use of that GPU until the process ends.  A call whose workspace
  * (qmla_decode_workspace_bytes) would exceed that size returns
  * QMLA_ERR_UNSUPPORTED before anything is launched; the 128-head,
- * batch-64 decode over 256 compute units needs 84 MiB.  The call allocates
+ * batch-64 decode over 256 compute units needs 40 MiB.  The call allocates
  * nothing.  Every call on one GPU shares that GPU's array: calls that
  * overlap on one GPU (other streams, other threads) race and must be
  * serialised by the caller. */
-#define QMLA_DECODE_NOALLOC_SCRATCH_BYTES ((size_t)96 << 20)
+#define QMLA_DECODE_NOALLOC_SCRATCH_BYTES ((size_t)48 << 20)
 QMLA_API qmla_status qmla_decode_absorbed_noalloc(const qmla_decode_dims *dims,
                                          const qmla_kv_cache *cache, qmla_dtype q_dtype,
                                          const void *q_latent, const void *q_rope, double scale,

@@ -281,7 +281,9 @@ DecodeWorkspace decode_workspace_layout(int32_t batch, int32_t rows, int32_t r, 
   const size_t prow = mfma ? (size_t)((rows + 31) / 32) * 32 : (size_t)rows;
   w.plan_bytes = align256(plan);
   w.part_o_off = w.plan_bytes;
-  w.part_lse_off = w.part_o_off + align256(sizeof(float) * (size_t)w.slots * prow * r);
+  // partial outputs: f32, or bf16 on the MFMA path (its log-sum-exp stays f32)
+  const size_t pelt = mfma ? sizeof(uint16_t) : sizeof(float);
+  w.part_lse_off = w.part_o_off + align256(pelt * (size_t)w.slots * prow * r);
   w.total = w.part_lse_off + align256(sizeof(float) * (size_t)w.slots * prow);
   return w;
 }

@@ -623,15 +623,16 @@ constexpr size_t decode_lds_bytes() {
 }
 
 // Partial results: slot-major, then 32-row block, then 32-column block; a
-// block is 4 KB in the MFMA accumulator order [jq][lane][4] (element j of
-// lane l: row l % 32, column 8 (j / 4) + 4 (l / 32) + j % 4), so each store
-// instruction writes 1 KB contiguously.  part_lse: [slot][rows padded to 32].
+// block is 1024 bf16 (2 KB, rounded to nearest even; the log-sum-exp stays
+// f32) in the MFMA accumulator order [jq][lane][4] (element j of lane l:
+// row l % 32, column 8 (j / 4) + 4 (l / 32) + j % 4), so each store
+// instruction writes 512 B contiguously.  part_lse: [slot][rows padded to 32].
 template <int R, int DR, int NW, int NSTAGE, typename QT>
 __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
     const uint8_t *__restrict__ pool, const int64_t *__restrict__ offsets,
     const int32_t *__restrict__ lens, int32_t batch, const QT *__restrict__ q_lat,
     const QT *__restrict__ q_rope, int32_t rows, float scale_log2, int32_t seg_tokens,
-    int32_t pending, int2 *__restrict__ seq_info, float *__restrict__ part_o,
+    int32_t pending, int2 *__restrict__ seq_info, uint16_t *__restrict__ part_o,
     float *__restrict__ part_lse) {
   using SH = DecodeShape<R, DR>;
   using PS = PvSplit<R, NW>;
@@ -851,16 +852,16 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
     for (int r = 0; r < PS::NRB; ++r) {
       const int rb = blockIdx.y * NW + rg + r * PS::RW;  // 32-row block of the padded rows
       if (rb >= row_blocks) continue;
-      float *blk = part_o + (((int64_t)slot * row_blocks + rb) * (R / 32)) * 1024 + fl * 4;
+      uint16_t *blk = part_o + (((int64_t)slot * row_blocks + rb) * (R / 32)) * 1024 + fl * 4;
 #pragma unroll
       for (int i = 0; i < PS::NCB; ++i) {
         const int cb = cw + i * PS::CW;
 #pragma unroll
         for (int jq = 0; jq < 4; ++jq) {
-          floatx4_t v;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = o[i][r][jq * 4 + e] * inv[r];
-          *reinterpret_cast<floatx4_t *>(blk + cb * 1024 + jq * 256) = v;
+          u32x2_t v;
+          v[0] = pack2_bf16(o[i][r][jq * 4] * inv[r], o[i][r][jq * 4 + 1] * inv[r]);
+          v[1] = pack2_bf16(o[i][r][jq * 4 + 2] * inv[r], o[i][r][jq * 4 + 3] * inv[r]);
+          *reinterpret_cast<u32x2_t *>(blk + cb * 1024 + jq * 256) = v;
         }
       }
     }
@@ -880,7 +881,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
 template <int R>
 __global__ __launch_bounds__(256) void k_decode_merge_frag(
     int32_t rows, int32_t row_blocks, const int2 *__restrict__ seq_info,
-    const float *__restrict__ part_o, const float *__restrict__ part_lse, float *__restrict__ out,
+    const uint16_t *__restrict__ part_o, const float *__restrict__ part_lse, float *__restrict__ out,
     float *__restrict__ out_lse, int32_t *__restrict__ adv_lens, int32_t adv, int32_t adv_n) {
   constexpr int CB = R / 32;
   // lengths that the decode read as lens + pending become lens + pending
@@ -909,13 +910,15 @@ __global__ __launch_bounds__(256) void k_decode_merge_frag(
   for (int k = 0; k < ns; ++k) {
     const float w = expf(part_lse[(int64_t)(sb + k) * rows_pad + row] - mx);
     wsum += w;
-    const float *blk =
+    const uint16_t *blk =
         part_o + (((int64_t)(sb + k) * row_blocks + rb) * CB + cb) * 1024 + lane * 4;
 #pragma unroll
     for (int jq = 0; jq < 4; ++jq) {
-      const floatx4_t v = *reinterpret_cast<const floatx4_t *>(blk + jq * 256);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) acc[jq * 4 + e] += w * v[e];
+      const u32x2_t v = *reinterpret_cast<const u32x2_t *>(blk + jq * 256);
+      acc[jq * 4 + 0] += w * __builtin_bit_cast(float, v[0] << 16);
+      acc[jq * 4 + 1] += w * __builtin_bit_cast(float, v[0] & 0xffff0000u);
+      acc[jq * 4 + 2] += w * __builtin_bit_cast(float, v[1] << 16);
+      acc[jq * 4 + 3] += w * __builtin_bit_cast(float, v[1] & 0xffff0000u);
     }
   }
   const float inv = ns > 0 ? 1.f / wsum : 0.f;
@@ -999,7 +1002,7 @@ __global__ __launch_bounds__(256) void k_decode_narrow(
     const uint8_t *__restrict__ pool, const int64_t *__restrict__ offsets,
     const int32_t *__restrict__ lens, int32_t batch, const QT *__restrict__ q_lat,
     const QT *__restrict__ q_rope, int32_t rows, float scale_log2, int32_t seg_tokens,
-    int32_t pending, int2 *__restrict__ seq_info, float *__restrict__ part_o,
+    int32_t pending, int2 *__restrict__ seq_info, uint16_t *__restrict__ part_o,
     float *__restrict__ part_lse) {
   using SH = DecodeShape<R, DR>;
   constexpr int NW = 4, NSTAGE = kNarrowStages;
@@ -1269,16 +1272,16 @@ __global__ __launch_bounds__(256) void k_decode_narrow(
     if (wave == 0 && fh == 0)
       part_lse[(int64_t)slot * 32 + fn] = (m_ref + log2f(l_row)) * 0.69314718055994531f;
     const float inv = 1.f / l_row;
-    float *blk = part_o + ((int64_t)slot * SH::CB) * 1024 + fl * 4;
+    uint16_t *blk = part_o + ((int64_t)slot * SH::CB) * 1024 + fl * 4;
 #pragma unroll
     for (int i = 0; i < NCB; ++i) {
       const int cb = wave * NCB + i;
 #pragma unroll
       for (int jq = 0; jq < 4; ++jq) {
-        floatx4_t v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = o[i][jq * 4 + e] * inv;
-        *reinterpret_cast<floatx4_t *>(blk + cb * 1024 + jq * 256) = v;
+        u32x2_t v;
+        v[0] = pack2_bf16(o[i][jq * 4] * inv, o[i][jq * 4 + 1] * inv);
+        v[1] = pack2_bf16(o[i][jq * 4 + 2] * inv, o[i][jq * 4 + 3] * inv);
+        *reinterpret_cast<u32x2_t *>(blk + cb * 1024 + jq * 256) = v;
       }
     }
     // xrow and the stages are rewritten by the next segment only after its
@@ -1297,7 +1300,7 @@ qmla_status launch_merge(const DecodeArgs &a, hipStream_t stream) {
   const int row_blocks = (a.rows + 31) / 32;
   dim3 mgrid((unsigned)(a.batch * row_blocks), (R / 32 + 3) / 4);
   k_decode_merge_frag<R><<<mgrid, dim3(256), 0, stream>>>(
-      a.rows, row_blocks, a.seq_info, a.part_o, a.part_lse, a.out, a.out_lse,
+      a.rows, row_blocks, a.seq_info, (const uint16_t *)a.part_o, a.part_lse, a.out, a.out_lse,
       a.advance ? a.cache->d_lens : nullptr, a.pending, a.batch);
   QMLA_LAUNCH_CHECK("k_decode_merge_frag");
   return QMLA_OK;
@@ -1317,13 +1320,13 @@ qmla_status launch_shape(const DecodeArgs &a, hipStream_t stream) {
     QMLA_TRY(ensure_dynamic_lds((const void *)k, lds));
     k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, a.cache->d_lens, a.batch,
                                     (const uint16_t *)a.q_lat, (const uint16_t *)a.q_rope, a.rows,
-                                    sl2, seg_tokens, a.pending, a.seq_info, a.part_o, a.part_lse);
+                                    sl2, seg_tokens, a.pending, a.seq_info, (uint16_t *)a.part_o, a.part_lse);
   } else {
     auto k = k_decode_mfma<R, DR, NW, NSTAGE, float>;
     QMLA_TRY(ensure_dynamic_lds((const void *)k, lds));
     k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, a.cache->d_lens, a.batch,
                                     (const float *)a.q_lat, (const float *)a.q_rope, a.rows, sl2,
-                                    seg_tokens, a.pending, a.seq_info, a.part_o, a.part_lse);
+                                    seg_tokens, a.pending, a.seq_info, (uint16_t *)a.part_o, a.part_lse);
   }
   QMLA_LAUNCH_CHECK("k_decode_mfma");
   return launch_merge<R>(a, stream);
@@ -1341,13 +1344,13 @@ qmla_status launch_narrow(const DecodeArgs &a, hipStream_t stream) {
     QMLA_TRY(ensure_dynamic_lds((const void *)k, lds));
     k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, a.cache->d_lens, a.batch,
                                     (const uint16_t *)a.q_lat, (const uint16_t *)a.q_rope, a.rows,
-                                    sl2, seg_tokens, a.pending, a.seq_info, a.part_o, a.part_lse);
+                                    sl2, seg_tokens, a.pending, a.seq_info, (uint16_t *)a.part_o, a.part_lse);
   } else {
     auto k = k_decode_narrow<R, DR, float>;
     QMLA_TRY(ensure_dynamic_lds((const void *)k, lds));
     k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, a.cache->d_lens, a.batch,
                                     (const float *)a.q_lat, (const float *)a.q_rope, a.rows, sl2,
-                                    seg_tokens, a.pending, a.seq_info, a.part_o, a.part_lse);
+                                    seg_tokens, a.pending, a.seq_info, (uint16_t *)a.part_o, a.part_lse);
   }
   QMLA_LAUNCH_CHECK("k_decode_narrow");
   return launch_merge<R>(a, stream);

@@ -33,7 +33,7 @@ pub const QMLA_BF16: qmla_dtype = 1;
 pub type qmla_stream = *mut c_void;
 
 /// Scratch of `qmla_decode_absorbed_noalloc` per GPU, in bytes.
-pub const QMLA_DECODE_NOALLOC_SCRATCH_BYTES: usize = 96 << 20;
+pub const QMLA_DECODE_NOALLOC_SCRATCH_BYTES: usize = 48 << 20;
 
 /// Opaque latent KV cache (replaces KVCache, src/model.rs:86-105).
 #[repr(C)]

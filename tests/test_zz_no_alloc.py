@@ -75,11 +75,11 @@ def test_noalloc_decode_equals_the_workspace_entry_point(qmla_gpu, dt):
 
 
 def test_noalloc_decode_rejects_a_workspace_beyond_its_scratch(qmla_gpu):
-    """400 sequences x 128 rows need more than the 96 MiB scratch: the call
+    """400 sequences x 128 rows need more than the 48 MiB scratch: the call
     fails before launching anything and leaves the output untouched."""
     q = qmla_gpu
     c = _cache(q, [1] * 400, q.BF16, 60)
-    assert q.decode_workspace_bytes(c, 400, 128) > (96 << 20)
+    assert q.decode_workspace_bytes(c, 400, 128) > (48 << 20)
     dd = q.DecodeDims(400, 128, 512, 64)
     ql = q.DeviceBuffer(400 * 128 * 512 * 4)
     qr = q.DeviceBuffer(400 * 128 * 64 * 4)
