@@ -52,8 +52,10 @@ struct PackedArgs {
   const float *x;           // [vectors][ld_x] f32
   int64_t ld_x;
   int32_t src_div;          // source vector of slot s = s / src_div
-  const int2 *ebin;         // per expert {first bin position, pairs} (grid y = expert);
-                            //   null: grid y = tiles of kTokTile over `count` slots
+  const int2 *ebin;         // per expert {first bin position, pairs} (grid y = expert x
+                            //   slices); null: grid y = tiles of kTokTile over `count` slots
+  int32_t slices;           // with bins: blocks sharing an expert's bin; block
+                            //   (e, s) takes its tiles s, s + slices, ...
   const int32_t *slots;     // bin position -> slot (null: identity)
   int32_t count;
   float *out;               // out[slot * ld_out + row]
@@ -69,15 +71,20 @@ struct TileInfo {
 };
 
 // The block's expert and its bin range [first, first + count): with bins,
-// grid y is the expert and the block walks all of its tiles; without, grid y
-// is one tile of the `count` slots.
+// grid y is (expert, slice) and the block walks every slices-th tile of the
+// expert's bin starting at its slice; without, grid y is one tile of the
+// `count` slots.
 __device__ __forceinline__ int block_expert(const PackedArgs &a) {
-  return a.ebin ? (int)blockIdx.y : 0;
+  return a.ebin ? (int)blockIdx.y / a.slices : 0;
+}
+
+__device__ __forceinline__ int block_slice(const PackedArgs &a) {
+  return a.ebin ? (int)blockIdx.y % a.slices : 0;
 }
 
 __device__ __forceinline__ void block_range(const PackedArgs &a, int &first, int &count) {
   if (a.ebin) {
-    const int2 eb = a.ebin[blockIdx.y];
+    const int2 eb = a.ebin[blockIdx.y / a.slices];
     first = eb.x;
     count = eb.y;
   } else {
@@ -131,7 +138,7 @@ __global__ __launch_bounds__(kMfmaThreads) void k_packed_mfma(PackedArgs a) {
   const bool wave_ok = m0 < a.M;
   const bool row_ok = m0 + n < a.M;
   const int bpr = a.K >> 2;
-  const int expert = block_expert(a);
+  const int expert = block_expert(a), slice = block_slice(a);
   const uint8_t *wp[NMAT];
 #pragma unroll
   for (int i = 0; i < NMAT; ++i)
@@ -147,24 +154,32 @@ __global__ __launch_bounds__(kMfmaThreads) void k_packed_mfma(PackedArgs a) {
   constexpr int NR = NG > 0 ? (NG < PD ? NG : PD) : D;
   u32x4_t ring[NR][NMAT];
   const int ng0 = min(kSlab, a.K) >> 7;
+  // Slice 0 requests its first weight groups before it reads its bin; the
+  // other slices of an expert (which have work only for bins of more than
+  // one tile) request theirs once they know they have a tile.
+  if (slice == 0) {
 #pragma unroll
-  for (int d = 0; d < NR; ++d)
+    for (int d = 0; d < NR; ++d)
 #pragma unroll
-    for (int i = 0; i < NMAT; ++i)
-      ring[d][i] = gload16(wp[i] + (NG > 0 ? d : min(d, ng0 - 1)) * 32);
+      for (int i = 0; i < NMAT; ++i)
+        ring[d][i] = gload16(wp[i] + (NG > 0 ? d : min(d, ng0 - 1)) * 32);
+  }
 
   int first, count;
   block_range(a, first, count);
-  if (count <= 0) {  // an expert no token chose: drain the requested groups
+  const int tt0 = slice * kTokTile;
+  if (count <= tt0) {  // no tile for this block: drain the requested groups
     wait_vm<0>();
     return;
   }
-  for (int tt = 0; tt < count; tt += kTokTile) {
+  // without bins the grid position is the block's only tile (count <= kTokTile)
+  const int tstep = a.ebin ? a.slices * kTokTile : kTokTile;
+  for (int tt = tt0; tt < count; tt += tstep) {
   const TileInfo ti{expert, first + tt, min(kTokTile, count - tt)};
-  if (tt > 0) {
-    // next tile of the same expert: the LDS of the last one is free once
-    // every wave is past its epilogue; its weights come again (from L2)
-    __syncthreads();
+  if (tt != tt0 || slice != 0) {
+    // a later tile of this block: the LDS of the last one is free once every
+    // wave is past its epilogue; its weights come again (from L2)
+    if (tt != tt0) __syncthreads();
 #pragma unroll
     for (int d = 0; d < NR; ++d)
 #pragma unroll
@@ -432,7 +447,8 @@ __global__ __launch_bounds__(256) void k_packed_generic(PackedArgs a) {
   if (row >= a.M) return;
   const int bpr = a.K >> 2;
   const TileInfo ti{block_expert(a), first, count};
-  for (int t = 0; t < ti.ntok; ++t) {
+  const int stride = a.ebin ? a.slices : 1;  // slices >= 1 whenever bins are given
+  for (int t = block_slice(a); t < ti.ntok; t += stride) {
     const int pos = ti.start + t;
     const int slot = a.slots ? a.slots[pos] : pos;
     const float *xv = a.x + (int64_t)(slot / a.src_div) * a.ld_x;
@@ -679,6 +695,7 @@ size_t mfma_lds_bytes(int32_t K, int nmat) {
 int mfma_row_blocks(int32_t M) { return (M + 32 * kMfmaWaves - 1) / (32 * kMfmaWaves); }
 
 constexpr int64_t kMaxTileGrid = 65535;  // grid y limit
+constexpr int64_t kMaxSlices = 64;       // blocks sharing one expert's bin
 
 template <int NMAT, int NG>
 qmla_status launch_mfma(const PackedArgs &a, int64_t tile_grid, hipStream_t s) {
@@ -881,7 +898,17 @@ qmla_status qmla_moe_forward(const qmla_moe_config *cfg, const float *xs, int32_
   gu.src_max = xmax;
   gu.src_max_parts = 1;
   gu.out_max = fast_gu && fast_dn ? hmax : nullptr;
-  QMLA_TRY(launch_packed<2>(gu, c.num_experts, fast_gu, s));
+  // Split each expert's bin over `slices` blocks when the pairs outnumber
+  // the experts' first tiles (prefill-sized calls, skewed routing); a
+  // decode-sized call keeps one block per expert and row block.
+  {
+    const int64_t tiles = ((int64_t)P + kTokTile - 1) / kTokTile;
+    int64_t sl = (tiles + c.num_experts - 1) / c.num_experts;
+    sl = std::max<int64_t>(1, std::min<int64_t>({sl, kMaxSlices, kMaxTileGrid / c.num_experts}));
+    gu.slices = (int32_t)sl;
+  }
+  QMLA_REQUIRE(gu.slices >= 1, QMLA_ERR_SHAPE, "bin slices");
+  QMLA_TRY(launch_packed<2>(gu, (int64_t)c.num_experts * gu.slices, fast_gu, s));
 
   PackedArgs dn = gu;
   dn.w[0] = dn.w[1] = down_packed;
@@ -898,7 +925,7 @@ qmla_status qmla_moe_forward(const qmla_moe_config *cfg, const float *xs, int32_
   dn.src_max = fast_gu && fast_dn ? hmax : nullptr;
   dn.src_max_parts = mfma_row_blocks(I);
   dn.out_max = nullptr;
-  QMLA_TRY(launch_packed<1>(dn, c.num_experts, fast_dn, s));
+  QMLA_TRY(launch_packed<1>(dn, (int64_t)c.num_experts * dn.slices, fast_dn, s));
 
   hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, s, ybuf,
                      sel, selw, T, c.top_k, H, out);

@@ -208,3 +208,29 @@ def test_moe_no_experts_and_bad_top_k(qmla_gpu):
     with pytest.raises(q.QmlaError) as e:
         moe_layer(q, W).workspace_bytes(4)
     assert e.value.status == 2
+
+
+@pytest.mark.parametrize("E,k,H,I,T", [
+    (64, 6, 256, 384, 1024),  # prefill-sized: ~10 tiles a bin, bins split over 10 blocks
+    (4, 2, 100, 256, 64),     # gate/up on the fallback, down on MFMA with its own pass 1, ~3 tiles a bin
+])
+def test_moe_forward_prefill_sized_bins(qmla_gpu, E, k, H, I, T):
+    """Many (token, expert) pairs per expert: each bin spans several tiles
+    of 10 pairs, which the blocks of the expert's slices share (tiles s,
+    s + slices, ...)."""
+    W = O.random_moe_weights(E, k, H, I, 5000 + E + T)
+    check_moe(qmla_gpu, W, O.normal((T, H), 5100 + T), f"E={E} k={k} H={H} I={I} T={T}")
+
+
+@pytest.mark.parametrize("H,I", [(256, 256), (100, 384)])
+def test_moe_forward_skewed_routing(qmla_gpu, H, I):
+    """Every token ranks expert 0 first: its bin holds all 200 tokens (20
+    tiles) while the other experts share the second choices, so the hot
+    bin is split over the expert's slices."""
+    E, k, T = 8, 2, 200
+    W = O.random_moe_weights(E, k, H, I, 6000 + H)
+    W.gate_weight[0] = 0.5  # with x ~ N(1, 1), expert 0's logit is ~0.5 H
+    xs = (O.normal((T, H), 6001) + 1.0).astype(np.float32)
+    out, idx, _ = moe_layer(qmla_gpu, W).forward(xs, return_routing=True)
+    assert (idx[:, 0] == 0).all()
+    check_moe(qmla_gpu, W, xs, f"skewed H={H} I={I}")
