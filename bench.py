@@ -115,7 +115,8 @@ class DecodeBench:
         self.caches = []
         for r in range(self.replicas):
             c = qmla.KVCache(self.lens, 512, 64, qmla.BF16)
-            fill_bf16(c.describe().rows, self.tokens * ROW_ELEMS, seed + 1000003 * r, tmp, stream)
+            d = c.describe()  # fill every page, padding included
+            fill_bf16(d.rows, d.total_rows * ROW_ELEMS, seed + 1000003 * r, tmp, stream)
             c.set_lengths(self.lens, stream)
             self.caches.append(c)
         nq = self.batch * heads
@@ -190,8 +191,12 @@ class LayerDecodeBench:
     per sequence: f32 projections, LayerNorm + RoPE of the new latent rows
     into a bf16 latent cache, the absorbed decode core, W_UV and o_proj.
     V2-Lite head shapes (hidden 2048, 16 heads, dn 128, dr 64, dv 128,
-    r 512), batch 32, 4096 cached tokens per sequence (the cache grows by one
-    token per step); weights N(0, 0.02^2), activations N(0, 1), seeded."""
+    r 512), batch 32, 4096 cached tokens per sequence; weights N(0, 0.02^2),
+    activations N(0, 1), seeded.  The cache grows by one token per step in
+    growth mode: each sequence holds exactly its 4096 rows (16 pages of 256)
+    and takes a page from the pool's free list (sized for 512 more tokens per
+    sequence at creation) when it crosses a page boundary, inside the timed
+    steps once steps + warmup > 256."""
 
     def __init__(self, stream, seed, batch=32, ctx=4096, hidden=2048, heads=16):
         rng = np.random.default_rng(seed)
@@ -209,9 +214,11 @@ class LayerDecodeBench:
         self.layer = qmla.MlaLayer(w)
         self.weight_bytes = 4 * (w.wq.size + w.wkva.size + w.wkvb.size + w.wo.size)
         self.batch, self.ctx, self.stream = batch, ctx, stream
-        self.cache = qmla.KVCache([ctx + 512] * batch, r, dr, qmla.BF16)
+        self.cache = qmla.KVCache([ctx] * batch, r, dr, qmla.BF16, grow=True,
+                                  pool_rows=batch * (ctx + 512))
         tmp = qmla.DeviceBuffer(64 << 20)
-        fill_bf16(self.cache.describe().rows, batch * (ctx + 512) * ROW_ELEMS, seed + 1, tmp, stream)
+        d = self.cache.describe()
+        fill_bf16(d.rows, d.total_rows * ROW_ELEMS, seed + 1, tmp, stream)
         stream.sync()
         tmp.free()
         self.cache.set_lengths([ctx] * batch, stream)
@@ -229,14 +236,18 @@ class LayerDecodeBench:
             self.ws_bytes, qmla._sh(self.stream)))
 
     def run(self, steps, warmup):
-        assert steps + warmup <= 512, "the cache has room for 512 new tokens per sequence"
+        assert steps + warmup <= 512, "the page pool has room for 512 new tokens per sequence"
+        pool0 = self.cache.pool_info()
         wall, ev = time_steps(self.step, steps, warmup, self.stream)
+        assert self.cache.pool_info()[0] == pool0[0], "the pool grew: a step allocated"
         t = ev * 1e-3
         mean_ctx = self.ctx + warmup + (steps + 1) / 2.0
         hbm = self.weight_bytes + self.batch * mean_ctx * ROW_BYTES
+        pages = (pool0[1] - self.cache.pool_info()[1]) // 256
         return {"tok_s": self.batch / t, "ms_per_step": ev, "wall_ms_per_step": wall,
                 "weight_bytes": self.weight_bytes, "bytes_per_step": hbm, "tb_s": hbm / t / 1e12,
-                "hbm_frac": hbm / t / 1e12 / (HBM_PEAK_GBS / 1e3), "step_ms": dict(STATS)}
+                "hbm_frac": hbm / t / 1e12 / (HBM_PEAK_GBS / 1e3), "pages_taken": int(pages),
+                "step_ms": dict(STATS)}
 
 
 def ref_bench_packed(out_f: int, in_f: int):
@@ -543,7 +554,8 @@ def main():
         lb = LayerDecodeBench(stream, seed=51)
         secondary["layer_decode_step"] = {
             "workload": "MlaAttention forward_with_cache, hidden 2048, 16 heads, r 512, batch 32, "
-                        "4096 cached + 1, f32 weights, bf16 latent cache",
+                        "4096 cached + 1, f32 weights, bf16 latent cache in growth mode (256-row pages "
+                        "taken from a pre-sized pool)",
             **lb.run(args.steps, args.warmup)}
         log("layer decode step", json.dumps(secondary["layer_decode_step"]))
         del lb

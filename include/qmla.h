@@ -14,7 +14,9 @@
  *    before anything is launched; nothing aborts the process.
  *  - Compute calls are asynchronous on the given stream and allocate no
  *    device memory; scratch comes from a caller-provided workspace whose
- *    size is returned by the matching *_workspace_bytes query.
+ *    size is returned by the matching *_workspace_bytes query.  The one
+ *    exception is cache growth past an exhausted page pool (see
+ *    qmla_cache_set_growth; qmla_cache_reserve_pool avoids it).
  *  - Tensors are row-major and contiguous, in the layouts documented at
  *    each call.  bf16 values are stored as uint16 bit patterns.
  *  - No global mutable state apart from the per-thread error string and a
@@ -129,9 +131,13 @@ QMLA_API qmla_status qmla_eager_prefill_attn(int32_t b, int32_t h, int32_t s, in
  * Replaces KVCache, src/model.rs:86-105 ({k, v, k_rope} decompressed
  * per-head tensors grown by Tensor::cat on every append) with one latent row
  * per token, [c_kv (kv_lora_rank) | k_pe (rope_dim)], stored once for all
- * heads.  Sequence i owns rows [offset_i, offset_i + capacity_i) of one
- * contiguous HBM pool; its current length lives in a device int32 table
- * (mirrored on the host for validation, so no call needs a device sync).  */
+ * heads.  Rows live in pages of page_rows rows (a power of two >= 32); a
+ * device block table lists each sequence's pages, so token t of sequence i
+ * is row t % page_rows of page pages[i * table_width + t / page_rows].
+ * Lengths live in a device int32 table, mirrored on the host together with
+ * the block table, so no call needs a device sync to validate or to grow.
+ * A sequence's capacity is the number of rows it may hold without growing
+ * (at most its pages x page_rows). */
 typedef struct qmla_kv_cache qmla_kv_cache;
 
 typedef struct {
@@ -140,19 +146,39 @@ typedef struct {
   int32_t rope_dim;
   qmla_dtype dtype;  /* element type of the rows                    */
   int64_t row_elems; /* kv_lora_rank + rope_dim                      */
+  /* Layout at creation: one chunk holding every sequence's pages in order,
+   * sequence i from row offsets[i].  Valid while `contiguous` is 1 (no page
+   * has been taken from the free list since); otherwise rows and offsets
+   * are NULL and total_rows is 0. */
   int64_t total_rows;
   void *rows;        /* device: [total_rows, row_elems]               */
   int64_t *offsets;  /* device: [num_seqs] first row of each sequence */
   int32_t *lengths;  /* device: [num_seqs] current lengths            */
   int32_t *capacity; /* device: [num_seqs]                            */
+  uint64_t *pages;   /* device: [num_seqs, table_width] page addresses */
+  int32_t page_rows;
+  int32_t table_width; /* pages one sequence can hold                 */
+  int32_t contiguous;
+  int32_t reserved;
 } qmla_cache_desc;
 
 /* KVCache::new, src/model.rs:95-97.  capacity[num_seqs] is a host array of
- * per-sequence token capacities; all lengths start at 0. */
+ * per-sequence token capacities; all lengths start at 0.  Same as
+ * qmla_cache_create_paged(num_seqs, capacity, 0, 0, 0, ...). */
 QMLA_API qmla_status qmla_cache_create(int32_t num_seqs, const int32_t *capacity, int32_t kv_lora_rank,
                               int32_t rope_dim, qmla_dtype dtype, qmla_kv_cache **out);
+/* KVCache::new with the pool laid out by the caller.  max_len: the longest
+ * a sequence may grow (0: 163840, DeepSeek-V2's max_position_embeddings, or
+ * the largest capacity if larger); it sizes the block table.  pool_rows:
+ * rows of HBM to allocate now (0: just the capacities); rows beyond the
+ * capacities start on the free list that growth draws from.  page_rows: 0
+ * for 256. */
+QMLA_API qmla_status qmla_cache_create_paged(int32_t num_seqs, const int32_t *capacity, int64_t max_len,
+                                    int64_t pool_rows, int32_t page_rows, int32_t kv_lora_rank,
+                                    int32_t rope_dim, qmla_dtype dtype, qmla_kv_cache **out);
 QMLA_API qmla_status qmla_cache_destroy(qmla_kv_cache *cache);
-/* #[derive(Clone)] on KVCache, src/model.rs:87: deep copy of rows and lengths. */
+/* #[derive(Clone)] on KVCache, src/model.rs:87: deep copy of rows and
+ * lengths (capacities kept; the clone's pages are packed into one chunk). */
 QMLA_API qmla_status qmla_cache_clone(const qmla_kv_cache *cache, qmla_kv_cache **out, qmla_stream stream);
 /* KVCache::append, src/model.rs:99-104: appends n_new tokens to each of
  * sequences 0..n_seqs-1.  rows [n_seqs, n_new, kv_lora_rank + rope_dim] on
@@ -164,31 +190,53 @@ QMLA_API qmla_status qmla_cache_append(qmla_kv_cache *cache, const void *rows, q
 /* Ragged form: appends n_new rows to sequence `seq` only. */
 QMLA_API qmla_status qmla_cache_append_seq(qmla_kv_cache *cache, int32_t seq, const void *rows,
                                   qmla_dtype rows_dtype, int32_t n_new, qmla_stream stream);
-/* Sets every sequence's length (host array [num_seqs]) without writing
- * rows: rows past the old length keep whatever the pool holds.  Used to
- * truncate, or after filling the pool directly through qmla_cache_describe. */
+/* Sets every sequence's length (host array [num_seqs], each <= its
+ * capacity) without writing rows: rows past the old length keep whatever
+ * the pages hold.  Used to truncate, or after filling the pool directly
+ * through qmla_cache_describe.  Stream-ordered; `lengths` may be reused as
+ * soon as the call returns and the host does not wait for the device. */
 QMLA_API qmla_status qmla_cache_set_lengths(qmla_kv_cache *cache, const int32_t *lengths,
                                    qmla_stream stream);
 /* Length read (`cache.k.dim(2)`, src/model.rs:259) from the host mirror. */
 QMLA_API qmla_status qmla_cache_lengths(const qmla_kv_cache *cache, int32_t *lengths_out);
 QMLA_API qmla_status qmla_cache_describe(const qmla_kv_cache *cache, qmla_cache_desc *out);
+/* Rows [t0, t0 + n) of sequence `seq` (t0 + n <= its capacity) copied into
+ * `out` (device, [n, row_elems] in the cache dtype): the reference's
+ * `cache.k` read of one sequence, in latent form, whatever pages hold it. */
+QMLA_API qmla_status qmla_cache_gather(const qmla_kv_cache *cache, int32_t seq, int32_t t0, int32_t n,
+                              void *out, qmla_stream stream);
 /* Capacity growth.  KVCache::append (src/model.rs:99-104) grows its tensors
- * without bound; here growth is explicit, so that a caller that sized the
- * cache up front keeps its pool (and pointers) fixed.
+ * without bound by copying them; here a sequence grows by taking pages from
+ * the cache's free list and writing their addresses into its block table
+ * (one small kernel on `stream`).  No row moves, no pointer from
+ * qmla_cache_describe changes meaning except rows/offsets (see above), and
+ * the host does not wait.  Device memory is allocated only when the free
+ * list is short: then a chunk of max(missing pages, half the pool) pages is
+ * added with hipMalloc.  qmla_cache_reserve_pool tops the free list up ahead
+ * of time, so that appends and layer calls allocate nothing.
  * qmla_cache_reserve raises sequence i's capacity to at least
  * min_capacity[i] (host array [num_seqs]; smaller entries change nothing).
- * The pool is re-laid out: live rows move to new offsets, so pointers from
- * qmla_cache_describe are stale afterwards.  It synchronises `stream`; no
- * work on another stream may use the cache meanwhile.  On failure the
- * cache is unchanged.
  * qmla_cache_set_growth(cache, 1): appends and the layer calls that would
- * pass a sequence's capacity first grow it to max(needed, 2 x capacity, 16)
- * instead of failing with QMLA_ERR_CAPACITY.  Off by default; clones
- * inherit it.  qmla_cache_capacity reads the host mirror of the capacities. */
+ * pass a sequence's capacity first take the pages they need (the capacity
+ * becomes every row of the sequence's pages) instead of failing with
+ * QMLA_ERR_CAPACITY; past max_len they still fail.  Off by default; clones
+ * inherit it.  qmla_cache_capacity reads the host mirror of the capacities.
+ * qmla_cache_trim returns each listed sequence's pages beyond its current
+ * length to the free list (capacities shrink to match); pages freed here
+ * may be handed out by the next growth, so work on other streams that still
+ * reads those rows must be ordered before it.  qmla_cache_pool_info reports
+ * the pool's rows and the free list's rows (either pointer may be NULL).
+ * On failure (QMLA_ERR_CAPACITY past max_len, QMLA_ERR_OOM) the cache is
+ * unchanged. */
 QMLA_API qmla_status qmla_cache_reserve(qmla_kv_cache *cache, const int32_t *min_capacity,
                                qmla_stream stream);
+QMLA_API qmla_status qmla_cache_reserve_pool(qmla_kv_cache *cache, int64_t free_rows);
 QMLA_API qmla_status qmla_cache_set_growth(qmla_kv_cache *cache, int32_t enable);
 QMLA_API qmla_status qmla_cache_capacity(const qmla_kv_cache *cache, int32_t *capacity_out);
+QMLA_API qmla_status qmla_cache_trim(qmla_kv_cache *cache, int32_t seq0, int32_t n_seqs,
+                            qmla_stream stream);
+QMLA_API qmla_status qmla_cache_pool_info(const qmla_kv_cache *cache, int64_t *pool_rows,
+                                 int64_t *free_rows);
 
 /* ------------------------------------------- absorbed latent decode ------
  * The attention core of MlaAttention::forward_with_cache,

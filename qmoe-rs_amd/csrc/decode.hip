@@ -153,8 +153,7 @@ __device__ inline float load_q(const QT *p, int64_t i) {
 
 template <typename QT>
 __global__ __launch_bounds__(kF32Threads) void k_decode_f32(
-    const float *__restrict__ pool, const int64_t *__restrict__ offsets,
-    const QT *__restrict__ q_lat, const QT *__restrict__ q_rope, int32_t rows, int32_t r,
+    PageTable tab, const QT *__restrict__ q_lat, const QT *__restrict__ q_rope, int32_t rows, int32_t r,
     int32_t dr, float scale, DecodePlanView plan, float *__restrict__ out,
     float *__restrict__ out_lse, float *__restrict__ part_o, float *__restrict__ part_lse) {
   extern __shared__ float qs[];  // [r + dr]
@@ -171,7 +170,10 @@ __global__ __launch_bounds__(kF32Threads) void k_decode_f32(
     for (int c = tid; c < r; c += kF32Threads) qs[c] = load_q(q_lat, qrow * r + c);
     for (int c = tid; c < dr; c += kF32Threads) qs[r + c] = load_q(q_rope, qrow * dr + c);
     __syncthreads();
-    const float *base = pool + (offsets[sg.seq] + sg.t0) * (int64_t)w;
+    // token t of the segment: row sg.t0 + t of the sequence, via its pages
+    auto row_at = [&](int32_t t) {
+      return reinterpret_cast<const float *>(tab.row(sg.seq, (int64_t)sg.t0 + t, (int64_t)w * 4));
+    };
     const int32_t T = sg.t1 - sg.t0;
     float m_run = -INFINITY, l_run = 0.f;
     float acc[kColsPerThread];
@@ -181,7 +183,7 @@ __global__ __launch_bounds__(kF32Threads) void k_decode_f32(
       const int tt = tid >> 2, part = tid & 3;
       float d = 0.f;
       if (t0 + tt < T) {
-        const float *row = base + (int64_t)(t0 + tt) * w;
+        const float *row = row_at(t0 + tt);
         for (int c = part; c < w; c += 4) d += qs[c] * row[c];
       }
       d += __shfl_xor(d, 1);
@@ -199,7 +201,7 @@ __global__ __launch_bounds__(kF32Threads) void k_decode_f32(
       for (int j = 0; j < nt; ++j) {
         const float p = expf(sc[j] - m_new);
         l_run += p;
-        const float *row = base + (int64_t)(t0 + j) * w;
+        const float *row = row_at(t0 + j);
 #pragma unroll
         for (int k = 0; k < kColsPerThread; ++k) {
           const int c = tid + k * kF32Threads;
@@ -341,15 +343,15 @@ qmla_status launch_decode_f32(const DecodeArgs &a, hipStream_t stream) {
   QMLA_REQUIRE(a.rows <= 65535, QMLA_ERR_SHAPE, "rows %d > 65535", a.rows);
   dim3 grid(a.blocks, a.rows), block(kF32Threads);
   size_t lds = sizeof(float) * (a.r + a.dr);
-  const float *pool = static_cast<const float *>(a.cache->rows);
+  const PageTable tab = a.cache->table();
   if (a.q_dtype == QMLA_F32) {
     k_decode_f32<float><<<grid, block, lds, stream>>>(
-        pool, a.cache->d_offsets, (const float *)a.q_lat, (const float *)a.q_rope, a.rows, a.r,
-        a.dr, a.scale, a.plan, a.out, a.out_lse, a.part_o, a.part_lse);
+        tab, (const float *)a.q_lat, (const float *)a.q_rope, a.rows, a.r, a.dr, a.scale, a.plan,
+        a.out, a.out_lse, a.part_o, a.part_lse);
   } else {
     k_decode_f32<uint16_t><<<grid, block, lds, stream>>>(
-        pool, a.cache->d_offsets, (const uint16_t *)a.q_lat, (const uint16_t *)a.q_rope, a.rows,
-        a.r, a.dr, a.scale, a.plan, a.out, a.out_lse, a.part_o, a.part_lse);
+        tab, (const uint16_t *)a.q_lat, (const uint16_t *)a.q_rope, a.rows, a.r, a.dr, a.scale,
+        a.plan, a.out, a.out_lse, a.part_o, a.part_lse);
   }
   QMLA_LAUNCH_CHECK("k_decode_f32");
   return QMLA_OK;

@@ -427,6 +427,18 @@ __device__ __forceinline__ void issue_full_tile(const FullTileDma &d) {
   for (int k = 0; k < DmaSlots<SH, NW>::MI; ++k) issue_full_one<SH, NW>(d, k);
 }
 
+// First row of the tile of a sequence starting at token t, a multiple of
+// kTok: the plan cuts sequences at multiples of kTok and a page holds a
+// multiple of kTok rows, so the tile's rows are consecutive in one page.
+// `prow` is the sequence's block-table row; t is uniform, so this is one
+// scalar load.
+template <class SH>
+__device__ __forceinline__ const uint8_t *tile_rows(const uint64_t *__restrict__ prow, int shift,
+                                                    int t) {
+  const uint64_t page = prow[t >> shift];
+  return reinterpret_cast<const uint8_t *>(page) + (int64_t)(t & ((1 << shift) - 1)) * (SH::W * 2);
+}
+
 // DMA of the segment's last, partial tile: tokens past `last` (the last
 // valid token, relative to the tile) re-load that token's row, which the
 // softmax masks.  Sources are the uniform tile base plus 32-bit per-lane
@@ -462,10 +474,9 @@ __device__ __forceinline__ void issue_clamped_tile(const uint8_t *__restrict__ t
 }
 
 template <class SH, int NW>
-__device__ __forceinline__ void issue_any_tile(const uint8_t *__restrict__ seq_base, int tile_t0,
+__device__ __forceinline__ void issue_any_tile(const uint8_t *__restrict__ tile_base, int tile_t0,
                                                int seg_t1, lds_char *stage, int wave, int lane,
                                                uint32_t v_kv, uint32_t v_rope, const WaveDma &w) {
-  const uint8_t *tile_base = seq_base + (int64_t)tile_t0 * (SH::W * 2);
   if (tile_t0 + kTok <= seg_t1)
     issue_full_tile<SH, NW>(FullTileDma{tile_base, stage, wave, v_kv, v_rope, w});
   else
@@ -567,7 +578,12 @@ __device__ int32_t lds_exscan(int32_t *a, int32_t n, int32_t *tmp) {
 // sequences >= from, sets *next to the first sequence not listed (batch
 // when done).  scratch: 2 * (batch + 1) + NT int32 of idle LDS.  In the
 // virtual stream, sequence b occupies [P[b], P[b + 1]) with its real
-// tokens at [P[b] + seg_tokens, P[b + 1]).
+// tokens at [v0, v0 + L) = [P[b] + seg_tokens, P[b + 1]).  Sequences are
+// cut only at tile boundaries (multiples of kTok from the sequence start):
+// the tile starting at virtual position v belongs to the piece holding v,
+// so every segment starts at a multiple of kTok and each of its tiles lies
+// in one cache page.  A piece is at least kTok long, so the pieces holding
+// a sequence's tile starts are consecutive and each gets a non-empty segment.
 template <int NT>
 __device__ void plan_round(const int32_t *__restrict__ lens, int32_t pending, int32_t batch,
                            int32_t from, int32_t seg_tokens, int32_t *scratch, SegDesc *list,
@@ -579,17 +595,27 @@ __device__ void plan_round(const int32_t *__restrict__ lens, int32_t pending, in
   __syncthreads();
   const int32_t N = lds_exscan<NT>(P, batch, tmp);
   if (tid == 0) P[batch] = N;
-  const int32_t chunk = max(1, (N + blocks - 1) / blocks);
+  const int32_t chunk = max(kTok, (N + blocks - 1) / blocks);
   __syncthreads();
-  // pieces touching the real tokens [v0, v1) of sequence b
-  auto touched = [&](int32_t v0, int32_t v1) { return v1 > v0 ? (v1 - 1) / chunk - v0 / chunk + 1 : 0; };
-  for (int b = tid; b < batch; b += NT) SB[b] = touched(P[b] + seg_tokens, P[b + 1]);
+  // pieces holding the tile starts of a sequence with real tokens [v0, v0 + L)
+  auto touched = [&](int32_t v0, int32_t L) {
+    return L > 0 ? (v0 + (L - 1) / kTok * kTok) / chunk - v0 / chunk + 1 : 0;
+  };
+  // sequence-relative cut at virtual position x: the first tile start >= x
+  auto cut = [&](int32_t x, int32_t v0, int32_t L) {
+    return x <= v0 ? 0 : min(L, (x - v0 + kTok - 1) / kTok * kTok);
+  };
+  for (int b = tid; b < batch; b += NT) {
+    const int32_t v0 = P[b] + seg_tokens;
+    SB[b] = touched(v0, P[b + 1] - v0);
+  }
   __syncthreads();
   (void)lds_exscan<NT>(SB, batch, tmp);
   if (from == 0 && blockIdx.y == 0) {
     for (int b = tid; b < batch; b += NT) {
-      const int32_t v0 = P[b] + seg_tokens, v1 = P[b + 1];
-      if (min(v0 / chunk, blocks - 1) == piece) seq_info[b] = make_int2(SB[b], touched(v0, v1));
+      const int32_t v0 = P[b] + seg_tokens;
+      if (min(v0 / chunk, blocks - 1) == piece)
+        seq_info[b] = make_int2(SB[b], touched(v0, P[b + 1] - v0));
     }
   }
   if (tid == 0) {
@@ -602,10 +628,10 @@ __device__ void plan_round(const int32_t *__restrict__ lens, int32_t pending, in
     }
     int32_t cnt = 0, b = lo;
     for (; b < batch && P[b] + seg_tokens < end && cnt < kSegCap; ++b) {
-      const int32_t v0 = P[b] + seg_tokens, v1 = P[b + 1];
-      const int32_t a = max(start, v0), e = min(end, v1);
-      if (e <= a) continue;  // empty sequence, or real tokens outside the piece
-      list[cnt++] = SegDesc{b, a - v0, e - v0, SB[b] + (piece - v0 / chunk)};
+      const int32_t v0 = P[b] + seg_tokens, L = P[b + 1] - v0;
+      const int32_t t0 = cut(start, v0, L), t1 = cut(end, v0, L);
+      if (t1 <= t0) continue;  // empty sequence, or no tile start inside the piece
+      list[cnt++] = SegDesc{b, t0, t1, SB[b] + (piece - v0 / chunk)};
     }
     meta[0] = cnt;
     meta[1] = (b < batch && P[b] + seg_tokens < end) ? b : batch;
@@ -629,7 +655,7 @@ constexpr size_t decode_lds_bytes() {
 // instruction writes 512 B contiguously.  part_lse: [slot][rows padded to 32].
 template <int R, int DR, int NW, int NSTAGE, typename QT>
 __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
-    const uint8_t *__restrict__ pool, const int64_t *__restrict__ offsets,
+    const uint64_t *__restrict__ pages, int32_t pt_width, int32_t pt_shift,
     const int32_t *__restrict__ lens, int32_t batch, const QT *__restrict__ q_lat,
     const QT *__restrict__ q_rope, int32_t rows, float scale_log2, int32_t seg_tokens,
     int32_t pending, int2 *__restrict__ seq_info, uint16_t *__restrict__ part_o,
@@ -699,7 +725,7 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
       sg.slot = __builtin_amdgcn_readfirstlane(d.slot);
     }
     const int64_t qrow_c = (int64_t)sg.seq * rows + row_c;
-    const uint8_t *seq_base = pool + offsets[sg.seq] * (int64_t)(SH::W * 2);
+    const uint64_t *prow = pages + (int64_t)sg.seq * pt_width;
     const int T = sg.t1 - sg.t0;
     const int ntiles = (T + kTok - 1) / kTok;
     auto stage = [&](int t) { return ring + (t % NSTAGE) * SH::STAGE_BYTES; };
@@ -709,8 +735,8 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
 #pragma unroll
       for (int p = 0; p < NSTAGE - 1; ++p)
         if (p < ntiles)
-          issue_any_tile<SH, NW>(seq_base, sg.t0 + p * kTok, sg.t1, stage(p), wave, lane, v_kv,
-                                 v_rope, wd);
+          issue_any_tile<SH, NW>(tile_rows<SH>(prow, pt_shift, sg.t0 + p * kTok), sg.t0 + p * kTok,
+                                 sg.t1, stage(p), wave, lane, v_kv, v_rope, wd);
     };
     prologue();
 
@@ -760,6 +786,10 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
       // their (possibly clamped) DMA up front and mask the scores.
       auto step = [&](auto fast, int it) __attribute__((always_inline)) {
         constexpr bool FAST = decltype(fast)::value;
+        const int nxt = it + NSTAGE - 1;
+        // rows of tile nxt, loaded ahead of barrier A, whose wait covers it
+        const uint8_t *nxt_rows =
+            tile_rows<SH>(prow, pt_shift, sg.t0 + min(nxt, ntiles - 1) * kTok);
         // tile it+1 must be complete; tile it+2 (if issued) may stay in flight
         if constexpr (FAST)
           wait_tiles<SH, NW>(NSTAGE - 3, my_instr);
@@ -770,16 +800,13 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
         __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        const int nxt = it + NSTAGE - 1;
         if (!FAST && nxt < ntiles)
-          issue_any_tile<SH, NW>(seq_base, sg.t0 + nxt * kTok, sg.t1, stage(nxt), wave, lane,
+          issue_any_tile<SH, NW>(nxt_rows, sg.t0 + nxt * kTok, sg.t1, stage(nxt), wave, lane,
                                  v_kv, v_rope, wd);
         p_write(la, pbuf_u, pn);
         __builtin_amdgcn_sched_barrier(0);
-        s_phase<SH, NW, FAST>(
-            la, stage(it + 1), qf, s,
-            FullTileDma{seq_base + (int64_t)(sg.t0 + nxt * kTok) * (SH::W * 2), stage(nxt), wave,
-                        v_kv, v_rope, wd});
+        s_phase<SH, NW, FAST>(la, stage(it + 1), qf, s,
+                              FullTileDma{nxt_rows, stage(nxt), wave, v_kv, v_rope, wd});
         // Barrier B: P^T of tile it is complete in LDS.
         __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
         __builtin_amdgcn_s_barrier();
@@ -999,7 +1026,7 @@ constexpr size_t narrow_lds_bytes() {
 
 template <int R, int DR, typename QT>
 __global__ __launch_bounds__(256) void k_decode_narrow(
-    const uint8_t *__restrict__ pool, const int64_t *__restrict__ offsets,
+    const uint64_t *__restrict__ pages, int32_t pt_width, int32_t pt_shift,
     const int32_t *__restrict__ lens, int32_t batch, const QT *__restrict__ q_lat,
     const QT *__restrict__ q_rope, int32_t rows, float scale_log2, int32_t seg_tokens,
     int32_t pending, int2 *__restrict__ seq_info, uint16_t *__restrict__ part_o,
@@ -1077,7 +1104,7 @@ __global__ __launch_bounds__(256) void k_decode_narrow(
       sg.slot = __builtin_amdgcn_readfirstlane(d.slot);
     }
     const int64_t qrow_c = (int64_t)sg.seq * rows + row_c;
-    const uint8_t *seq_base = pool + offsets[sg.seq] * (int64_t)(SH::W * 2);
+    const uint64_t *prow = pages + (int64_t)sg.seq * pt_width;
     const int T = sg.t1 - sg.t0;
     const int ntiles = (T + kTok - 1) / kTok;
     auto stage = [&](int t) { return ring + (t % NSTAGE) * SH::STAGE_BYTES; };
@@ -1086,8 +1113,8 @@ __global__ __launch_bounds__(256) void k_decode_narrow(
 #pragma unroll
       for (int p = 0; p < NSTAGE - 1; ++p)
         if (p < ntiles)
-          issue_any_tile<SH, NW>(seq_base, sg.t0 + p * kTok, sg.t1, stage(p), wave, lane, v_kv,
-                                 v_rope, wd);
+          issue_any_tile<SH, NW>(tile_rows<SH>(prow, pt_shift, sg.t0 + p * kTok), sg.t0 + p * kTok,
+                                 sg.t1, stage(p), wave, lane, v_kv, v_rope, wd);
     };
     prologue();
     bf16x8_t qf[KQ];
@@ -1114,6 +1141,10 @@ __global__ __launch_bounds__(256) void k_decode_narrow(
       if (lane == 0) ds_w32(flags_u + 4 * wave, 0u);
       if (m_init != -INFINITY) prologue();
       for (int it = 0; it < ntiles; ++it) {
+        const int nxt = it + NSTAGE - 1;
+        // rows of tile nxt, loaded ahead of the wait below, which covers it
+        const uint8_t *nxt_rows =
+            tile_rows<SH>(prow, pt_shift, sg.t0 + min(nxt, ntiles - 1) * kTok);
         // tile it complete and visible; P.V of tile it-1 done everywhere
         wait_tiles<SH, NW>(min(NSTAGE - 2, ntiles - 1 - it), my_instr);
         wait_lgkm<0>();
@@ -1121,13 +1152,11 @@ __global__ __launch_bounds__(256) void k_decode_narrow(
         __builtin_amdgcn_sched_barrier(0);
         // DMA of tile nxt: a full tile's slots go under the S^T MFMAs, a
         // partial (clamped) one is issued up front
-        const int nxt = it + NSTAGE - 1;
         const bool full_nxt = nxt < ntiles && (nxt + 1) * kTok <= T;
         if (nxt < ntiles && !full_nxt)
-          issue_any_tile<SH, NW>(seq_base, sg.t0 + nxt * kTok, sg.t1, stage(nxt), wave, lane, v_kv,
+          issue_any_tile<SH, NW>(nxt_rows, sg.t0 + nxt * kTok, sg.t1, stage(nxt), wave, lane, v_kv,
                                  v_rope, wd);
-        const FullTileDma fd{seq_base + (int64_t)(sg.t0 + nxt * kTok) * (SH::W * 2), stage(nxt),
-                             wave, v_kv, v_rope, wd};
+        const FullTileDma fd{nxt_rows, stage(nxt), wave, v_kv, v_rope, wd};
         const uint32_t st = lds_u32(stage(it));
         // partial S^T over this wave's k-steps, to LDS by quarter
         narrow_s_phase<KQ>(st, sa, qf, s, [&](int kk) __attribute__((always_inline)) {
@@ -1314,17 +1343,17 @@ qmla_status launch_shape(const DecodeArgs &a, hipStream_t stream) {
   dim3 grid(a.blocks, passes), block(NW * 64);
   const float sl2 = a.scale * 1.4426950408889634f;
   const int32_t seg_tokens = decode_mfma_seg_tokens(a.rows, R, DR);
-  const uint8_t *pool = static_cast<const uint8_t *>(a.cache->rows);
+  const PageTable tab = a.cache->table();
   if (a.q_dtype == QMLA_BF16) {
     auto k = k_decode_mfma<R, DR, NW, NSTAGE, uint16_t>;
     QMLA_TRY(ensure_dynamic_lds((const void *)k, lds));
-    k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, a.cache->d_lens, a.batch,
+    k<<<grid, block, lds, stream>>>(tab.pages, tab.width, tab.shift, a.cache->d_lens, a.batch,
                                     (const uint16_t *)a.q_lat, (const uint16_t *)a.q_rope, a.rows,
                                     sl2, seg_tokens, a.pending, a.seq_info, (uint16_t *)a.part_o, a.part_lse);
   } else {
     auto k = k_decode_mfma<R, DR, NW, NSTAGE, float>;
     QMLA_TRY(ensure_dynamic_lds((const void *)k, lds));
-    k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, a.cache->d_lens, a.batch,
+    k<<<grid, block, lds, stream>>>(tab.pages, tab.width, tab.shift, a.cache->d_lens, a.batch,
                                     (const float *)a.q_lat, (const float *)a.q_rope, a.rows, sl2,
                                     seg_tokens, a.pending, a.seq_info, (uint16_t *)a.part_o, a.part_lse);
   }
@@ -1338,17 +1367,17 @@ qmla_status launch_narrow(const DecodeArgs &a, hipStream_t stream) {
   dim3 grid(a.blocks, 1), block(256);
   const float sl2 = a.scale * 1.4426950408889634f;
   const int32_t seg_tokens = decode_mfma_seg_tokens(a.rows, R, DR);
-  const uint8_t *pool = static_cast<const uint8_t *>(a.cache->rows);
+  const PageTable tab = a.cache->table();
   if (a.q_dtype == QMLA_BF16) {
     auto k = k_decode_narrow<R, DR, uint16_t>;
     QMLA_TRY(ensure_dynamic_lds((const void *)k, lds));
-    k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, a.cache->d_lens, a.batch,
+    k<<<grid, block, lds, stream>>>(tab.pages, tab.width, tab.shift, a.cache->d_lens, a.batch,
                                     (const uint16_t *)a.q_lat, (const uint16_t *)a.q_rope, a.rows,
                                     sl2, seg_tokens, a.pending, a.seq_info, (uint16_t *)a.part_o, a.part_lse);
   } else {
     auto k = k_decode_narrow<R, DR, float>;
     QMLA_TRY(ensure_dynamic_lds((const void *)k, lds));
-    k<<<grid, block, lds, stream>>>(pool, a.cache->d_offsets, a.cache->d_lens, a.batch,
+    k<<<grid, block, lds, stream>>>(tab.pages, tab.width, tab.shift, a.cache->d_lens, a.batch,
                                     (const float *)a.q_lat, (const float *)a.q_rope, a.rows, sl2,
                                     seg_tokens, a.pending, a.seq_info, (uint16_t *)a.part_o, a.part_lse);
   }

@@ -5,10 +5,29 @@
 
 #include "common.hpp"
 
-// Latent KV cache: one row [c_kv | k_pe] per token, sequence i owning rows
-// [offsets[i], offsets[i] + capacity[i]) of a single HBM pool.  Lengths are
-// kept on the device (read by kernels) and mirrored on the host (validation
-// without a device sync).
+namespace qmla {
+
+// Block table of a paged latent cache: token t of sequence s is row
+// t & (2^shift - 1) of page pages[s * width + (t >> shift)] (a device
+// address).  Pages hold 2^shift rows, a multiple of the 32-token tile of the
+// MFMA decode, so a tile that starts at a multiple of 32 lies in one page.
+struct PageTable {
+  const uint64_t *pages;  // device [sequences][width]
+  int32_t width;
+  int32_t shift;
+  __device__ __forceinline__ uint8_t *row(int32_t seq, int64_t t, int64_t row_bytes) const {
+    const uint64_t page = pages[(int64_t)seq * width + (t >> shift)];
+    return reinterpret_cast<uint8_t *>(page) + (t & ((int64_t(1) << shift) - 1)) * row_bytes;
+  }
+};
+
+}  // namespace qmla
+
+// Latent KV cache: one row [c_kv | k_pe] per token in pages of page_rows
+// rows taken from HBM chunks; sequence i owns the pages listed in its block
+// table row, h_npages[i] of them.  Lengths and the table are kept on the
+// device (read by kernels) and mirrored on the host (validation and page
+// bookkeeping without a device sync).
 struct qmla_kv_cache {
   int device = 0;
   int32_t num_seqs = 0;
@@ -16,18 +35,31 @@ struct qmla_kv_cache {
   int32_t dr = 0;
   qmla_dtype dtype = QMLA_F32;
   int64_t row_elems = 0;
-  int64_t total_rows = 0;
-  void *rows = nullptr;          // device [total_rows, row_elems]
-  int64_t *d_offsets = nullptr;  // device [num_seqs]
+  int32_t page_rows = 0;
+  int32_t page_shift = 0;
+  int32_t table_width = 0;       // pages one sequence can hold
+  uint64_t *d_pages = nullptr;   // device [num_seqs][table_width] page addresses
   int32_t *d_lens = nullptr;     // device [num_seqs]
   int32_t *d_cap = nullptr;      // device [num_seqs]
-  std::vector<int64_t> h_offsets;
+  std::vector<uint64_t> h_pages;
+  std::vector<int32_t> h_npages;
   std::vector<int32_t> h_lens;
-  std::vector<int32_t> h_cap;
-  bool grow = false;  // appends past capacity grow it instead of failing
+  std::vector<int32_t> h_cap;    // capacity (rows), <= h_npages * page_rows
+  std::vector<void *> chunks;    // HBM chunks the pages come from
+  int64_t pool_pages = 0;        // pages over all chunks
+  std::vector<uint64_t> free_pages;  // unowned pages (taken from the back)
+  // Layout at creation: chunks[0] holds every sequence's pages in order,
+  // sequence i from row offset h_offsets[i].  Holds while `contiguous`.
+  int64_t total_rows = 0;        // rows of chunks[0]
+  int64_t *d_offsets = nullptr;  // device [num_seqs]
+  std::vector<int64_t> h_offsets;
+  bool contiguous = true;
+  bool grow = false;  // appends past capacity take more pages instead of failing
 
   size_t elem_bytes() const { return dtype == QMLA_BF16 ? 2 : 4; }
   size_t row_bytes() const { return (size_t)row_elems * elem_bytes(); }
+  size_t page_bytes() const { return (size_t)page_rows * row_bytes(); }
+  qmla::PageTable table() const { return qmla::PageTable{d_pages, table_width, page_shift}; }
 };
 
 namespace qmla {

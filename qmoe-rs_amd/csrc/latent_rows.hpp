@@ -17,9 +17,8 @@ struct LatentRowsArgs {
   float eps;
   const float *inv_freq;   // [dr / 2]
   float mscale;
-  void *pool;              // cache rows (f32 or bf16 bits)
+  PageTable table;         // cache pages (rows f32 or bf16 bits)
   bool bf16;
-  const int64_t *offsets;  // [sequences] first pool row
   const int32_t *lens;     // [sequences] current length (the new rows go after it)
   float *rows;             // optional f32 copy [tokens][r + dr], or null
 };
@@ -41,8 +40,8 @@ __host__ __device__ inline size_t latent_row_lds_bytes(int r, int dr) {
   return sizeof(float) * ((size_t)r + dr + 16);
 }
 
-// Token `tok` = (b, i) of the call: its row goes to pool row
-// offsets[b] + lens[b] + i at position lens[b] + i.  LayerNorm as
+// Token `tok` = (b, i) of the call: its row goes to sequence b's cache row
+// lens[b] + i (through the block table) at position lens[b] + i.  LayerNorm as
 // candle_nn::LayerNorm (src/model.rs:136): mean, biased variance of the
 // centred values, divide by sqrt(var + eps), weight, bias.  `lds` holds
 // latent_row_lds_bytes(r, dr): the row is read from HBM once.
@@ -54,13 +53,13 @@ __device__ inline void latent_row(const LatentRowsArgs &a, int tok, float *lds) 
   __syncthreads();
   float *y = a.rows ? a.rows + (int64_t)tok * (r + dr) : nullptr;
   const int32_t len = a.lens[b];
-  const int64_t drow = (a.offsets[b] + len + i) * (int64_t)(r + dr);
+  uint8_t *dst = a.table.row(b, (int64_t)len + i, (int64_t)(r + dr) * (a.bf16 ? 2 : 4));
   auto put = [&](int c, float v) {
     if (y) y[c] = v;
     if (a.bf16)
-      static_cast<uint16_t *>(a.pool)[drow + c] = f32_to_bf16_bits(v);
+      reinterpret_cast<uint16_t *>(dst)[c] = f32_to_bf16_bits(v);
     else
-      static_cast<float *>(a.pool)[drow + c] = v;
+      reinterpret_cast<float *>(dst)[c] = v;
   };
   float sum = 0.f;
   for (int c = threadIdx.x; c < r; c += blockDim.x) sum += x[c];

@@ -183,9 +183,8 @@ LatentRowsArgs latent_rows_args(const qmla_layer *L, const float *kva, int seq, 
   a.eps = (float)g.ln_eps;
   a.inv_freq = L->inv_freq;
   a.mscale = (float)g.rope_mscale;
-  a.pool = cache->rows;
+  a.table = cache->table();
   a.bf16 = cache->dtype == QMLA_BF16;
-  a.offsets = cache->d_offsets;
   a.lens = cache->d_lens;
   a.rows = rows;
   return a;
@@ -263,14 +262,13 @@ __global__ __launch_bounds__(128) void k_merge_heads(const float *__restrict__ c
 
 // Materialising the reference KVCache (src/model.rs:86-105) from latent rows:
 // the c_kv part of sequence seq0 + b's first T rows as f32 [n, T, r] (the
-// A operand of the kv_b_proj GEMMs for a bf16 cache).
+// A operand of the kv_b_proj GEMMs).
 template <typename SrcT>
-__global__ __launch_bounds__(256) void k_latent_c_f32(const SrcT *__restrict__ pool,
-                                                      const int64_t *__restrict__ offsets,
-                                                      int seq0, int T, int r, int dr,
-                                                      float *__restrict__ dst) {
+__global__ __launch_bounds__(256) void k_latent_c_f32(PageTable tab, int seq0, int T, int r,
+                                                      int dr, float *__restrict__ dst) {
   const int t = blockIdx.x, b = blockIdx.y;
-  const SrcT *src = pool + (offsets[seq0 + b] + t) * (int64_t)(r + dr);
+  const SrcT *src =
+      reinterpret_cast<const SrcT *>(tab.row(seq0 + b, t, (int64_t)(r + dr) * sizeof(SrcT)));
   float *o = dst + ((int64_t)b * T + t) * r;
   for (int c = threadIdx.x; c < r; c += blockDim.x) {
     if constexpr (sizeof(SrcT) == 2)
@@ -283,12 +281,12 @@ __global__ __launch_bounds__(256) void k_latent_c_f32(const SrcT *__restrict__ p
 // k_rope [n, H, T, dr]: the stored (roped) k_pe of each token broadcast to
 // every head, as the reference's expand at src/model.rs:217-219 / :281-285.
 template <typename SrcT>
-__global__ __launch_bounds__(256) void k_broadcast_rope(const SrcT *__restrict__ pool,
-                                                        const int64_t *__restrict__ offsets,
-                                                        int seq0, int T, int H, int r, int dr,
+__global__ __launch_bounds__(256) void k_broadcast_rope(PageTable tab, int seq0, int T, int H,
+                                                        int r, int dr,
                                                         float *__restrict__ k_rope) {
   const int t = blockIdx.x, b = blockIdx.y;
-  const SrcT *src = pool + (offsets[seq0 + b] + t) * (int64_t)(r + dr) + r;
+  const SrcT *src =
+      reinterpret_cast<const SrcT *>(tab.row(seq0 + b, t, (int64_t)(r + dr) * sizeof(SrcT))) + r;
   for (int e = threadIdx.x; e < H * dr; e += blockDim.x) {
     const int h = e / dr, c = e % dr;
     float v;
@@ -462,7 +460,7 @@ qmla_status check_materialise(const qmla_layer *L, const qmla_kv_cache *c, int32
 }
 
 size_t materialise_ws_bytes(const qmla_kv_cache *c, int32_t n, int32_t T) {
-  return c->dtype == QMLA_BF16 ? sizeof(float) * (size_t)n * T * c->r : 0;
+  return sizeof(float) * (size_t)n * T * c->r;
 }
 
 // Decode workspace for the largest piece count the decode may choose
@@ -784,26 +782,28 @@ qmla_status qmla_cache_materialise(const qmla_layer *L, const qmla_kv_cache *cac
   const bool bf = cache->dtype == QMLA_BF16;
   if (k_rope && dr > 0) {
     if (bf)
-      k_broadcast_rope<uint16_t><<<dim3(T, n_seqs), dim3(256), 0, s>>>(
-          (const uint16_t *)cache->rows, cache->d_offsets, seq0, T, H, r, dr, k_rope);
+      k_broadcast_rope<uint16_t><<<dim3(T, n_seqs), dim3(256), 0, s>>>(cache->table(), seq0, T, H,
+                                                                        r, dr, k_rope);
     else
-      k_broadcast_rope<float><<<dim3(T, n_seqs), dim3(256), 0, s>>>(
-          (const float *)cache->rows, cache->d_offsets, seq0, T, H, r, dr, k_rope);
+      k_broadcast_rope<float><<<dim3(T, n_seqs), dim3(256), 0, s>>>(cache->table(), seq0, T, H, r,
+                                                                     dr, k_rope);
     QMLA_LAUNCH_CHECK("k_broadcast_rope");
   }
   if (!k && !v) return QMLA_OK;
+  // the c_kv rows, gathered from the pages into [n, T, r] f32
   float *lat = static_cast<float *>(workspace);
-  if (bf) {
-    k_latent_c_f32<uint16_t><<<dim3(T, n_seqs), dim3(256), 0, s>>>(
-        (const uint16_t *)cache->rows, cache->d_offsets, seq0, T, r, dr, lat);
-    QMLA_LAUNCH_CHECK("k_latent_c_f32");
-  }
+  if (bf)
+    k_latent_c_f32<uint16_t><<<dim3(T, n_seqs), dim3(256), 0, s>>>(cache->table(), seq0, T, r,
+                                                                    dr, lat);
+  else
+    k_latent_c_f32<float><<<dim3(T, n_seqs), dim3(256), 0, s>>>(cache->table(), seq0, T, r, dr,
+                                                                 lat);
+  QMLA_LAUNCH_CHECK("k_latent_c_f32");
   // compute_kv (src/model.rs:178-190) per sequence, batched over heads:
   //   k[b][h] = c_b W_UK^h^T + b_K^h,  v[b][h] = c_b W_UV^h^T + b_V^h
   for (int32_t b = 0; b < n_seqs; ++b) {
-    const float *A = bf ? lat + (size_t)b * T * r
-                        : (const float *)cache->rows + cache->h_offsets[seq0 + b] * (r + dr);
-    const int64_t lda = bf ? r : r + dr;
+    const float *A = lat + (size_t)b * T * r;
+    const int64_t lda = r;
     if (k) {
       GemmArgs a{A, L->wkvb, L->bkvb, k + (size_t)b * H * T * dn, T, dn, r, lda, r, dn,
                  0, (int64_t)(dn + dv) * r, (int64_t)T * dn, (int64_t)(dn + dv)};

@@ -56,7 +56,8 @@ class CacheDesc(C.Structure):
     _fields_ = [("num_seqs", C.c_int32), ("kv_lora_rank", C.c_int32), ("rope_dim", C.c_int32),
                 ("dtype", C.c_int), ("row_elems", C.c_int64), ("total_rows", C.c_int64),
                 ("rows", C.c_void_p), ("offsets", C.c_void_p), ("lengths", C.c_void_p),
-                ("capacity", C.c_void_p)]
+                ("capacity", C.c_void_p), ("pages", C.c_void_p), ("page_rows", C.c_int32),
+                ("table_width", C.c_int32), ("contiguous", C.c_int32), ("reserved", C.c_int32)]
 
 
 class LayerConfig(C.Structure):
@@ -94,6 +95,8 @@ SIGNATURES = {
     "qmla_reference_eager_attn": (_st, [_i32] * 5 + [_st, _vp, _vp, _vp, _d, C.c_int, _vp, _vp]),
     "qmla_eager_prefill_attn": (_st, [_i32] * 5 + [_st, _vp, _vp, _vp, _d, C.c_int, _vp, _vp]),
     "qmla_cache_create": (_st, [_i32, C.POINTER(_i32), _i32, _i32, _st, C.POINTER(_vp)]),
+    "qmla_cache_create_paged": (_st, [_i32, C.POINTER(_i32), C.c_int64, C.c_int64, _i32, _i32, _i32, _st,
+                                      C.POINTER(_vp)]),
     "qmla_cache_destroy": (_st, [_vp]),
     "qmla_cache_clone": (_st, [_vp, C.POINTER(_vp), _vp]),
     "qmla_cache_append": (_st, [_vp, _vp, _st, _i32, _i32, _vp]),
@@ -101,9 +104,13 @@ SIGNATURES = {
     "qmla_cache_set_lengths": (_st, [_vp, C.POINTER(_i32), _vp]),
     "qmla_cache_lengths": (_st, [_vp, C.POINTER(_i32)]),
     "qmla_cache_describe": (_st, [_vp, C.POINTER(CacheDesc)]),
+    "qmla_cache_gather": (_st, [_vp, _i32, _i32, _i32, _vp, _vp]),
     "qmla_cache_reserve": (_st, [_vp, C.POINTER(_i32), _vp]),
     "qmla_cache_set_growth": (_st, [_vp, _i32]),
     "qmla_cache_capacity": (_st, [_vp, C.POINTER(_i32)]),
+    "qmla_cache_reserve_pool": (_st, [_vp, C.c_int64]),
+    "qmla_cache_trim": (_st, [_vp, _i32, _i32, _vp]),
+    "qmla_cache_pool_info": (_st, [_vp, C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
     "qmla_decode_workspace_bytes": (_st, [C.POINTER(DecodeDims), _vp, C.POINTER(_sz)]),
     "qmla_decode_workspace_bytes_splits": (_st, [C.POINTER(DecodeDims), _vp, _i32, C.POINTER(_sz)]),
     "qmla_decode_absorbed": (_st, [C.POINTER(DecodeDims), _vp, _st, _vp, _vp, _d, _vp, _vp, _vp, _sz, _vp]),
@@ -277,14 +284,15 @@ class KVCache:
     """Latent KV cache (replaces KVCache, src/model.rs:86-105)."""
 
     def __init__(self, capacity, kv_lora_rank: int, rope_dim: int, dtype: int = BF16, _handle=None,
-                 grow: bool = False):
+                 grow: bool = False, page_rows: int = 0, max_len: int = 0, pool_rows: int = 0):
         cap = np.ascontiguousarray(capacity, np.int32)
         self.num_seqs = int(cap.size)
         self.r, self.dr, self.dtype = kv_lora_rank, rope_dim, dtype
         if _handle is None:
             h = C.c_void_p()
-            check(lib().qmla_cache_create(self.num_seqs, cap.ctypes.data_as(C.POINTER(C.c_int32)),
-                                          kv_lora_rank, rope_dim, dtype, C.byref(h)))
+            check(lib().qmla_cache_create_paged(self.num_seqs, cap.ctypes.data_as(C.POINTER(C.c_int32)),
+                                                max_len, pool_rows, page_rows, kv_lora_rank, rope_dim,
+                                                dtype, C.byref(h)))
             _handle = h.value
         self.handle = _handle
         if grow:
@@ -330,9 +338,17 @@ class KVCache:
         c.num_seqs, c.r, c.dr, c.dtype, c.handle = self.num_seqs, self.r, self.dr, self.dtype, h.value
         return c
 
-    def read_rows(self) -> np.ndarray:
-        """Whole pool as numpy ([total_rows, r + dr], f32 or uint16)."""
+    def _contiguous_desc(self) -> CacheDesc:
         d = self.describe()
+        if not d.contiguous:
+            raise QmlaError(2, "the cache's pages are no longer laid out in order; "
+                                            "read sequences with read_seq")
+        return d
+
+    def read_rows(self) -> np.ndarray:
+        """Whole creation-time chunk as numpy ([total_rows, r + dr], f32 or
+        uint16); sequence i starts at row offsets()[i]."""
+        d = self._contiguous_desc()
         npdt = _DT[d.dtype]
         out = np.empty((d.total_rows, d.row_elems), npdt)
         if out.nbytes:
@@ -341,15 +357,62 @@ class KVCache:
         return out
 
     def write_pool(self, rows: np.ndarray):
-        """Overwrite the whole pool (host array in the cache dtype)."""
-        d = self.describe()
-        a = np.ascontiguousarray(rows, _DT[d.dtype])
-        assert a.size == d.total_rows * d.row_elems
+        """Overwrite the creation-time chunk from a host array in the cache
+        dtype: either the chunk itself ([total_rows, r + dr]) or the
+        sequences' capacities back to back ([sum(capacity), r + dr],
+        sequence i's rows first), which is spread to each sequence's offset."""
+        d = self._contiguous_desc()
+        a = np.ascontiguousarray(rows, _DT[d.dtype]).reshape(-1, d.row_elems)
+        if a.shape[0] != d.total_rows:
+            caps = self.capacity().astype(np.int64)
+            assert a.shape[0] == caps.sum(), (a.shape, d.total_rows, caps.sum())
+            pool = np.zeros((d.total_rows, d.row_elems), a.dtype)
+            offs, src = self.offsets(), 0
+            for i, c in enumerate(caps):
+                pool[offs[i]:offs[i] + c] = a[src:src + c]
+                src += c
+            a = pool
         check(lib().qmla_memcpy_h2d(d.rows, a.ctypes.data, a.nbytes, None))
         check(lib().qmla_stream_synchronize(None))
 
-    def offsets(self) -> np.ndarray:
+    def read_seq(self, seq: int, n: int = None, t0: int = 0) -> np.ndarray:
+        """Rows [t0, t0 + n) of one sequence (default: its live rows) as numpy,
+        gathered through the block table ([n, r + dr], f32 or uint16)."""
+        if n is None:
+            n = int(self.lengths()[seq]) - t0
+        out = np.empty((n, self.r + self.dr), _DT[self.dtype])
+        if n:
+            buf = DeviceBuffer(out.nbytes)
+            check(lib().qmla_cache_gather(self.handle, seq, t0, n, _p(buf), None))
+            check(lib().qmla_stream_synchronize(None))
+            check(lib().qmla_memcpy_d2h(out.ctypes.data, _p(buf), out.nbytes, None))
+        return out
+
+    def trim(self, seq0: int = 0, n_seqs: int = None, stream=None):
+        """Return pages beyond each listed sequence's length to the free list."""
+        n_seqs = self.num_seqs - seq0 if n_seqs is None else n_seqs
+        check(lib().qmla_cache_trim(self.handle, seq0, n_seqs, _sh(stream)))
+
+    def reserve_pool(self, free_rows: int):
+        """Top the free list up to at least free_rows rows (allocates now)."""
+        check(lib().qmla_cache_reserve_pool(self.handle, free_rows))
+
+    def pool_info(self):
+        """(pool rows, free rows)."""
+        a, b = C.c_int64(), C.c_int64()
+        check(lib().qmla_cache_pool_info(self.handle, C.byref(a), C.byref(b)))
+        return a.value, b.value
+
+    def page_table(self) -> np.ndarray:
+        """Host copy of the device block table [num_seqs, table_width] (uint64)."""
         d = self.describe()
+        out = np.empty((self.num_seqs, d.table_width), np.uint64)
+        check(lib().qmla_memcpy_d2h(out.ctypes.data, d.pages, out.nbytes, None))
+        check(lib().qmla_stream_synchronize(None))
+        return out
+
+    def offsets(self) -> np.ndarray:
+        d = self._contiguous_desc()
         out = np.empty(self.num_seqs, np.int64)
         check(lib().qmla_memcpy_d2h(out.ctypes.data, d.offsets, out.nbytes, None))
         check(lib().qmla_stream_synchronize(None))

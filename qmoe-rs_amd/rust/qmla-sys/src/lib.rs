@@ -76,6 +76,11 @@ pub struct qmla_cache_desc {
     pub offsets: *mut i64,
     pub lengths: *mut i32,
     pub capacity: *mut i32,
+    pub pages: *mut u64,
+    pub page_rows: i32,
+    pub table_width: i32,
+    pub contiguous: i32,
+    pub reserved: i32,
 }
 
 /// Shapes of an absorbed decode call.
@@ -165,6 +170,10 @@ extern "C" {
         num_seqs: i32, capacity: *const i32, kv_lora_rank: i32, rope_dim: i32, dtype: qmla_dtype,
         out: *mut *mut qmla_kv_cache
     ) -> qmla_status;
+    pub fn qmla_cache_create_paged(
+        num_seqs: i32, capacity: *const i32, max_len: i64, pool_rows: i64, page_rows: i32,
+        kv_lora_rank: i32, rope_dim: i32, dtype: qmla_dtype, out: *mut *mut qmla_kv_cache
+    ) -> qmla_status;
     pub fn qmla_cache_destroy(cache: *mut qmla_kv_cache) -> qmla_status;
     // #[derive(Clone)] KVCache, src/model.rs:87
     pub fn qmla_cache_clone(
@@ -187,11 +196,22 @@ extern "C" {
     pub fn qmla_cache_describe(
         cache: *const qmla_kv_cache, out: *mut qmla_cache_desc
     ) -> qmla_status;
+    pub fn qmla_cache_gather(
+        cache: *const qmla_kv_cache, seq: i32, t0: i32, n: i32, out: *mut c_void,
+        stream: qmla_stream
+    ) -> qmla_status;
     pub fn qmla_cache_reserve(
         cache: *mut qmla_kv_cache, min_capacity: *const i32, stream: qmla_stream
     ) -> qmla_status;
+    pub fn qmla_cache_reserve_pool(cache: *mut qmla_kv_cache, free_rows: i64) -> qmla_status;
     pub fn qmla_cache_set_growth(cache: *mut qmla_kv_cache, enable: i32) -> qmla_status;
     pub fn qmla_cache_capacity(cache: *const qmla_kv_cache, capacity_out: *mut i32) -> qmla_status;
+    pub fn qmla_cache_trim(
+        cache: *mut qmla_kv_cache, seq0: i32, n_seqs: i32, stream: qmla_stream
+    ) -> qmla_status;
+    pub fn qmla_cache_pool_info(
+        cache: *const qmla_kv_cache, pool_rows: *mut i64, free_rows: *mut i64
+    ) -> qmla_status;
     // attention core of forward_with_cache, src/model.rs:294-303
     pub fn qmla_decode_workspace_bytes(
         dims: *const qmla_decode_dims, cache: *const qmla_kv_cache, bytes: *mut usize

@@ -193,6 +193,44 @@ impl KVCache {
         }
         Ok(c)
     }
+    /// KVCache::new with the page pool laid out by the caller: `pool_rows`
+    /// rows of HBM now (growth draws on the spare ones without allocating),
+    /// `max_len` the longest a sequence may grow (0: default), `page_rows`
+    /// a power of two >= 32 (0: 256).
+    pub fn paged(capacity: &[i32], kv_lora_rank: usize, rope_dim: usize, dtype: DType, max_len: i64,
+                 pool_rows: i64, page_rows: i32, grow: bool) -> Result<Self> {
+        let mut raw: *mut qmla_kv_cache = ptr::null_mut();
+        ok(unsafe {
+            qmla_cache_create_paged(capacity.len() as i32, capacity.as_ptr(), max_len, pool_rows, page_rows,
+                                    kv_lora_rank as i32, rope_dim as i32, dtype.raw(), &mut raw)
+        })?;
+        let c = KVCache { raw, num_seqs: capacity.len(), kv_lora_rank, rope_dim, dtype };
+        if grow {
+            ok(unsafe { qmla_cache_set_growth(c.raw, 1) })?;
+        }
+        Ok(c)
+    }
+    /// Rows [t0, t0 + n) of sequence `seq` into `out` ([n, r + dr] in the
+    /// cache dtype), wherever its pages are.
+    pub fn gather(&self, seq: usize, t0: usize, n: usize, out: &mut DeviceBuffer, stream: &Stream) -> Result<()> {
+        assert!(out.bytes() >= n * (self.kv_lora_rank + self.rope_dim) * self.dtype.size(), "out too small");
+        ok(unsafe { qmla_cache_gather(self.raw, seq as i32, t0 as i32, n as i32, out.ptr_mut(), stream.raw()) })
+    }
+    /// Returns the pages of sequences seq0..seq0 + n beyond their lengths to
+    /// the free list.
+    pub fn trim(&mut self, seq0: usize, n: usize, stream: &Stream) -> Result<()> {
+        ok(unsafe { qmla_cache_trim(self.raw, seq0 as i32, n as i32, stream.raw()) })
+    }
+    /// Tops the free list up to at least `free_rows` rows (allocates now).
+    pub fn reserve_pool(&mut self, free_rows: i64) -> Result<()> {
+        ok(unsafe { qmla_cache_reserve_pool(self.raw, free_rows) })
+    }
+    /// (pool rows, free rows).
+    pub fn pool_info(&self) -> Result<(i64, i64)> {
+        let (mut a, mut b) = (0i64, 0i64);
+        ok(unsafe { qmla_cache_pool_info(self.raw, &mut a, &mut b) })?;
+        Ok((a, b))
+    }
     pub fn raw(&self) -> *mut qmla_kv_cache {
         self.raw
     }

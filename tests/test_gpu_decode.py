@@ -142,7 +142,7 @@ def test_decode_bf16_v3_ragged_full_size(qmla_gpu):
     print(f"C4 tokens={int(lens.sum())} min={lens.min()} max={lens.max()}", flush=True)
     cache = q.KVCache(lens, 512, 64, q.BF16)
     d = cache.describe()
-    total = int(lens.sum())
+    total = int(d.total_rows)  # every page, padding included
     tmp = q.DeviceBuffer(total * 576 * 4)
     q.check(q.lib().qmla_fill_normal_f32(tmp.ptr, total * 576, 77, 0.0, 1.0, None))
     q.check(q.lib().qmla_f32_to_bf16(tmp.ptr, d.rows, total * 576, None))
@@ -153,7 +153,7 @@ def test_decode_bf16_v3_ragged_full_size(qmla_gpu):
     out, lse = run(q, cache, ql, qr, s)
     assert np.isfinite(out).all() and np.isfinite(lse).all()
     pool = cache.read_rows()
-    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+    offs = cache.offsets()
     pick = [int(np.argmin(lens)), int(np.argmax(lens))] + list(range(0, 64, 9))
     rows = np.concatenate([bf16_to_f32(pool[offs[b]:offs[b] + lens[b]]) for b in pick])
     sel_lens = lens[pick]
@@ -164,8 +164,15 @@ def test_decode_bf16_v3_ragged_full_size(qmla_gpu):
         print(f"C4 seq {b} T={lens[b]} rel_err={err:.2e}", flush=True)
         assert err < TOL_BF16
         np.testing.assert_allclose(lse[b], rlse[i], atol=2e-2)
+    # Another split count cuts the sequences elsewhere, so P and the bf16
+    # partials round differently: each run stays within ~5e-3 of the oracle
+    # (above), two runs within the sum, on every sequence.
     out2, lse2 = run(q, cache, ql, qr, s, splits=97)
-    assert rel_err(out2, out) < 5e-3
+    for i, b in enumerate(pick):
+        assert rel_err(out2[b], ref[i]) < TOL_BF16
+    per_seq = [rel_err(out2[b], out[b]) for b in range(64)]
+    print(f"C4 splits=97 vs default: max per-sequence rel_err={max(per_seq):.2e}", flush=True)
+    assert max(per_seq) < 1e-2
     np.testing.assert_allclose(lse2, lse, atol=5e-3)
 
 

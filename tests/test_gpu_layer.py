@@ -46,8 +46,8 @@ def test_multi_token_decode_two_sequences(qmla_gpu, golden):
     cache.append(q.DeviceBuffer.from_numpy(lat), 2, 256)
     out = layer.forward_with_cache(O.normal((2, 3, 512), 9), cache)
     assert rel_err(out, golden["c1b_out"]) < TOL
-    pool = cache.read_rows().reshape(2, 259, 80)
-    assert rel_err(pool[:, 256:], golden["c1b_new_rows"]) < TOL
+    rows = np.stack([cache.read_seq(i) for i in range(2)])
+    assert rel_err(rows[:, 256:], golden["c1b_new_rows"]) < TOL
 
 
 def test_prefill_then_decode_matches_reference(qmla_gpu):
@@ -136,7 +136,7 @@ def _ragged_cache(q, lens, r, dr, dtype, seed, spare=2):
     else:
         cache.write_pool(pool)
     cache.set_lengths(lens)
-    offs = cache.offsets()
+    offs = np.concatenate([[0], np.cumsum(lens + spare)[:-1]])  # rows of `pool` per sequence
     per_seq = [pool[offs[i]:offs[i] + lens[i]] for i in range(lens.size)]
     return cache, per_seq
 
@@ -281,3 +281,34 @@ def test_decode_step_projections_at_v2lite_width(qmla_gpu, batch, seq, dt):
         worst = max(worst, rel_err(out[b], ref[0]))
     print(f"batch {batch} seq {seq} {dt}: worst rel_err={worst:.2e}")
     assert worst < tol
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_growth_mode_layer_loop_over_pages(qmla_gpu, dt):
+    """forward_prefill then decode steps of 1-3 tokens on a cache created
+    empty in growth mode with 32-row pages: the steps take new pages as the
+    sequences cross page boundaries, and every output and new cache row
+    matches the reference's decompressed path."""
+    q = qmla_gpu
+    w = O.MlaWeights.random(256, 4, 32, 16, 32, 64, seed=720)
+    layer = q.MlaLayer(w)
+    b, s = 3, 29
+    dtype = q.F32 if dt == "f32" else q.BF16
+    tol = TOL if dt == "f32" else 2e-2
+    cache = q.KVCache([0] * b, 64, 16, dtype, grow=True, page_rows=32)
+    xs = O.normal((b, s, 256), 721)
+    out = layer.forward_prefill(xs, cache)
+    ref, (k, v, kr) = O.mla_forward_prefill(w, xs)
+    assert rel_err(out, ref) < tol
+    n = s
+    for step, m in enumerate((1, 1, 2, 1, 3, 1, 29, 1)):
+        x1 = O.normal((b, m, 256), 730 + step)
+        out1 = layer.forward_with_cache(x1, cache)
+        ref1, (k, v, kr) = O.mla_forward_with_cache(w, x1, k, v, kr, return_cache=True)
+        n += m
+        err = rel_err(out1, ref1)
+        print(f"{dt} step {step} (+{m} -> {n}) rel_err={err:.2e}")
+        assert err < tol
+    assert list(cache.lengths()) == [n] * b
+    assert cache.describe().contiguous == 0
+    assert all(c >= n for c in cache.capacity())
