@@ -40,6 +40,7 @@ constexpr int kSlab = 4096;    // codes of B staged in LDS at once (128 KB)
 constexpr int kMfmaWaves = 4;  // waves per block; each owns 32 rows
 constexpr int kMfmaThreads = 64 * kMfmaWaves;
 constexpr int kMaxExperts = 4096;
+constexpr int kSelLds = 2048;  // routing tables up to this many pairs are read into LDS
 constexpr int kMaxK = 1 << 20;
 
 
@@ -57,6 +58,8 @@ struct PackedArgs {
   int32_t slices;           // with bins: blocks sharing an expert's bin; block
                             //   (e, s) takes its tiles s, s + slices, ...
   const int32_t *slots;     // bin position -> slot (null: identity)
+  const int32_t *sel;       // instead of ebin/slots: expert e's bin is the pairs p with
+  int32_t npairs;           //   sel[p] == e, ascending (each block reads it itself)
   int32_t count;
   float *out;               // out[slot * ld_out + row]
   int64_t ld_out;
@@ -74,12 +77,51 @@ struct TileInfo {
 // grid y is (expert, slice) and the block walks every slices-th tile of the
 // expert's bin starting at its slice; without, grid y is one tile of the
 // `count` slots.
+__device__ __forceinline__ bool binned(const PackedArgs &a) { return a.ebin || a.sel; }
+
 __device__ __forceinline__ int block_expert(const PackedArgs &a) {
-  return a.ebin ? (int)blockIdx.y / a.slices : 0;
+  return binned(a) ? (int)blockIdx.y / a.slices : 0;
 }
 
 __device__ __forceinline__ int block_slice(const PackedArgs &a) {
-  return a.ebin ? (int)blockIdx.y % a.slices : 0;
+  return binned(a) ? (int)blockIdx.y % a.slices : 0;
+}
+
+// Expert e's bin read from the routing table (the pairs p with sel[p] == e,
+// ascending p): returns its size, and with `out` lists the pairs at bin
+// positions [t0, t0 + n) into out[0..n).  Each thread scans a contiguous run
+// of the table; a block scan of the runs' counts orders them.  Every thread
+// of the block calls it (two barriers); tmp holds kMfmaWaves ints.
+__device__ int sel_bin(const int32_t *sel, int np, int e, int t0, int n, int *out, int *tmp) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int per = (np + kMfmaThreads - 1) / kMfmaThreads;
+  const int lo = min(np, tid * per), hi = min(np, lo + per);
+  int c = 0;
+  for (int p = lo; p < hi; ++p) c += sel[p] == e;
+  int incl = c;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(incl, o);
+    if (lane >= o) incl += u;
+  }
+  if (lane == 63) tmp[wave] = incl;
+  __syncthreads();
+  int base = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < kMfmaWaves; ++w) {
+    base += w < wave ? tmp[w] : 0;
+    total += tmp[w];
+  }
+  if (out) {
+    int r = base + incl - c;
+    for (int p = lo; p < hi && r < t0 + n; ++p)
+      if (sel[p] == e) {
+        if (r >= t0) out[r - t0] = p;
+        ++r;
+      }
+  }
+  __syncthreads();
+  return total;
 }
 
 __device__ __forceinline__ void block_range(const PackedArgs &a, int &first, int &count) {
@@ -131,6 +173,9 @@ __global__ __launch_bounds__(kMfmaThreads) void k_packed_mfma(PackedArgs a) {
   __shared__ int vexp[kTokTile];
   __shared__ unsigned long long vsum[kTokTile];
   __shared__ unsigned bmax[kTokTile];
+  __shared__ int sel_list[kTokTile];
+  __shared__ int sel_tmp[kMfmaWaves];
+  __shared__ int32_t sel_lds[kSelLds];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, h = lane >> 5;
@@ -165,15 +210,25 @@ __global__ __launch_bounds__(kMfmaThreads) void k_packed_mfma(PackedArgs a) {
         ring[d][i] = gload16(wp[i] + (NG > 0 ? d : min(d, ng0 - 1)) * 32);
   }
 
-  int first, count;
-  block_range(a, first, count);
+  int first = 0, count;
+  // the routing table, read once (into LDS when it fits)
+  const int32_t *bins = a.sel;
+  if (a.sel && a.npairs <= kSelLds) {
+    for (int p = tid; p < a.npairs; p += kMfmaThreads) sel_lds[p] = a.sel[p];
+    __syncthreads();
+    bins = sel_lds;
+  }
+  if (a.sel)
+    count = sel_bin(bins, a.npairs, expert, 0, 0, nullptr, sel_tmp);
+  else
+    block_range(a, first, count);
   const int tt0 = slice * kTokTile;
   if (count <= tt0) {  // no tile for this block: drain the requested groups
     wait_vm<0>();
     return;
   }
   // without bins the grid position is the block's only tile (count <= kTokTile)
-  const int tstep = a.ebin ? a.slices * kTokTile : kTokTile;
+  const int tstep = binned(a) ? a.slices * kTokTile : kTokTile;
   for (int tt = tt0; tt < count; tt += tstep) {
   const TileInfo ti{expert, first + tt, min(kTokTile, count - tt)};
   if (tt != tt0 || slice != 0) {
@@ -187,12 +242,13 @@ __global__ __launch_bounds__(kMfmaThreads) void k_packed_mfma(PackedArgs a) {
         ring[d][i] = gload16(wp[i] + (NG > 0 ? d : min(d, ng0 - 1)) * 32);
   }
 
+  if (a.sel) sel_bin(bins, a.npairs, expert, tt, ti.ntok, sel_list, sel_tmp);
   if (tid < kTokTile) {
     vmax[tid] = 0;
     vsum[tid] = 0;
     if (tid < ti.ntok) {
       const int pos = ti.start + tid;
-      const int slot = a.slots ? a.slots[pos] : pos;
+      const int slot = a.sel ? sel_list[tid] : a.slots ? a.slots[pos] : pos;
       const int src = slot / a.src_div;
       vslot[tid] = slot;
       voff[tid] = (int64_t)src * a.ld_x;
@@ -873,12 +929,16 @@ qmla_status qmla_moe_forward(const qmla_moe_config *cfg, const float *xs, int32_
   hipLaunchKernelGGL(k_moe_route, dim3(T), dim3(1024), 0, s, xs, gate_weight, c.num_experts, H,
                      c.top_k, sel, selw, top_experts, top_weights, xmax);
   QMLA_LAUNCH_CHECK("k_moe_route");
-  hipLaunchKernelGGL(k_moe_bin, dim3(1), dim3(1024), 0, s, sel, P, c.num_experts, ebin, slots);
-  QMLA_LAUNCH_CHECK("k_moe_bin");
-
   const bool fast_gu = mfma_ok(H) && aligned16(gate_packed) && aligned16(up_packed) &&
                        aligned16(xs);
   const bool fast_dn = mfma_ok(I) && aligned16(down_packed) && aligned16(hbuf);
+  // The MFMA GEMV blocks read their expert's bin from the routing table
+  // themselves; the per-row fallback walks prebuilt bins.
+  const bool block_bins = fast_gu && fast_dn;
+  if (!block_bins) {
+    hipLaunchKernelGGL(k_moe_bin, dim3(1), dim3(1024), 0, s, sel, P, c.num_experts, ebin, slots);
+    QMLA_LAUNCH_CHECK("k_moe_bin");
+  }
   PackedArgs gu{};
   gu.w[0] = gate_packed;
   gu.w[1] = up_packed;
@@ -891,8 +951,10 @@ qmla_status qmla_moe_forward(const qmla_moe_config *cfg, const float *xs, int32_
   gu.x = xs;
   gu.ld_x = H;
   gu.src_div = c.top_k;
-  gu.ebin = ebin;
-  gu.slots = slots;
+  gu.ebin = block_bins ? nullptr : ebin;
+  gu.slots = block_bins ? nullptr : slots;
+  gu.sel = block_bins ? sel : nullptr;
+  gu.npairs = P;
   gu.out = hbuf;
   gu.ld_out = I;
   gu.src_max = xmax;

@@ -24,11 +24,11 @@
 // and a wave's whole K-slice is one contiguous run.
 //
 // Work split: block (nb, z) owns 32 outputs (n) of one z (a head for the
-// batched per-head products); its NW waves take consecutive K-slices.  Each
-// wave streams its A fragments (hi and lo) from HBM into registers, two
-// chunks of kChunk steps in flight, reads its B fragments (16 k x 32
-// tokens) from the f32 activations, and accumulates C^T[32 n][32 m] in 16
-// registers.  The NW partial tiles are summed through LDS in slice order
+// batched per-head products); its NW (<= 16) waves take consecutive
+// K-slices.  Each wave streams its A fragments (hi and lo) from HBM into
+// registers, two chunks of kChunk steps in flight, reads its B fragments
+// (16 k x 32 tokens) from the f32 activations, and accumulates
+// C^T[32 n][32 m] in 16 registers.  The NW partial tiles are summed through LDS in slice order
 // (deterministic, no atomics) and the block's epilogue adds the bias and
 // writes the output in the layout its consumer reads:
 //   FINAL  y[m][n]
@@ -230,10 +230,13 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_gemm(SkinnyGemmArgs a, Laten
 
 }  // namespace
 
-// Waves per block: the K split, up to 8, with each wave's range a multiple
-// of 16 and at least 64 wide when K allows.
+// Waves per block: the K split, up to 16, with each wave's range a multiple
+// of 16 and at least 64 wide when K allows.  At 16 waves a K of 2048 leaves
+// each wave 8 k-steps, all of them in flight at once.  (A block's time is
+// set by what one CU moves -- its weight slab plus the activations -- not by
+// the number of waits: 8 and 16 waves time alike.)
 int skinny_waves(int K) {
-  int nw = 8;
+  int nw = 16;
   while (nw > 1 && (K % (16 * nw) != 0 || K / nw < 64)) nw >>= 1;
   return K % (16 * nw) == 0 ? nw : 0;
 }
@@ -280,6 +283,7 @@ qmla_status launch_skinny_gemm(const SkinnyGemmArgs &a, hipStream_t stream,
   if (a.x_packed) {
     QMLA_REQUIRE(a.Z == 1, QMLA_ERR_SHAPE, "packed activations need Z = 1");
     switch (nw) {
+      case 16: k_skinny_gemm<16, true><<<grid, dim3(1024), lds, stream>>>(a, ra, extra); break;
       case 8: k_skinny_gemm<8, true><<<grid, dim3(512), lds, stream>>>(a, ra, extra); break;
       case 4: k_skinny_gemm<4, true><<<grid, dim3(256), lds, stream>>>(a, ra, extra); break;
       case 2: k_skinny_gemm<2, true><<<grid, dim3(128), lds, stream>>>(a, ra, extra); break;
@@ -287,6 +291,7 @@ qmla_status launch_skinny_gemm(const SkinnyGemmArgs &a, hipStream_t stream,
     }
   } else {
     switch (nw) {
+      case 16: k_skinny_gemm<16, false><<<grid, dim3(1024), lds, stream>>>(a, ra, extra); break;
       case 8: k_skinny_gemm<8, false><<<grid, dim3(512), lds, stream>>>(a, ra, extra); break;
       case 4: k_skinny_gemm<4, false><<<grid, dim3(256), lds, stream>>>(a, ra, extra); break;
       case 2: k_skinny_gemm<2, false><<<grid, dim3(128), lds, stream>>>(a, ra, extra); break;
