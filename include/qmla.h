@@ -22,6 +22,10 @@
  *  - No global mutable state apart from the per-thread error string and a
  *    per-device cached CU count, so calls on different streams may run from
  *    different threads.  A cache object must not be mutated concurrently.
+ *    A layer object may be used from several threads at once: its GEMM path
+ *    (prefill, and decode shapes the skinny kernel does not take) takes one
+ *    of 4 rocBLAS handles created with the layer, so up to 4 such calls run
+ *    without waiting for each other.
  */
 #ifndef QMLA_H
 #define QMLA_H

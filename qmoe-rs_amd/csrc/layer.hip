@@ -18,10 +18,13 @@
 // rope key stored once (k_rope_heads = 1) instead of broadcast per head.
 
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <cstring>
+#include <functional>
 #include <mutex>
 #include <new>
+#include <thread>
 #include <vector>
 
 #include <rocblas/rocblas.h>
@@ -44,8 +47,15 @@ struct qmla_layer {
   float *buv = nullptr;  // [H][dv]: b_V^h
   bool skinny = false;   // the split weights exist (every K a multiple of 16)
   std::vector<void *> allocs;
-  rocblas_handle blas = nullptr;
-  mutable std::mutex blas_mu;
+  // rocBLAS handles for the GEMM path (prefill, and decode shapes the skinny
+  // kernel does not take).  A call takes a free one and sets its stream, so
+  // calls on different streams run concurrently up to kBlasHandles.
+  static constexpr int kBlasHandles = 4;
+  struct BlasSlot {
+    rocblas_handle h = nullptr;
+    std::mutex mu;
+  };
+  mutable std::array<BlasSlot, kBlasHandles> blas;
 };
 
 namespace qmla {
@@ -97,11 +107,27 @@ qmla_status gemm(const qmla_layer *L, const GemmArgs &g, int batch, bool trans_b
     beta = 1.f;
   }
   const float one = 1.f;
-  std::lock_guard<std::mutex> lock(L->blas_mu);  // the handle's stream is set per call
-  rocblas_status st = rocblas_set_stream(L->blas, s);
+  // a free handle, or (all busy) the one this thread maps to; the handle's
+  // stream is set per call
+  qmla_layer::BlasSlot *slot = nullptr;
+  std::unique_lock<std::mutex> lock;
+  for (auto &b : L->blas) {
+    std::unique_lock<std::mutex> l(b.mu, std::try_to_lock);
+    if (l.owns_lock()) {
+      slot = &b;
+      lock = std::move(l);
+      break;
+    }
+  }
+  if (!slot) {
+    slot = &L->blas[std::hash<std::thread::id>{}(std::this_thread::get_id()) %
+                    qmla_layer::kBlasHandles];
+    lock = std::unique_lock<std::mutex>(slot->mu);
+  }
+  rocblas_status st = rocblas_set_stream(slot->h, s);
   if (st == rocblas_status_success)
     st = rocblas_sgemm_strided_batched(
-        L->blas, trans_b ? rocblas_operation_transpose : rocblas_operation_none,
+        slot->h, trans_b ? rocblas_operation_transpose : rocblas_operation_none,
         rocblas_operation_none, g.N, g.M, g.K, &one, g.B, (rocblas_int)g.ldb, g.sB, g.A,
         (rocblas_int)g.lda, g.sA, &beta, g.C, (rocblas_int)g.ldc, g.sC, batch);
   QMLA_REQUIRE(st == rocblas_status_success, QMLA_ERR_HIP, "rocBLAS sgemm: %s",
@@ -515,10 +541,13 @@ qmla_status qmla_layer_create(const qmla_layer_config *cfg, const float *wq, con
   qmla_layer *L = new (std::nothrow) qmla_layer();
   QMLA_REQUIRE(L, QMLA_ERR_OOM, "host allocation failed");
   L->cfg = g;
-  if (rocblas_create_handle(&L->blas) != rocblas_status_success) {
-    delete L;
-    return fail(QMLA_ERR_HIP, "rocBLAS handle creation failed");
-  }
+  for (auto &b : L->blas)
+    if (rocblas_create_handle(&b.h) != rocblas_status_success) {
+      for (auto &c : L->blas)
+        if (c.h) (void)rocblas_destroy_handle(c.h);
+      delete L;
+      return fail(QMLA_ERR_HIP, "rocBLAS handle creation failed");
+    }
   const int H = g.heads;
   struct W {
     float **dst;
@@ -568,7 +597,7 @@ qmla_status qmla_layer_create(const qmla_layer_config *cfg, const float *wq, con
     st = make_skinny_weights(L, wq, bq, wkva, bkva, wkvb, bkvb, wo);
   if (st != QMLA_OK) {
     for (void *p : L->allocs) (void)hipFree(p);
-    (void)rocblas_destroy_handle(L->blas);
+    for (auto &b : L->blas) (void)rocblas_destroy_handle(b.h);
     delete L;
     return st;
   }
@@ -579,7 +608,8 @@ qmla_status qmla_layer_create(const qmla_layer_config *cfg, const float *wq, con
 qmla_status qmla_layer_destroy(qmla_layer *layer) {
   if (!layer) return QMLA_OK;
   for (void *p : layer->allocs) (void)hipFree(p);
-  if (layer->blas) (void)rocblas_destroy_handle(layer->blas);
+  for (auto &b : layer->blas)
+    if (b.h) (void)rocblas_destroy_handle(b.h);
   delete layer;
   return QMLA_OK;
 }

@@ -490,26 +490,26 @@ class MlaLayer:
         check(lib().qmla_layer_workspace_bytes(self.handle, cache.handle, batch, seq, C.byref(n)))
         return n.value
 
-    def forward_with_cache(self, xs: np.ndarray, cache: KVCache) -> np.ndarray:
+    def forward_with_cache(self, xs: np.ndarray, cache: KVCache, stream=None) -> np.ndarray:
         b, s, _ = xs.shape
         bx = DeviceBuffer.from_numpy(np.ascontiguousarray(xs, np.float32))
         out = DeviceBuffer(b * s * self.hidden * 4)
         wsb = self.workspace_bytes(cache, b, s)
         ws = DeviceBuffer(wsb)
         check(lib().qmla_layer_forward_with_cache(self.handle, bx.ptr, b, s, cache.handle, out.ptr, ws.ptr,
-                                                  wsb, None))
-        check(lib().qmla_stream_synchronize(None))
+                                                  wsb, _sh(stream)))
+        check(lib().qmla_stream_synchronize(_sh(stream)))
         return out.to_numpy(np.float32, (b, s, self.hidden))
 
-    def forward_prefill(self, xs: np.ndarray, cache: KVCache) -> np.ndarray:
+    def forward_prefill(self, xs: np.ndarray, cache: KVCache, stream=None) -> np.ndarray:
         b, s, _ = xs.shape
         bx = DeviceBuffer.from_numpy(np.ascontiguousarray(xs, np.float32))
         out = DeviceBuffer(b * s * self.hidden * 4)
         wsb = self.workspace_bytes(cache, b, s)
         ws = DeviceBuffer(wsb)
         check(lib().qmla_layer_forward_prefill(self.handle, bx.ptr, b, s, cache.handle, out.ptr, ws.ptr,
-                                               wsb, None))
-        check(lib().qmla_stream_synchronize(None))
+                                               wsb, _sh(stream)))
+        check(lib().qmla_stream_synchronize(_sh(stream)))
         return out.to_numpy(np.float32, (b, s, self.hidden))
 
     def materialise(self, cache: KVCache, seq0: int = 0, n_seqs: int | None = None):

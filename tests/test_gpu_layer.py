@@ -312,3 +312,34 @@ def test_growth_mode_layer_loop_over_pages(qmla_gpu, dt):
     assert list(cache.lengths()) == [n] * b
     assert cache.describe().contiguous == 0
     assert all(c >= n for c in cache.capacity())
+
+
+def test_layer_calls_from_several_threads(qmla_gpu):
+    """forward_prefill (the rocBLAS GEMM path) on one layer from four
+    threads at once, each with its own stream and cache, gives exactly the
+    results of the same calls made one after another."""
+    import threading
+    q = qmla_gpu
+    w = O.MlaWeights.random(256, 4, 32, 16, 32, 64, seed=800)
+    layer = q.MlaLayer(w)
+    xs = [O.normal((2, 37, 256), 801 + i) for i in range(4)]
+    want = [layer.forward_prefill(x, q.KVCache([40, 40], 64, 16, q.F32)) for x in xs]
+    got, errs = [None] * 4, []
+
+    def run(i):
+        try:
+            st = q.Stream()
+            for _ in range(3):
+                got[i] = layer.forward_prefill(xs[i], q.KVCache([40, 40], 64, 16, q.F32), stream=st)
+            st.close()
+        except Exception as e:  # reported below
+            errs.append(e)
+
+    ts = [threading.Thread(target=run, args=(i,)) for i in range(4)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join(timeout=120)
+    assert not errs, errs
+    for i in range(4):
+        np.testing.assert_array_equal(got[i], want[i])
