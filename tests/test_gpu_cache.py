@@ -246,3 +246,67 @@ def test_decode_over_scattered_pages(qmla_gpu, case):
     print(f"{case} lens={list(lens)} rel_err={err:.2e}")
     assert err < tol
     np.testing.assert_allclose(lse, rlse, atol=tol)
+
+
+def test_clone_of_scattered_cache_is_deep_and_packed(qmla_gpu):
+    """A clone of a cache whose pages are scattered holds the same rows per
+    sequence, packed in order into one chunk, and is independent of it."""
+    q = qmla_gpu
+    cache, held = _scattered_cache(q, q.BF16, 64, 16, (5, 40, 1, 70, 33), 3)
+    c2 = cache.clone()
+    assert c2.describe().contiguous == 1
+    assert list(c2.lengths()) == list(cache.lengths())
+    assert list(c2.capacity()) == list(cache.capacity())
+    for i in range(3):
+        np.testing.assert_array_equal(c2.read_seq(i), held[i])
+    more = O.normal((1, 50, 80), 9)
+    cache.append_seq(0, q.DeviceBuffer.from_numpy(more), 50)
+    np.testing.assert_array_equal(c2.read_seq(0), held[0])
+    np.testing.assert_array_equal(cache.read_seq(0), np.concatenate([held[0], bf16_bits(more[0])]))
+
+
+@pytest.mark.parametrize("page_rows", [64, 1024])
+def test_decode_over_other_page_sizes(qmla_gpu, page_rows):
+    """The same scattered-pages decode with 64- and 1024-row pages (the tile
+    and its page share a 32-row alignment for every power-of-two page)."""
+    q = qmla_gpu
+    cache, held = _scattered_cache(q, q.BF16, 512, 64, (33, 300, 64, 1111), 4, page_rows=page_rows,
+                                   seed=900 + page_rows)
+    lens = np.array([h.shape[0] for h in held], np.int32)
+    flat = bf16_to_f32(np.concatenate(held))
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+    for rows_m in (16, 128):
+        ql, qr = O.normal((4, rows_m, 512), 63), O.normal((4, rows_m, 64), 64)
+        out, lse = q.decode_numpy(cache, bf16_bits(ql), bf16_bits(qr), 192 ** -0.5, q_dtype=q.BF16)
+        ref, rlse = O.decode_absorbed(bf16_to_f32(bf16_bits(ql)), bf16_to_f32(bf16_bits(qr)), flat,
+                                      offs, lens, 192 ** -0.5)
+        err = np.abs(out - ref).max() / np.abs(ref).max()
+        print(f"page_rows={page_rows} rows={rows_m} lens={list(lens)} rel_err={err:.2e}")
+        assert err < 2e-2
+        np.testing.assert_allclose(lse, rlse, atol=2e-2)
+
+
+def test_trim_then_regrow_and_decode(qmla_gpu):
+    """Truncate every sequence, return the spare pages, regrow with new rows:
+    pages freed by one sequence are reused by another, and the decode sees
+    exactly the rows each sequence now holds."""
+    q = qmla_gpu
+    cache, held = _scattered_cache(q, q.F32, 64, 16, (40, 70), 3)
+    keep = [10, 33, 0]
+    cache.set_lengths(keep)
+    cache.trim()
+    pool, free = cache.pool_info()
+    assert free > 0
+    new = [O.normal((1, n, 80), 70 + i) for i, n in enumerate((90, 3, 150))]
+    for i, x in enumerate(new):
+        cache.append_seq(i, q.DeviceBuffer.from_numpy(x), x.shape[1])
+    assert cache.pool_info()[0] == pool            # no new chunk: freed pages reused
+    rows = [np.concatenate([held[i][:keep[i]], new[i][0]]) for i in range(3)]
+    for i in range(3):
+        np.testing.assert_array_equal(cache.read_seq(i), rows[i])
+    lens = np.array([r.shape[0] for r in rows], np.int32)
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+    ql, qr = O.normal((3, 4, 64), 81), O.normal((3, 4, 16), 82)
+    out, lse = q.decode_numpy(cache, ql, qr, 0.15)
+    ref, rlse = O.decode_absorbed(ql, qr, np.concatenate(rows), offs, lens, 0.15)
+    assert np.abs(out - ref).max() / np.abs(ref).max() < 1e-4
