@@ -215,8 +215,8 @@ QMLA_API qmla_status qmla_cache_gather(const qmla_kv_cache *cache, int32_t seq, 
  * (one small kernel on `stream`).  No row moves, no pointer from
  * qmla_cache_describe changes meaning except rows/offsets (see above), and
  * the host does not wait.  Device memory is allocated only when the free
- * list is short: then a chunk of max(missing pages, half the pool) pages is
- * added with hipMalloc.  qmla_cache_reserve_pool tops the free list up ahead
+ * list is short: then a chunk of max(missing pages, min(half the pool,
+ * 1 GiB)) is added with hipMalloc.  qmla_cache_reserve_pool tops the free list up ahead
  * of time, so that appends and layer calls allocate nothing.
  * qmla_cache_reserve raises sequence i's capacity to at least
  * min_capacity[i] (host array [num_seqs]; smaller entries change nothing).

@@ -9,8 +9,9 @@
 // the table with one small kernel on the caller's stream: no live row is
 // copied, nothing is re-laid out and the host never waits for the device.
 // Pages come from HBM chunks allocated at creation (pool_rows), by
-// qmla_cache_reserve, or -- only when the free list runs dry during an
-// append in growth mode -- by a new chunk sized to half the pool again.
+// qmla_cache_reserve / qmla_cache_reserve_pool, or -- only when the free
+// list runs dry during an append in growth mode -- by a new chunk of half
+// the pool again, at most 1 GiB (or the missing pages, if more).
 
 #include <algorithm>
 #include <cstring>
@@ -157,9 +158,12 @@ qmla_status ensure_capacity(qmla_kv_cache *c, int32_t seq0, const std::vector<in
                  (long long)want[i], (long long)std::min<int64_t>(max_rows, 0x7fffffff));
     extra += std::max<int64_t>(0, ceil_div(want[i], P) - c->h_npages[q]);
   }
-  if (extra > (int64_t)c->free_pages.size())
-    QMLA_TRY(add_chunk(c, std::max<int64_t>(extra - (int64_t)c->free_pages.size(),
-                                            std::max<int64_t>(1, c->pool_pages / 2))));
+  if (extra > (int64_t)c->free_pages.size()) {
+    // the missing pages, or half the pool again up to 1 GiB, whichever is more
+    const int64_t cap_pages = std::max<int64_t>(1, ((int64_t)1 << 30) / (int64_t)c->page_bytes());
+    const int64_t grow = std::max<int64_t>(1, std::min(c->pool_pages / 2, cap_pages));
+    QMLA_TRY(add_chunk(c, std::max(extra - (int64_t)c->free_pages.size(), grow)));
+  }
   TableWriter tw(c, s);
   for (int32_t i = 0; i < n; ++i) {
     const int32_t q = seq0 + i;
