@@ -41,6 +41,10 @@ namespace {
 
 using namespace pipe;
 
+__device__ __forceinline__ void ds_w64(uint32_t addr, u32x2_t v) {
+  asm volatile("ds_write_b64 %0, %1" : : "v"(addr), "v"(v));
+}
+
 constexpr int kPKeys = 32;      // keys per tile
 constexpr int kPWaves = 8;      // two groups of four
 constexpr int kPDmaWaves = 4;   // group 1 issues every tile's DMA
@@ -603,12 +607,17 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
   // the final P.V MFMAs complete before their accumulators are read
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 
-  // finalise
+  // finalise: O / l in bf16.  Lane (n, half) holds 4 consecutive columns
+  // of row n per (cb, jq); stored as they are, each store instruction
+  // would write 16 bytes into each of 32 rows.  When it fits, the wave's
+  // 32 rows go through its own region of the idle ring instead (every wave
+  // is past its last ring read: the overflow check's barrier), and each
+  // store instruction writes whole consecutive rows, 1 KB.
   const float l = xor32_sum(l_run);
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  const int row = row_first + n;
-  if (row < d.seq_q) {
-    uint16_t *dst = out + (bhq + row) * DV;
+  constexpr int STR = DV * 2 + 16;  // staged row stride in bytes (padded: fewer bank conflicts)
+  if constexpr (kPWaves * 32 * STR <= kPStages * SH::STAGE_BYTES) {
+    const uint32_t wb = ring_u + (uint32_t)(wave * 32 * STR);
 #pragma unroll
     for (int cb = 0; cb < SH::CB; ++cb)
 #pragma unroll
@@ -616,8 +625,37 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
         u32x2_t w;
         w[0] = pack2_bf16(o[cb][jq * 4 + 0] * inv, o[cb][jq * 4 + 1] * inv);
         w[1] = pack2_bf16(o[cb][jq * 4 + 2] * inv, o[cb][jq * 4 + 3] * inv);
-        *reinterpret_cast<u32x2_t *>(dst + cb * 32 + 8 * jq + 4 * half) = w;
+        ds_w64(wb + n * STR + (cb * 32 + 8 * jq + 4 * half) * 2, w);
       }
+    constexpr int CPR = DV / 8;        // 16-byte chunks per row
+    constexpr int RPI = 64 / CPR;      // rows per store instruction
+    constexpr int NI = 32 / RPI;       // store instructions per wave
+    const int lr = lane / CPR, lc = lane % CPR;
+    bf16x8_t rows[NI];
+    wait_lgkm<0>();
+#pragma unroll
+    for (int i = 0; i < NI; ++i) rows[i] = ds_b128<0>(wb + (i * RPI + lr) * STR + lc * 16);
+    wait_lgkm<0>();
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      arrived(rows[i]);
+      const int r = row_first + i * RPI + lr;
+      if (r < d.seq_q) *reinterpret_cast<bf16x8_t *>(out + (bhq + r) * DV + lc * 8) = rows[i];
+    }
+  } else {
+    const int row = row_first + n;
+    if (row < d.seq_q) {
+      uint16_t *dst = out + (bhq + row) * DV;
+#pragma unroll
+      for (int cb = 0; cb < SH::CB; ++cb)
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+          u32x2_t w;
+          w[0] = pack2_bf16(o[cb][jq * 4 + 0] * inv, o[cb][jq * 4 + 1] * inv);
+          w[1] = pack2_bf16(o[cb][jq * 4 + 2] * inv, o[cb][jq * 4 + 3] * inv);
+          *reinterpret_cast<u32x2_t *>(dst + cb * 32 + 8 * jq + 4 * half) = w;
+        }
+    }
   }
 }
 
