@@ -639,6 +639,91 @@ __device__ void plan_round(const int32_t *__restrict__ lens, int32_t pending, in
   __syncthreads();
 }
 
+// The same plan for batch <= 64, computed by every wave in registers (lane b
+// = sequence b): two shuffle scans and a ballot instead of LDS round trips
+// and barriers, so the first tiles are requested sooner.  A piece then holds
+// at most 64 <= kSegCap segments: one round.  Segment i is the i-th set bit
+// of mask, in ascending sequence order as in plan_round.
+struct WavePlan {
+  uint64_t mask;
+  int32_t t0, t1, slot;  // this lane's sequence
+};
+
+__device__ __forceinline__ int32_t wave_incl_scan(int32_t x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int32_t v = __shfl_up(x, off);
+    if (lane >= off) x += v;
+  }
+  return x;
+}
+
+__device__ WavePlan plan_wave(const int32_t *__restrict__ lens, int32_t pending, int32_t batch,
+                              int32_t seg_tokens, int2 *__restrict__ seq_info) {
+  static_assert(kSegCap >= 64, "one round per piece");
+  const int lane = threadIdx.x & 63;
+  const int blocks = gridDim.x, piece = blockIdx.x;
+  const bool live = lane < batch;
+  const int32_t x = live ? lens[lane] + pending + seg_tokens : 0;
+  const int32_t incl = wave_incl_scan(x);  // P[b + 1]
+  const int32_t N = __shfl(incl, 63);
+  const int32_t chunk = max(kTok, (N + blocks - 1) / blocks);
+  const int32_t v0 = incl - x + seg_tokens, L = x - seg_tokens;
+  const int32_t first = v0 / chunk;
+  const int32_t touched = live && L > 0 ? (v0 + (L - 1) / kTok * kTok) / chunk - first + 1 : 0;
+  const int32_t sb = wave_incl_scan(touched) - touched;
+  if (blockIdx.y == 0 && (threadIdx.x >> 6) == 0 && live && min(first, blocks - 1) == piece)
+    seq_info[lane] = make_int2(sb, touched);
+  const int32_t start = min(piece * chunk, N), end = min(start + chunk, N);
+  auto cut = [&](int32_t c) { return c <= v0 ? 0 : min(L, (c - v0 + kTok - 1) / kTok * kTok); };
+  WavePlan w;
+  w.t0 = cut(start);
+  w.t1 = cut(end);
+  w.slot = sb + (piece - first);
+  w.mask = __ballot(live && incl > start && v0 < end && w.t1 > w.t0);
+  return w;
+}
+
+// One planning round of a block: the segment count; next_seq = the first
+// sequence of the next round (batch when there is none).
+template <int NT>
+__device__ __forceinline__ int32_t plan_segments(const int32_t *__restrict__ lens, int32_t pending,
+                                                 int32_t batch, int32_t &next_seq,
+                                                 int32_t seg_tokens, int32_t *scratch,
+                                                 SegDesc *list, int32_t *meta,
+                                                 int2 *__restrict__ seq_info, WavePlan &wp) {
+  if (batch <= 64) {
+    wp = plan_wave(lens, pending, batch, seg_tokens, seq_info);
+    next_seq = batch;
+    return __builtin_popcountll(wp.mask);
+  }
+  plan_round<NT>(lens, pending, batch, next_seq, seg_tokens, scratch, list, meta, seq_info);
+  next_seq = __builtin_amdgcn_readfirstlane(meta[1]);
+  return __builtin_amdgcn_readfirstlane(meta[0]);
+}
+
+// Segment si of the round (called for si = 0, 1, ... in order).
+__device__ __forceinline__ SegDesc plan_segment(int32_t si, int32_t batch, const SegDesc *list,
+                                                WavePlan &wp) {
+  SegDesc sg;
+  if (batch <= 64) {
+    const int ln = __builtin_ctzll(wp.mask);
+    wp.mask &= wp.mask - 1;
+    sg.seq = ln;
+    sg.t0 = __builtin_amdgcn_readlane(wp.t0, ln);
+    sg.t1 = __builtin_amdgcn_readlane(wp.t1, ln);
+    sg.slot = __builtin_amdgcn_readlane(wp.slot, ln);
+  } else {
+    const SegDesc d = list[si];
+    sg.seq = __builtin_amdgcn_readfirstlane(d.seq);
+    sg.t0 = __builtin_amdgcn_readfirstlane(d.t0);
+    sg.t1 = __builtin_amdgcn_readfirstlane(d.t1);
+    sg.slot = __builtin_amdgcn_readfirstlane(d.slot);
+  }
+  return sg;
+}
+
 // Dynamic LDS of one block: the NSTAGE tile ring, the P^T staging rows,
 // the per-row softmax denominators exchanged at the end of a segment, the
 // per-wave reference-overflow flags and the segment list (+ 2 words).
@@ -711,19 +796,11 @@ __global__ __launch_bounds__(NW * 64) void k_decode_mfma(
 
   int32_t next_seq = 0;
   do {
-  plan_round<NW * 64>(lens, pending, batch, next_seq, seg_tokens, (int32_t *)ring_raw, seg_list, seg_meta,
-                      seq_info);
-  const int32_t nseg = __builtin_amdgcn_readfirstlane(seg_meta[0]);
-  next_seq = __builtin_amdgcn_readfirstlane(seg_meta[1]);
+  WavePlan wp;
+  const int32_t nseg = plan_segments<NW * 64>(lens, pending, batch, next_seq, seg_tokens,
+                                              (int32_t *)ring_raw, seg_list, seg_meta, seq_info, wp);
   for (int32_t si = 0; si < nseg; ++si) {
-    SegDesc sg;
-    {
-      const SegDesc d = seg_list[si];
-      sg.seq = __builtin_amdgcn_readfirstlane(d.seq);
-      sg.t0 = __builtin_amdgcn_readfirstlane(d.t0);
-      sg.t1 = __builtin_amdgcn_readfirstlane(d.t1);
-      sg.slot = __builtin_amdgcn_readfirstlane(d.slot);
-    }
+    const SegDesc sg = plan_segment(si, batch, seg_list, wp);
     const int64_t qrow_c = (int64_t)sg.seq * rows + row_c;
     const uint64_t *prow = pages + (int64_t)sg.seq * pt_width;
     const int T = sg.t1 - sg.t0;
@@ -1090,19 +1167,11 @@ __global__ __launch_bounds__(256) void k_decode_narrow(
 
   int32_t next_seq = 0;
   do {
-  plan_round<NW * 64>(lens, pending, batch, next_seq, seg_tokens, (int32_t *)ring_raw, seg_list, seg_meta,
-                      seq_info);
-  const int32_t nseg = __builtin_amdgcn_readfirstlane(seg_meta[0]);
-  next_seq = __builtin_amdgcn_readfirstlane(seg_meta[1]);
+  WavePlan wp;
+  const int32_t nseg = plan_segments<NW * 64>(lens, pending, batch, next_seq, seg_tokens,
+                                              (int32_t *)ring_raw, seg_list, seg_meta, seq_info, wp);
   for (int32_t si = 0; si < nseg; ++si) {
-    SegDesc sg;
-    {
-      const SegDesc d = seg_list[si];
-      sg.seq = __builtin_amdgcn_readfirstlane(d.seq);
-      sg.t0 = __builtin_amdgcn_readfirstlane(d.t0);
-      sg.t1 = __builtin_amdgcn_readfirstlane(d.t1);
-      sg.slot = __builtin_amdgcn_readfirstlane(d.slot);
-    }
+    const SegDesc sg = plan_segment(si, batch, seg_list, wp);
     const int64_t qrow_c = (int64_t)sg.seq * rows + row_c;
     const uint64_t *prow = pages + (int64_t)sg.seq * pt_width;
     const int T = sg.t1 - sg.t0;

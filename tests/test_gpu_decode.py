@@ -276,3 +276,25 @@ def test_decode_bf16_mixed_lengths_sweep(qmla_gpu, rows_m, q_bf16):
         empty = np.asarray(lens) == 0
         assert np.all(out[empty] == 0) and np.all(np.isneginf(lse[empty]))
         np.testing.assert_allclose(lse[~empty], rlse[~empty], atol=2e-2)
+
+
+@pytest.mark.parametrize("rows_m", [16, 128])
+def test_decode_bf16_large_batch_lds_plan(qmla_gpu, rows_m):
+    """More than 64 sequences: the blocks plan their segments through LDS
+    (up to 64 they plan in registers).  150 ragged sequences with empty ones,
+    the narrow (16 rows) and the 4-wave (128 rows) kernels, two split counts."""
+    q = qmla_gpu
+    lens = O.uniform_int(150, 77, 0, 400).astype(np.int32)
+    lens[::17] = 0
+    cache, rows, offs = make_cache(q, lens, 512, 64, q.BF16, 1300 + rows_m)
+    b = len(lens)
+    ql, qr = O.normal((b, rows_m, 512), 1301), O.normal((b, rows_m, 64), 1302)
+    ref, rlse = O.decode_absorbed(ql, qr, rows, offs, lens, 0.07)
+    empty = lens == 0
+    for splits in (0, 300):
+        out, lse = run(q, cache, ql, qr, 0.07, splits=splits)
+        err = rel_err(out, ref)
+        print(f"batch={b} rows={rows_m} splits={splits} rel_err={err:.2e}", flush=True)
+        assert err < TOL_BF16
+        assert np.all(out[empty] == 0) and np.all(np.isneginf(lse[empty]))
+        np.testing.assert_allclose(lse[~empty], rlse[~empty], atol=2e-2)
