@@ -506,7 +506,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the decode path shards by batch "
-              f"with no exchange, so N GPUs scale the one-GPU number (see DESIGN.md).", file=sys.stderr)
+              f"with no exchange, so N GPUs scale the one-GPU number.", file=sys.stderr)
         sys.exit(2)
 
     dev, cus, arch = qmla.device_info()
