@@ -178,16 +178,6 @@ qmla_status linear(const qmla_layer *L, const float *x, int M, int K, const floa
   return gemm(L, g, 1, true, s);
 }
 
-__device__ inline float block_sum(float v, float *red) {
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-  __syncthreads();
-  if (l == 0) red[w] = v;
-  __syncthreads();
-  float t = 0.f;
-  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) t += red[i];
-  return t;
-}
 
 // Latent rows of new tokens, written straight into the cache (the append of
 // src/model.rs:99-104 fused in): one block per token (latent_rows.hpp).
