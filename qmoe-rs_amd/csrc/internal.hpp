@@ -160,6 +160,8 @@ qmla_status launch_prefill_f32(const qmla_prefill_dims &d, const float *q_nope,
                                const float *q_rope, const float *k, const float *k_rope,
                                const float *v, float scale, int causal, float *out,
                                hipStream_t stream);
+// (dn, dr, dv) combinations the bf16 MFMA prefill takes.
+bool prefill_bf16_supported(int dn, int dr, int dv);
 qmla_status launch_prefill_bf16(const qmla_prefill_dims &d, const uint16_t *q_nope,
                                 const uint16_t *q_rope, const uint16_t *k,
                                 const uint16_t *k_rope, const uint16_t *v, float scale,

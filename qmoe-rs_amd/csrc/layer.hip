@@ -218,62 +218,73 @@ qmla_status latent_to_cache(const qmla_layer *L, const float *kva, int batch, in
   return cache_advance(cache, 0, batch, seq, s);
 }
 
+// Element stores of the prefill operands: f32 as is, or bf16 (round to
+// nearest even) for the bf16 MFMA prefill.
+__device__ __forceinline__ void put(float *p, float v) { *p = v; }
+__device__ __forceinline__ void put(uint16_t *p, float v) { *p = f32_to_bf16_bits(v); }
+__device__ __forceinline__ float get(const float *p) { return *p; }
+__device__ __forceinline__ float get(const uint16_t *p) { return bf16_bits_to_f32(*p); }
+
 // Split q [b*s, H, dn+dr] into q_nope and roped q_rope (src/model.rs:263-267
 // and :199-203); sequence b's token i sits at position lens[b] + i (its
 // cached length before this step's append).  Output layouts by `bhs`:
 //   bhs = 0: q_nope [b, s, H, dn], q_rope [b, s, H, dr]  (decode rows i*H + h)
 //   bhs = 1: q_nope [b, H, s, dn], q_rope [b, H, s, dr]  (prefill layout)
+template <typename OutT>
 __global__ __launch_bounds__(64) void k_split_rope_q(const float *__restrict__ q, int s, int H,
                                                       int dn, int dr,
                                                       const float *__restrict__ inv_freq,
                                                       float mscale,
                                                       const int32_t *__restrict__ lens, int bhs,
-                                                      float *__restrict__ q_nope,
-                                                      float *__restrict__ q_rope) {
+                                                      OutT *__restrict__ q_nope,
+                                                      OutT *__restrict__ q_rope) {
   const int tok = blockIdx.x, h = blockIdx.y;
   const int b = tok / s, i = tok % s;
   const float *src = q + ((int64_t)tok * H + h) * (dn + dr);
   const int64_t o = bhs ? ((int64_t)b * H + h) * s + i : (int64_t)tok * H + h;
-  for (int c = threadIdx.x; c < dn; c += blockDim.x) q_nope[o * dn + c] = src[c];
+  for (int c = threadIdx.x; c < dn; c += blockDim.x) put(q_nope + o * dn + c, src[c]);
   const float pos = (float)(lens[b] + i);
   for (int p = threadIdx.x; p < dr / 2; p += blockDim.x) {
     const float ang = pos * inv_freq[p];
     const float cs = cosf(ang) * mscale, sn = sinf(ang) * mscale;
     const float e = src[dn + 2 * p], od = src[dn + 2 * p + 1];
-    q_rope[o * dr + 2 * p] = e * cs - od * sn;
-    q_rope[o * dr + 2 * p + 1] = od * cs + e * sn;
+    put(q_rope + o * dr + 2 * p, e * cs - od * sn);
+    put(q_rope + o * dr + 2 * p + 1, od * cs + e * sn);
   }
 }
 
 // kvb [b*s, H, dn+dv] -> k [b, H, s, dn], v [b, H, s, dv]  (compute_kv's
 // reshape + transpose, src/model.rs:181-188 and :213-215)
+template <typename OutT>
 __global__ __launch_bounds__(128) void k_split_kv(const float *__restrict__ kvb, int s, int H,
-                                                   int dn, int dv, float *__restrict__ k,
-                                                   float *__restrict__ v) {
+                                                   int dn, int dv, OutT *__restrict__ k,
+                                                   OutT *__restrict__ v) {
   const int tok = blockIdx.x, h = blockIdx.y;
   const int b = tok / s, i = tok % s;
   const float *src = kvb + ((int64_t)tok * H + h) * (dn + dv);
   const int64_t o = ((int64_t)b * H + h) * s + i;
-  for (int c = threadIdx.x; c < dn; c += blockDim.x) k[o * dn + c] = src[c];
-  for (int c = threadIdx.x; c < dv; c += blockDim.x) v[o * dv + c] = src[dn + c];
+  for (int c = threadIdx.x; c < dn; c += blockDim.x) put(k + o * dn + c, src[c]);
+  for (int c = threadIdx.x; c < dv; c += blockDim.x) put(v + o * dv + c, src[dn + c]);
 }
 
 // rows [b*s, r+dr] -> k_rope [b, 1, s, dr]
+template <typename OutT>
 __global__ __launch_bounds__(64) void k_rows_rope(const float *__restrict__ rows, int r, int dr,
-                                                   float *__restrict__ k_rope) {
+                                                   OutT *__restrict__ k_rope) {
   const int tok = blockIdx.x;
   for (int c = threadIdx.x; c < dr; c += blockDim.x)
-    k_rope[(int64_t)tok * dr + c] = rows[(int64_t)tok * (r + dr) + r + c];
+    put(k_rope + (int64_t)tok * dr + c, rows[(int64_t)tok * (r + dr) + r + c]);
 }
 
-// ctx [b, H, s, dv] -> [b, s, H*dv]  (src/model.rs:248)
-__global__ __launch_bounds__(128) void k_merge_heads(const float *__restrict__ ctx, int s, int H,
+// ctx [b, H, s, dv] -> [b, s, H*dv] f32  (src/model.rs:248)
+template <typename InT>
+__global__ __launch_bounds__(128) void k_merge_heads(const InT *__restrict__ ctx, int s, int H,
                                                       int dv, float *__restrict__ o) {
   const int tok = blockIdx.x, h = blockIdx.y;
   const int b = tok / s, i = tok % s;
-  const float *src = ctx + (((int64_t)b * H + h) * s + i) * dv;
+  const InT *src = ctx + (((int64_t)b * H + h) * s + i) * dv;
   float *dst = o + ((int64_t)tok * H + h) * dv;
-  for (int c = threadIdx.x; c < dv; c += blockDim.x) dst[c] = src[c];
+  for (int c = threadIdx.x; c < dv; c += blockDim.x) dst[c] = get(src + c);
 }
 
 // Materialising the reference KVCache (src/model.rs:86-105) from latent rows:
@@ -699,8 +710,9 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
   QMLA_TRY(linear(L, xs, n, g.hidden, L->wq, L->bq, H * (dn + dr), q, s, part, w.part_elems));
   QMLA_TRY(linear(L, xs, n, g.hidden, L->wkva, L->bkva, r + dr, kva, s, part, w.part_elems));
   // q's positions are the lengths before this step's append (src/model.rs:267)
-  k_split_rope_q<<<dim3(n, H), dim3(64), 0, s>>>(q, seq, H, dn, dr, L->inv_freq,
-                                                (float)g.rope_mscale, cache->d_lens, 0, qn, qr);
+  k_split_rope_q<float><<<dim3(n, H), dim3(64), 0, s>>>(q, seq, H, dn, dr, L->inv_freq,
+                                                       (float)g.rope_mscale, cache->d_lens, 0, qn,
+                                                       qr);
   QMLA_LAUNCH_CHECK("k_split_rope_q");
   QMLA_TRY(latent_to_cache(L, kva, batch, seq, nullptr, cache, s));
   // q_lat[t, h, :] = q_nope[t, h, :] W_UK^h   (batched over heads)
@@ -749,8 +761,18 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
 
   QMLA_TRY(linear(L, xs, n, g.hidden, L->wq, L->bq, H * (dn + dr), q, s, part, w.part_elems));
   QMLA_TRY(linear(L, xs, n, g.hidden, L->wkva, L->bkva, r + dr, kva, s, part, w.part_elems));
-  k_split_rope_q<<<dim3(n, H), dim3(64), 0, s>>>(q, seq, H, dn, dr, L->inv_freq,
-                                                (float)g.rope_mscale, cache->d_lens, 1, qn, qr);
+  // With a bf16 cache the attention runs on the bf16 MFMA prefill: q, k, v
+  // and k_rope are written in bf16 (round to nearest even) into the same
+  // regions, and the bf16 context is widened again when the heads merge.
+  // An f32 cache keeps the f32 path throughout.
+  const bool bfa = cache->dtype == QMLA_BF16 && prefill_bf16_supported(dn, dr, dv);
+  if (bfa)
+    k_split_rope_q<uint16_t><<<dim3(n, H), dim3(64), 0, s>>>(
+        q, seq, H, dn, dr, L->inv_freq, (float)g.rope_mscale, cache->d_lens, 1, (uint16_t *)qn,
+        (uint16_t *)qr);
+  else
+    k_split_rope_q<float><<<dim3(n, H), dim3(64), 0, s>>>(
+        q, seq, H, dn, dr, L->inv_freq, (float)g.rope_mscale, cache->d_lens, 1, qn, qr);
   QMLA_LAUNCH_CHECK("k_split_rope_q");
   // the latent replacement of the KVCache returned at src/model.rs:250 (the
   // f32 rows also feed compute_kv below)
@@ -761,15 +783,29 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
                0, 0, 0, 0};
     QMLA_TRY(gemm(L, a, 1, true, s));
   }
-  k_split_kv<<<dim3(n, H), dim3(128), 0, s>>>(kvb, seq, H, dn, dv, k, v);
-  QMLA_LAUNCH_CHECK("k_split_kv");
-  if (dr > 0) {
-    k_rows_rope<<<dim3(n), dim3(64), 0, s>>>(rows, r, dr, kr);
-    QMLA_LAUNCH_CHECK("k_rows_rope");
-  }
   qmla_prefill_dims pd{batch, H, seq, seq, dn, dr, dv, 1, 0};
-  QMLA_TRY(launch_prefill_f32(pd, qn, qr, k, kr, v, (float)g.softmax_scale, 1, ctx, s));
-  k_merge_heads<<<dim3(n, H), dim3(128), 0, s>>>(ctx, seq, H, dv, o);
+  if (bfa) {
+    k_split_kv<uint16_t><<<dim3(n, H), dim3(128), 0, s>>>(kvb, seq, H, dn, dv, (uint16_t *)k,
+                                                         (uint16_t *)v);
+    QMLA_LAUNCH_CHECK("k_split_kv");
+    if (dr > 0) {
+      k_rows_rope<uint16_t><<<dim3(n), dim3(64), 0, s>>>(rows, r, dr, (uint16_t *)kr);
+      QMLA_LAUNCH_CHECK("k_rows_rope");
+    }
+    QMLA_TRY(launch_prefill_bf16(pd, (const uint16_t *)qn, (const uint16_t *)qr,
+                                 (const uint16_t *)k, (const uint16_t *)kr, (const uint16_t *)v,
+                                 (float)g.softmax_scale, 1, (uint16_t *)ctx, s));
+    k_merge_heads<uint16_t><<<dim3(n, H), dim3(128), 0, s>>>((const uint16_t *)ctx, seq, H, dv, o);
+  } else {
+    k_split_kv<float><<<dim3(n, H), dim3(128), 0, s>>>(kvb, seq, H, dn, dv, k, v);
+    QMLA_LAUNCH_CHECK("k_split_kv");
+    if (dr > 0) {
+      k_rows_rope<float><<<dim3(n), dim3(64), 0, s>>>(rows, r, dr, kr);
+      QMLA_LAUNCH_CHECK("k_rows_rope");
+    }
+    QMLA_TRY(launch_prefill_f32(pd, qn, qr, k, kr, v, (float)g.softmax_scale, 1, ctx, s));
+    k_merge_heads<float><<<dim3(n, H), dim3(128), 0, s>>>(ctx, seq, H, dv, o);
+  }
   QMLA_LAUNCH_CHECK("k_merge_heads");
   QMLA_TRY(linear(L, o, n, H * dv, L->wo, L->bo, g.hidden, out, s, part, w.part_elems));
   return QMLA_OK;

@@ -687,6 +687,12 @@ qmla_status launch_prefill_shape(const qmla_prefill_dims &d, const uint16_t *q_n
 
 }  // namespace
 
+bool prefill_bf16_supported(int dn, int dr, int dv) {
+  return (dn == 128 && dr == 64 && dv == 128) || (dn == 32 && dr == 16 && dv == 32) ||
+         (dn == 16 && dr == 16 && dv == 32) || (dn == 32 && dr == 0 && dv == 32) ||
+         (dn == 64 && dr == 64 && dv == 64);
+}
+
 qmla_status launch_prefill_bf16(const qmla_prefill_dims &d, const uint16_t *q_nope,
                                 const uint16_t *q_rope, const uint16_t *k,
                                 const uint16_t *k_rope, const uint16_t *v, float scale,

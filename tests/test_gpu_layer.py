@@ -98,9 +98,9 @@ def test_layer_argument_errors(qmla_gpu):
 ])
 def test_bf16_cache_prefill_then_decode(qmla_gpu, dims):
     """forward_prefill then forward_with_cache steps over a bf16 latent
-    cache: the decode core is the bf16 MFMA kernel; the reference is the
-    oracle's f32 decompressed path on the same weights and inputs
-    (tolerance 2e-2)."""
+    cache: the prefill attention and the decode core are the bf16 MFMA
+    kernels; the reference is the oracle's f32 decompressed path on the same
+    weights and inputs (tolerance 2e-2)."""
     q = qmla_gpu
     hidden, H, dn, dr, dv, r = dims
     w = O.MlaWeights.random(hidden, H, dn, dr, dv, r, seed=900 + r)
@@ -119,6 +119,26 @@ def test_bf16_cache_prefill_then_decode(qmla_gpu, dims):
         print(f"dims={dims} step {step} rel_err={err:.2e}")
         assert err < 2e-2
     assert list(cache.lengths()) == [s + 3] * b
+
+
+def test_bf16_cache_prefill_spans_query_tiles(qmla_gpu):
+    """forward_prefill over a bf16 cache at V2-Lite head shapes with 300
+    tokens per sequence: the attention runs on the bf16 MFMA prefill (q, k, v
+    rounded to bf16) across two 256-row query tiles, the second one partial;
+    the reference is the oracle's f32 path (tolerance 2e-2)."""
+    q = qmla_gpu
+    hidden, H, dn, dr, dv, r = 512, 16, 128, 64, 128, 512
+    w = O.MlaWeights.random(hidden, H, dn, dr, dv, r, seed=1600)
+    layer = q.MlaLayer(w)
+    b, s = 2, 300
+    xs = O.normal((b, s, hidden), 1601)
+    cache = q.KVCache([s] * b, r, dr, q.BF16)
+    out = layer.forward_prefill(xs, cache)
+    ref, _ = O.mla_forward_prefill(w, xs)
+    err = rel_err(out, ref)
+    print(f"prefill b={b} s={s} bf16 cache rel_err={err:.2e}")
+    assert err < 2e-2
+    assert list(cache.lengths()) == [s] * b
 
 
 def _ragged_cache(q, lens, r, dr, dtype, seed, spare=2):
