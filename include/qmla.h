@@ -327,10 +327,19 @@ QMLA_API qmla_status qmla_layer_create(const qmla_layer_config *cfg, const float
                               const float *ln_b, const float *wkvb, const float *bkvb,
                               const float *wo, const float *bo, qmla_layer **out);
 QMLA_API qmla_status qmla_layer_destroy(qmla_layer *layer);
-/* Device scratch needed by the two forward calls for (batch, seq) tokens
- * attending at most max_ctx cached+new tokens. */
+/* Device scratch that serves either forward call below for (batch, seq)
+ * new tokens: the larger of the two calls' needs (their call-specific
+ * regions overlay one another).  No counterpart in the reference, which
+ * allocates per call; the size does not depend on the cached lengths. */
 QMLA_API qmla_status qmla_layer_workspace_bytes(const qmla_layer *layer, const qmla_kv_cache *cache,
                                        int32_t batch, int32_t seq, size_t *bytes);
+/* Device scratch that qmla_layer_forward_prefill alone needs for (batch,
+ * seq) tokens (at most qmla_layer_workspace_bytes; the decode core's
+ * partials, which grow with seq x heads, are not part of it).  No
+ * counterpart in the reference. */
+QMLA_API qmla_status qmla_layer_prefill_workspace_bytes(const qmla_layer *layer,
+                                               const qmla_kv_cache *cache, int32_t batch,
+                                               int32_t seq, size_t *bytes);
 /* MlaAttention::forward_with_cache, src/model.rs:256-307, over the latent
  * cache: xs [batch, seq, hidden] f32 device, out [batch, seq, hidden] f32.
  * Appends the seq new latent rows of sequences 0..batch-1 to the cache and

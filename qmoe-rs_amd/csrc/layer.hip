@@ -413,9 +413,15 @@ struct LayerWs {
   size_t q, kva, rows, qn, qr, qlat, olat, o, dec, kvb, k, v, kr, ctx, part, part_elems, total;
 };
 
-// Scratch carve-up shared by the size query and the two forward calls.
-LayerWs layer_ws(const qmla_layer *L, const qmla_kv_cache *c, int32_t batch, int32_t seq,
-                 size_t dec_bytes) {
+// Which forward call a carve-up serves.  The two calls share the
+// projection regions; the decode-only regions (q_lat, o_lat, the decode
+// core's partials) and the prefill-only ones (LayerNorm'd rows, kv_b_proj
+// output, k, v, k_rope, context) overlay one another, so a workspace sized
+// for both is the larger of the two, not their sum.
+enum class WsFor { kDecode, kPrefill, kBoth };
+
+// Scratch carve-up shared by the size queries and the two forward calls.
+LayerWs layer_ws(const qmla_layer *L, int32_t batch, int32_t seq, size_t dec_bytes, WsFor use) {
   const auto &g = L->cfg;
   const size_t n = (size_t)batch * seq, H = g.heads;
   LayerWs w{};
@@ -427,27 +433,35 @@ LayerWs layer_ws(const qmla_layer *L, const qmla_kv_cache *c, int32_t batch, int
   };
   w.q = take(sizeof(float) * n * H * (g.qk_nope + g.qk_rope));
   w.kva = take(sizeof(float) * n * (g.kv_lora_rank + g.qk_rope));
-  w.rows = take(sizeof(float) * n * (g.kv_lora_rank + g.qk_rope));
   w.qn = take(sizeof(float) * n * H * g.qk_nope);
   w.qr = take(sizeof(float) * n * H * g.qk_rope + 4);
-  w.qlat = take(sizeof(float) * n * H * g.kv_lora_rank);
-  w.olat = take(sizeof(float) * n * H * g.kv_lora_rank);
   // o: [n][H dv] f32, or o_proj's packed B operand of 32 token rows (the
   // same 4 bytes per element, 32 rows at least)
   w.o = take(sizeof(float) * std::max<size_t>(n, 32) * H * g.v_dim);
-  w.dec = take(dec_bytes);
-  w.kvb = take(sizeof(float) * n * H * (g.qk_nope + g.v_dim));
-  w.k = take(sizeof(float) * n * H * g.qk_nope);
-  w.v = take(sizeof(float) * n * H * g.v_dim);
-  w.kr = take(sizeof(float) * n * g.qk_rope + 4);
-  w.ctx = take(sizeof(float) * n * H * g.v_dim);
   // split-K partials of the skinny projections (16 slices at most)
   const size_t widest = std::max<size_t>({(size_t)H * (g.qk_nope + g.qk_rope),
                                           (size_t)(g.kv_lora_rank + g.qk_rope), (size_t)g.hidden});
   w.part_elems = n <= (size_t)kSkinnyRows ? 16 * n * widest : 0;
   w.part = take(sizeof(float) * (w.part_elems ? w.part_elems : 1));
-  w.total = off;
-  (void)c;
+  const size_t shared = off;
+  size_t dec_end = shared, pre_end = shared;
+  if (use != WsFor::kPrefill) {
+    w.qlat = take(sizeof(float) * n * H * g.kv_lora_rank);
+    w.olat = take(sizeof(float) * n * H * g.kv_lora_rank);
+    w.dec = take(dec_bytes);
+    dec_end = off;
+  }
+  if (use != WsFor::kDecode) {
+    off = shared;
+    w.rows = take(sizeof(float) * n * (g.kv_lora_rank + g.qk_rope));
+    w.kvb = take(sizeof(float) * n * H * (g.qk_nope + g.v_dim));
+    w.k = take(sizeof(float) * n * H * g.qk_nope);
+    w.v = take(sizeof(float) * n * H * g.v_dim);
+    w.kr = take(sizeof(float) * n * g.qk_rope + 4);
+    w.ctx = take(sizeof(float) * n * H * g.v_dim);
+    pre_end = off;
+  }
+  w.total = std::max(dec_end, pre_end);
   return w;
 }
 
@@ -492,18 +506,20 @@ size_t materialise_ws_bytes(const qmla_kv_cache *c, int32_t n, int32_t T) {
 
 // Decode workspace for the largest piece count the decode may choose
 // (device CUs x pieces per CU), so the size does not creep up with the
-// context and a caller can size the workspace once per (batch, seq).
+// context and a caller can size the workspace once per (batch, seq).  The
+// cache's dtype fixes the decode path: bf16 partials on the MFMA decode,
+// f32 ones on the f32 decode.
 size_t decode_bytes_for(const qmla_layer *L, const qmla_kv_cache *c, int32_t batch,
                         int32_t seq) {
   int cus = device_cu_count();
   if (cus <= 0) cus = 256;
   const int32_t rows = seq * L->cfg.heads, r = L->cfg.kv_lora_rank, dr = L->cfg.qk_rope;
-  const bool mfma = c->dtype == QMLA_BF16 && decode_mfma_supported(rows, r, dr);
-  const int per_cu = mfma ? decode_mfma_blocks_per_cu(rows, r, dr) : 4;
+  const bool mfma = c->dtype == QMLA_BF16;
+  const int per_cu = mfma && decode_mfma_supported(rows, r, dr)
+                         ? decode_mfma_blocks_per_cu(rows, r, dr)
+                         : 4;
   const int32_t blocks = (int32_t)std::min<int64_t>((int64_t)cus * per_cu, kMaxPlanBlocks);
-  (void)batch;
-  return std::max(decode_workspace_layout(batch, rows, r, blocks, false).total,
-                  decode_workspace_layout(batch, rows, r, blocks, true).total);
+  return decode_workspace_layout(batch, rows, r, blocks, mfma).total;
 }
 
 }  // namespace
@@ -620,7 +636,18 @@ qmla_status qmla_layer_workspace_bytes(const qmla_layer *layer, const qmla_kv_ca
   QMLA_REQUIRE(layer && cache && bytes, QMLA_ERR_INVALID_ARG, "NULL pointer");
   QMLA_REQUIRE(batch > 0 && seq > 0 && batch <= cache->num_seqs, QMLA_ERR_SHAPE,
                "bad batch/seq");
-  *bytes = layer_ws(layer, cache, batch, seq, decode_bytes_for(layer, cache, batch, seq)).total;
+  *bytes = layer_ws(layer, batch, seq, decode_bytes_for(layer, cache, batch, seq), WsFor::kBoth)
+               .total;
+  return QMLA_OK;
+}
+
+qmla_status qmla_layer_prefill_workspace_bytes(const qmla_layer *layer,
+                                               const qmla_kv_cache *cache, int32_t batch,
+                                               int32_t seq, size_t *bytes) {
+  QMLA_REQUIRE(layer && cache && bytes, QMLA_ERR_INVALID_ARG, "NULL pointer");
+  QMLA_REQUIRE(batch > 0 && seq > 0 && batch <= cache->num_seqs, QMLA_ERR_SHAPE,
+               "bad batch/seq");
+  *bytes = layer_ws(layer, batch, seq, 0, WsFor::kPrefill).total;
   return QMLA_OK;
 }
 
@@ -639,7 +666,7 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
   QMLA_REQUIRE((int64_t)seq * H <= 0x7fffffff, QMLA_ERR_SHAPE, "seq x heads too large");
   QMLA_TRY(decode_shape_supported(cache, seq * H));
   const size_t dec_bytes = decode_bytes_for(L, cache, batch, seq);
-  const LayerWs w = layer_ws(L, cache, batch, seq, dec_bytes);
+  const LayerWs w = layer_ws(L, batch, seq, dec_bytes, WsFor::kDecode);
   QMLA_REQUIRE(workspace && workspace_bytes >= w.total, QMLA_ERR_WORKSPACE,
                "workspace of %zu bytes < required %zu", workspace_bytes, w.total);
   QMLA_TRY(make_room(cache, 0, batch, seq, as_stream(stream)));
@@ -746,7 +773,7 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
                  cache->h_lens[i], i);
   const auto &g = L->cfg;
   const int H = g.heads, dn = g.qk_nope, dr = g.qk_rope, dv = g.v_dim, r = g.kv_lora_rank;
-  const LayerWs w = layer_ws(L, cache, batch, seq, decode_bytes_for(L, cache, batch, seq));
+  const LayerWs w = layer_ws(L, batch, seq, 0, WsFor::kPrefill);
   QMLA_REQUIRE(workspace && workspace_bytes >= w.total, QMLA_ERR_WORKSPACE,
                "workspace of %zu bytes < required %zu", workspace_bytes, w.total);
   QMLA_TRY(make_room(cache, 0, batch, seq, as_stream(stream)));

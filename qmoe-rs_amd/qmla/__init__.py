@@ -121,6 +121,7 @@ SIGNATURES = {
     "qmla_layer_create": (_st, [C.POINTER(LayerConfig)] + [_vp] * 10 + [C.POINTER(_vp)]),
     "qmla_layer_destroy": (_st, [_vp]),
     "qmla_layer_workspace_bytes": (_st, [_vp, _vp, _i32, _i32, C.POINTER(_sz)]),
+    "qmla_layer_prefill_workspace_bytes": (_st, [_vp, _vp, _i32, _i32, C.POINTER(_sz)]),
     "qmla_layer_forward_with_cache": (_st, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "qmla_layer_forward_prefill": (_st, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "qmla_cache_materialise_workspace_bytes": (_st, [_vp, _vp, _i32, _i32, C.POINTER(_sz)]),
@@ -486,8 +487,15 @@ class MlaLayer:
         self.hidden = w.hidden
 
     def workspace_bytes(self, cache: KVCache, batch: int, seq: int) -> int:
+        """Scratch that serves either forward call for (batch, seq) tokens."""
         n = C.c_size_t()
         check(lib().qmla_layer_workspace_bytes(self.handle, cache.handle, batch, seq, C.byref(n)))
+        return n.value
+
+    def prefill_workspace_bytes(self, cache: KVCache, batch: int, seq: int) -> int:
+        """Scratch that forward_prefill alone needs for (batch, seq) tokens."""
+        n = C.c_size_t()
+        check(lib().qmla_layer_prefill_workspace_bytes(self.handle, cache.handle, batch, seq, C.byref(n)))
         return n.value
 
     def forward_with_cache(self, xs: np.ndarray, cache: KVCache, stream=None) -> np.ndarray:
@@ -505,7 +513,7 @@ class MlaLayer:
         b, s, _ = xs.shape
         bx = DeviceBuffer.from_numpy(np.ascontiguousarray(xs, np.float32))
         out = DeviceBuffer(b * s * self.hidden * 4)
-        wsb = self.workspace_bytes(cache, b, s)
+        wsb = self.prefill_workspace_bytes(cache, b, s)
         ws = DeviceBuffer(wsb)
         check(lib().qmla_layer_forward_prefill(self.handle, bx.ptr, b, s, cache.handle, out.ptr, ws.ptr,
                                                wsb, _sh(stream)))

@@ -250,6 +250,10 @@ extern "C" {
         layer: *const qmla_layer, cache: *const qmla_kv_cache, batch: i32, seq: i32,
         bytes: *mut usize
     ) -> qmla_status;
+    pub fn qmla_layer_prefill_workspace_bytes(
+        layer: *const qmla_layer, cache: *const qmla_kv_cache, batch: i32, seq: i32,
+        bytes: *mut usize
+    ) -> qmla_status;
     // MlaAttention::forward_with_cache, src/model.rs:256-307
     pub fn qmla_layer_forward_with_cache(
         layer: *const qmla_layer, xs: *const f32, batch: i32, seq: i32,

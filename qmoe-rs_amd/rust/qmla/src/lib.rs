@@ -348,9 +348,19 @@ impl MlaAttention {
         Ok(MlaAttention { raw, config })
     }
 
+    /// Scratch that serves either forward call for (batch, seq) tokens.
     pub fn workspace_bytes(&self, cache: &KVCache, batch: usize, seq: usize) -> Result<usize> {
         let mut n = 0usize;
         ok(unsafe { qmla_layer_workspace_bytes(self.raw, cache.raw, batch as i32, seq as i32, &mut n) })?;
+        Ok(n)
+    }
+
+    /// Scratch that forward_prefill alone needs for (batch, seq) tokens.
+    pub fn prefill_workspace_bytes(&self, cache: &KVCache, batch: usize, seq: usize) -> Result<usize> {
+        let mut n = 0usize;
+        ok(unsafe {
+            qmla_layer_prefill_workspace_bytes(self.raw, cache.raw, batch as i32, seq as i32, &mut n)
+        })?;
         Ok(n)
     }
 

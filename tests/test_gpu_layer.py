@@ -229,6 +229,45 @@ def test_rejected_layer_call_leaves_the_cache_unchanged(qmla_gpu):
     del C
 
 
+def test_prefill_workspace_is_its_own_and_is_enforced(qmla_gpu):
+    """qmla_layer_prefill_workspace_bytes sizes forward_prefill alone: at
+    most the size that serves both calls, and far below it where the decode
+    core's partials (seq x heads rows per piece) dominate.  A workspace one
+    alignment step short is rejected with the cache untouched; the exact
+    size runs and matches the oracle."""
+    q = qmla_gpu
+    hidden, H, dn, dr, dv, r = 512, 16, 128, 64, 128, 512
+    w = O.MlaWeights.random(hidden, H, dn, dr, dv, r, seed=1700)
+    layer = q.MlaLayer(w)
+    big = q.KVCache([2048] * 4, r, dr, q.BF16)
+    pre, both = layer.prefill_workspace_bytes(big, 4, 2048), layer.workspace_bytes(big, 4, 2048)
+    print(f"B4 S2048 workspace: prefill {pre >> 20} MiB, either call {both >> 20} MiB")
+    assert pre < (1 << 30) and pre * 4 < both
+    del big
+    for dt in (q.F32, q.BF16):
+        b, s = 2, 40
+        cache = q.KVCache([s] * b, r, dr, dt)
+        need = layer.prefill_workspace_bytes(cache, b, s)
+        assert need <= layer.workspace_bytes(cache, b, s)
+        xs = O.normal((b, s, hidden), 1701)
+        x = q.DeviceBuffer.from_numpy(xs)
+        out = q.DeviceBuffer(b * s * hidden * 4)
+        ws = q.DeviceBuffer(need)
+        st = q.lib().qmla_layer_forward_prefill(layer.handle, x.ptr, b, s, cache.handle, out.ptr, ws.ptr,
+                                                need - 256, None)
+        assert st == 7
+        assert list(cache.lengths()) == [0] * b
+        st = q.lib().qmla_layer_forward_prefill(layer.handle, x.ptr, b, s, cache.handle, out.ptr, ws.ptr,
+                                                need, None)
+        assert st == 0, q.lib().qmla_last_error()
+        q.check(q.lib().qmla_stream_synchronize(None))
+        ref, _ = O.mla_forward_prefill(w, xs)
+        err = rel_err(out.to_numpy(np.float32, (b, s, hidden)), ref)
+        print(f"dtype {dt} prefill rel_err={err:.2e}")
+        assert err < (TOL if dt == q.F32 else 2e-2)
+        assert list(cache.lengths()) == [s] * b
+
+
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
 def test_materialised_cache_equals_the_reference_kvcache(qmla_gpu, dt):
     """qmla_cache_materialise rebuilds KVCache {k, v, k_rope}
