@@ -95,12 +95,14 @@ def test_layer_argument_errors(qmla_gpu):
     # hidden, heads, qk_nope, qk_rope, v_dim, kv_lora_rank
     (512, 8, 32, 16, 32, 64),      # the tiny CPU-path shape
     (512, 16, 128, 64, 128, 512),  # V2-Lite head shape (hidden reduced)
+    (256, 4, 48, 16, 32, 64),      # head dims the bf16 prefill does not take: f32 attention
 ])
 def test_bf16_cache_prefill_then_decode(qmla_gpu, dims):
     """forward_prefill then forward_with_cache steps over a bf16 latent
     cache: the prefill attention and the decode core are the bf16 MFMA
-    kernels; the reference is the oracle's f32 decompressed path on the same
-    weights and inputs (tolerance 2e-2)."""
+    kernels (the prefill attention stays f32 for head dims the bf16 prefill
+    does not take); the reference is the oracle's f32 decompressed path on
+    the same weights and inputs (tolerance 2e-2)."""
     q = qmla_gpu
     hidden, H, dn, dr, dv, r = dims
     w = O.MlaWeights.random(hidden, H, dn, dr, dv, r, seed=900 + r)
