@@ -67,6 +67,11 @@ namespace qmla {
 inline bool valid_dtype(qmla_dtype d) { return d == QMLA_F32 || d == QMLA_BF16; }
 inline size_t dtype_bytes(qmla_dtype d) { return d == QMLA_BF16 ? 2 : 4; }
 
+// Zeroes `bytes` bytes at dst (any alignment) with a kernel on stream s.
+// Used instead of hipMemsetAsync wherever a caller may capture the call
+// into a HIP graph: a kernel node replays exactly as recorded.
+qmla_status zero_bytes(void *dst, size_t bytes, hipStream_t s);
+
 // ------------------------------------------------------------ decode plan
 // The token range of sequences 0..batch-1 (concatenated, N tokens) is cut
 // into `blocks` contiguous pieces of `chunk` tokens (the last one takes the

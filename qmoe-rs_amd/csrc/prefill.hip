@@ -183,11 +183,10 @@ qmla_status qmla_fused_prefill_attn(const qmla_prefill_dims *dims, qmla_dtype dt
   hipStream_t s = as_stream(stream);
   if (dims->seq_k == 0) {
     // no key at all: every row is empty
-    QMLA_HIP(hipMemsetAsync(out, 0,
-                            (size_t)dims->batch * dims->heads * dims->seq_q * dims->v_dim *
-                                dtype_bytes(dtype),
-                            s));
-    return QMLA_OK;
+    return zero_bytes(out,
+                      (size_t)dims->batch * dims->heads * dims->seq_q * dims->v_dim *
+                          dtype_bytes(dtype),
+                      s);
   }
   if (dtype == QMLA_F32)
     return launch_prefill_f32(*dims, (const float *)q_nope, (const float *)q_rope,

@@ -6,12 +6,13 @@
 // addresses to the attention entry points.
 
 #include <cmath>
+#include <algorithm>
 #include <cstring>
 #include <map>
 #include <mutex>
 #include <vector>
 
-#include "common.hpp"
+#include "internal.hpp"
 
 namespace qmla {
 
@@ -89,6 +90,30 @@ __global__ void k_fill_normal(float *__restrict__ dst, size_t n, uint64_t seed, 
   }
 }
 
+// Zero fill of n bytes at p: the bytes before the first 16-byte boundary
+// and after the last one go one by one, the aligned middle as 16-byte
+// stores, grid-stride.
+__global__ void k_zero_bytes(uint8_t *__restrict__ p, size_t n) {
+  const size_t head = std::min<size_t>(n, (16 - ((uintptr_t)p & 15)) & 15);
+  const size_t nvec = (n - head) / 16;
+  const size_t tail0 = head + nvec * 16;
+  const size_t i0 = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  uint4 *body = reinterpret_cast<uint4 *>(p + head);
+  for (size_t i = i0; i < nvec; i += stride) body[i] = make_uint4(0, 0, 0, 0);
+  if (i0 < head) p[i0] = 0;
+  if (i0 < n - tail0) p[tail0 + i0] = 0;
+}
+
+qmla_status zero_bytes(void *dst, size_t bytes, hipStream_t s) {
+  if (bytes == 0) return QMLA_OK;
+  const size_t nvec = bytes / 16 + 1;
+  const unsigned blocks = (unsigned)std::min<size_t>((nvec + 255) / 256, 4096);
+  k_zero_bytes<<<dim3(blocks), dim3(256), 0, s>>>(static_cast<uint8_t *>(dst), bytes);
+  QMLA_LAUNCH_CHECK("k_zero_bytes");
+  return QMLA_OK;
+}
+
 }  // namespace qmla
 
 using namespace qmla;
@@ -161,8 +186,7 @@ qmla_status qmla_memcpy_d2d(void *dst, const void *src, size_t bytes, qmla_strea
 
 qmla_status qmla_memset_zero(void *dst, size_t bytes, qmla_stream stream) {
   QMLA_REQUIRE(dst, QMLA_ERR_INVALID_ARG, "NULL pointer");
-  if (bytes) QMLA_HIP(hipMemsetAsync(dst, 0, bytes, as_stream(stream)));
-  return QMLA_OK;
+  return zero_bytes(dst, bytes, as_stream(stream));
 }
 
 qmla_status qmla_stream_create(qmla_stream *out) {
