@@ -1,6 +1,6 @@
 """HIP graph capture of the entry points a serving loop replays: the
-absorbed decode (with a workspace and allocation-free), the zero fill and a
-prefill call without keys.  A captured call records kernel nodes only (no
+absorbed decode (with a workspace and allocation-free), the 2-bit MoE layer,
+the zero fill and a prefill call without keys.  A captured call records kernel nodes only (no
 memset or copy nodes), and every replay reproduces the eager result bit for
 bit, with eager work and synchronisations between the replays.
 
@@ -168,3 +168,48 @@ def test_captured_zero_fill_and_keyless_prefill(qmla_gpu):
         assert np.array_equal(buf.to_numpy(np.uint8, (buf.nbytes,)), expect(40 + i)), f"replay {i}"
         assert not pre.to_numpy(np.uint16, (2 * 3 * 5 * 16,)).any(), f"replay {i}"
     g.close()
+
+
+def test_captured_moe_layer_replays_the_eager_result(qmla_gpu):
+    """qmla_moe_forward (routing, the two expert GEMVs, the combine) for 16
+    tokens: kernel nodes only, and each replay reproduces the eager output
+    and routing after they were overwritten."""
+    q = qmla_gpu
+    hip = _hip(q)
+    W = O.random_moe_weights(16, 4, 256, 384, seed=1900)
+    cfg = q.MoEConfig(W.num_experts, W.top_k, W.hidden_dim, W.intermediate_dim)
+    layer = q.QMoELayer(cfg, W.gate_weight, [((W.gate_packed[e], W.gate_scales[e]), (W.up_packed[e], W.up_scales[e]),
+                                              (W.down_packed[e], W.down_scales[e]))
+                                             for e in range(W.num_experts)])
+    T = 16
+    xs = O.normal((T, 256), 1901)
+    bx = q.DeviceBuffer.from_numpy(xs)
+    out = q.DeviceBuffer(T * 256 * 4)
+    ti, tw = q.DeviceBuffer(T * 4 * 4), q.DeviceBuffer(T * 4 * 4)
+    n = layer.workspace_bytes(T)
+    ws = q.DeviceBuffer(n)
+    s = q.Stream()
+
+    def call():
+        layer.forward_device(bx, T, out, ws, n, ti, tw, stream=s.handle)
+
+    def read():
+        return (out.to_numpy(np.float32, (T, 256)), ti.to_numpy(np.int32, (T, 4)), tw.to_numpy(np.float32, (T, 4)))
+
+    call()
+    s.sync()
+    want = read()
+    g = _Graph(hip, s.handle, call)
+    print(f"{len(g.kinds)} nodes, kinds {sorted(set(g.kinds))}", flush=True)
+    assert g.kinds and set(g.kinds) == {_NODE_KERNEL}
+    for i in range(_REPLAYS):
+        for j, b in enumerate((out, ti, tw)):
+            _garbage(b, 60 + 3 * i + j)
+        g.replay()
+        got = read()
+        for a, b in zip(got, want):
+            assert np.array_equal(a, b), f"replay {i}"
+    g.close()
+    ref, ridx, _ = O.moe_forward(W, xs, return_routing=True)
+    np.testing.assert_array_equal(want[1], ridx)
+    assert rel_err(want[0], ref) < 1e-4
