@@ -577,7 +577,7 @@ def main():
             **moe,
             "roofline": {"bound": "hbm", "achieved": moe["tb_s"] * 1e3, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": moe["hbm_frac"], "traffic": measured_traffic("moe_layer_kernel_trace.md"),
-                         "kernel": "whole qmla_moe_forward call (k_moe_route, k_packed_mfma gate/up and down, "
+                         "kernel": "whole qmla_moe_forward call (k_moe_logits, k_packed_mfma gate/up and down, "
                                    "k_moe_combine), HIP events on the launch stream",
                          "bytes_per_launch": moe["bytes_per_step"]},
             "cpu_baseline": None if args.no_cpu_baseline else moe_cpu_baseline()}

@@ -60,6 +60,12 @@ struct PackedArgs {
   const int32_t *slots;     // bin position -> slot (null: identity)
   const int32_t *sel;       // instead of ebin/slots: expert e's bin is the pairs p with
   int32_t npairs;           //   sel[p] == e, ascending (each block reads it itself)
+  const float *logits;      // instead of sel: gate logits [npairs / topk][n_experts]; the
+  int32_t n_experts, topk;  //   block ranks every token's experts itself (table in LDS)
+  int32_t *sel_out;         // with logits: block (0, slice 0) of expert e writes the
+  float *selw_out;          //   routing of e's pairs (expert, softmax weight), and the
+  int32_t *user_idx;        //   caller's copies when non-null
+  float *user_w;
   int32_t count;
   float *out;               // out[slot * ld_out + row]
   int64_t ld_out;
@@ -77,7 +83,7 @@ struct TileInfo {
 // grid y is (expert, slice) and the block walks every slices-th tile of the
 // expert's bin starting at its slice; without, grid y is one tile of the
 // `count` slots.
-__device__ __forceinline__ bool binned(const PackedArgs &a) { return a.ebin || a.sel; }
+__device__ __forceinline__ bool binned(const PackedArgs &a) { return a.ebin || a.sel || a.logits; }
 
 __device__ __forceinline__ int block_expert(const PackedArgs &a) {
   return binned(a) ? (int)blockIdx.y / a.slices : 0;
@@ -117,6 +123,67 @@ __device__ int sel_bin(const int32_t *sel, int np, int e, int t0, int n, int *ou
     for (int p = lo; p < hi && r < t0 + n; ++p)
       if (sel[p] == e) {
         if (r >= t0) out[r - t0] = p;
+        ++r;
+      }
+  }
+  __syncthreads();
+  return total;
+}
+
+constexpr int kRankTokens = 256;  // tokens the GEMV blocks rank themselves (LDS table)
+
+// rank[t] = rank of expert e among token t's E logits lg[t][*]: the number of
+// experts before it in (logit descending, index ascending) order, the
+// reference's stable descending sort (src/moe.rs:51-82); NaN ranks as -inf.
+// T <= kRankTokens; pow2 groups of threads share a token and add their
+// counts with LDS atomics into rank[], which the caller zeroed before a
+// barrier.  Every thread of the block calls it (one barrier).
+__device__ void rank_tokens(const float *lg, int T, int E, int e, int *rank) {
+  const int tid = threadIdx.x;
+  int g = 1;
+  while (g * 2 * T <= kMfmaThreads) g *= 2;
+  const int t = tid / g, part = tid - t * g;
+  if (t < T) {
+    const float *l = lg + t * E;
+    const float v = l[e] != l[e] ? -INFINITY : l[e];
+    int r = 0;
+    for (int j = part; j < E; j += g) {
+      const float u = l[j] != l[j] ? -INFINITY : l[j];
+      r += (u > v) || (u == v && j < e);
+    }
+    if (r) atomicAdd(&rank[t], r);
+  }
+  __syncthreads();
+}
+
+// sel_bin over the token ranks of expert e instead of a routing table: the
+// bin is the pairs t * topk + rank[t] of the tokens with rank[t] < topk,
+// ascending (the order sel_bin gives for the table those ranks make).
+__device__ int rank_bin(const int *rank, int T, int topk, int t0, int n, int *out, int *tmp) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int per = (T + kMfmaThreads - 1) / kMfmaThreads;
+  const int lo = min(T, tid * per), hi = min(T, lo + per);
+  int c = 0;
+  for (int t = lo; t < hi; ++t) c += rank[t] < topk;
+  int incl = c;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(incl, o);
+    if (lane >= o) incl += u;
+  }
+  if (lane == 63) tmp[wave] = incl;
+  __syncthreads();
+  int base = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < kMfmaWaves; ++w) {
+    base += w < wave ? tmp[w] : 0;
+    total += tmp[w];
+  }
+  if (out) {
+    int r = base + incl - c;
+    for (int t = lo; t < hi && r < t0 + n; ++t)
+      if (rank[t] < topk) {
+        if (r >= t0) out[r - t0] = t * topk + rank[t];
         ++r;
       }
   }
@@ -176,6 +243,7 @@ __global__ __launch_bounds__(kMfmaThreads) void k_packed_mfma(PackedArgs a) {
   __shared__ int sel_list[kTokTile];
   __shared__ int sel_tmp[kMfmaWaves];
   __shared__ int32_t sel_lds[kSelLds];
+  __shared__ int rank_lds[kRankTokens];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, h = lane >> 5;
@@ -211,17 +279,58 @@ __global__ __launch_bounds__(kMfmaThreads) void k_packed_mfma(PackedArgs a) {
   }
 
   int first = 0, count;
-  // the routing table, read once (into LDS when it fits)
+  // the routing table, read once (into LDS when it fits); or the logits
+  // (always in LDS: the host takes this path only when they fit)
   const int32_t *bins = a.sel;
-  if (a.sel && a.npairs <= kSelLds) {
+  const float *lg = reinterpret_cast<const float *>(sel_lds);
+  const int ntok_r = a.logits ? a.npairs / a.topk : 0;
+  if (a.logits) {
+    for (int i = tid; i < ntok_r * a.n_experts; i += kMfmaThreads)
+      sel_lds[i] = __float_as_int(a.logits[i]);
+    for (int t = tid; t < ntok_r; t += kMfmaThreads) rank_lds[t] = 0;
+    __syncthreads();
+  } else if (a.sel && a.npairs <= kSelLds) {
     for (int p = tid; p < a.npairs; p += kMfmaThreads) sel_lds[p] = a.sel[p];
     __syncthreads();
     bins = sel_lds;
   }
-  if (a.sel)
+  if (a.logits) {
+    rank_tokens(lg, ntok_r, a.n_experts, expert, rank_lds);
+    count = rank_bin(rank_lds, ntok_r, a.topk, 0, 0, nullptr, sel_tmp);
+  } else if (a.sel) {
     count = sel_bin(bins, a.npairs, expert, 0, 0, nullptr, sel_tmp);
-  else
+  } else {
     block_range(a, first, count);
+  }
+  if (a.sel_out && slice == 0) {
+    // This expert's part of the routing table, for the launches after this
+    // one: (expert, weight) at pair t * topk + rank.  The weight is the
+    // softmax over all experts' logits (src/moe.rs:51-82), one wave per
+    // token with k_moe_route's lane order and reductions; the expert's row
+    // blocks share the tokens (token t: row block t % gridDim.x).
+    const int E = a.n_experts, lane = tid & 63, wave = tid >> 6;
+    for (int t = blockIdx.x + (int)gridDim.x * wave; t < ntok_r;
+         t += (int)gridDim.x * kMfmaWaves) {
+      if (rank_lds[t] >= a.topk) continue;
+      const float *l = lg + t * E;
+      float mx = -INFINITY;
+      for (int j = lane; j < E; j += 64) mx = fmaxf(mx, l[j]);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+      float se = 0.f;
+      for (int j = lane; j < E; j += 64) se += expf(l[j] - mx);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) se += __shfl_xor(se, o);
+      if (lane == 0) {
+        const float w = expf(l[expert] - mx) / se;
+        const int o = t * a.topk + rank_lds[t];
+        a.sel_out[o] = expert;
+        a.selw_out[o] = w;
+        if (a.user_idx) a.user_idx[o] = expert;
+        if (a.user_w) a.user_w[o] = w;
+      }
+    }
+  }
   const int tt0 = slice * kTokTile;
   if (count <= tt0) {  // no tile for this block: drain the requested groups
     wait_vm<0>();
@@ -242,13 +351,16 @@ __global__ __launch_bounds__(kMfmaThreads) void k_packed_mfma(PackedArgs a) {
         ring[d][i] = gload16(wp[i] + (NG > 0 ? d : min(d, ng0 - 1)) * 32);
   }
 
-  if (a.sel) sel_bin(bins, a.npairs, expert, tt, ti.ntok, sel_list, sel_tmp);
+  if (a.logits)
+    rank_bin(rank_lds, ntok_r, a.topk, tt, ti.ntok, sel_list, sel_tmp);
+  else if (a.sel)
+    sel_bin(bins, a.npairs, expert, tt, ti.ntok, sel_list, sel_tmp);
   if (tid < kTokTile) {
     vmax[tid] = 0;
     vsum[tid] = 0;
     if (tid < ti.ntok) {
       const int pos = ti.start + tid;
-      const int slot = a.sel ? sel_list[tid] : a.slots ? a.slots[pos] : pos;
+      const int slot = a.sel || a.logits ? sel_list[tid] : a.slots ? a.slots[pos] : pos;
       const int src = slot / a.src_div;
       vslot[tid] = slot;
       voff[tid] = (int64_t)src * a.ld_x;
@@ -640,6 +752,61 @@ __global__ __launch_bounds__(1024) void k_moe_route(const float *__restrict__ xs
   }
 }
 
+// Gate logits only, one wave per (token, expert): grid (ceil(E / 4), T) of
+// 4 waves, so a token's E gate rows are read by E / 4 CUs rather than one.
+// Each wave's dot product runs the same lane and chunk order as
+// k_moe_route's, so the logits are the same bits.  Wave 0 of block (0, t)
+// also finds the token's largest |x| (f32 bits) for the expert GEMVs.  The
+// GEMV blocks rank the experts themselves (PackedArgs::logits).
+__global__ __launch_bounds__(256) void k_moe_logits(const float *__restrict__ xs,
+                                                    const float *__restrict__ gw, int E, int H,
+                                                    float *__restrict__ logits,
+                                                    uint32_t *__restrict__ xmax) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int e = blockIdx.x * 4 + wave, t = blockIdx.y;
+  if (e >= E) return;
+  const float *x = xs + (int64_t)t * H;
+  const float *w0 = gw + (int64_t)e * H;
+  const bool vec = (H & 3) == 0 && (((uintptr_t)xs | (uintptr_t)gw) & 15) == 0;
+  const bool want_max = blockIdx.x == 0 && wave == 0;
+  uint32_t xm = 0;
+  float s0 = 0.f;
+  if (vec) {
+    const int H4 = H >> 2;
+    constexpr int U = 8;
+    for (int base = 0; base < H4; base += 64 * U) {
+      floatx4_t xv[U], a0[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = min(base + lane + 64 * u, H4 - 1);  // branch-free loads
+        xv[u] = reinterpret_cast<const floatx4_t *>(x)[i];
+        a0[u] = reinterpret_cast<const floatx4_t *>(w0)[i];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (base + lane + 64 * u < H4) {
+          s0 += xv[u][0] * a0[u][0] + xv[u][1] * a0[u][1] + xv[u][2] * a0[u][2] +
+                xv[u][3] * a0[u][3];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) xm = max(xm, __float_as_uint(xv[u][j]) & 0x7fffffffu);
+        }
+    }
+  } else {
+    for (int k = lane; k < H; k += 64) {
+      s0 += x[k] * w0[k];
+      xm = max(xm, __float_as_uint(x[k]) & 0x7fffffffu);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s0 += __shfl_xor(s0, o);
+  if (lane == 0) logits[(int64_t)t * E + e] = s0;
+  if (want_max) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) xm = max(xm, (uint32_t)__shfl_xor((int)xm, o));
+    if (lane == 0) xmax[t] = xm;
+  }
+}
+
 // Exclusive prefix sum over a 1024-thread block (one value per thread).
 __device__ long long block_scan1024(long long v, long long *tmp) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -795,7 +962,7 @@ qmla_status check_packed_dims(int32_t out_f, int32_t in_f, int32_t batch) {
 }
 
 struct MoeWs {
-  size_t sel, selw, ebin, slots, xmax, hmax, h, y, total;
+  size_t sel, selw, ebin, slots, xmax, logits, hmax, h, y, total;
 };
 
 MoeWs moe_ws(const qmla_moe_config &c, int32_t T) {
@@ -813,6 +980,7 @@ MoeWs moe_ws(const qmla_moe_config &c, int32_t T) {
   w.ebin = take(sizeof(int2) * c.num_experts);
   w.slots = take(sizeof(int32_t) * P);
   w.xmax = take(sizeof(uint32_t) * T);
+  w.logits = take(sizeof(float) * T * c.num_experts);
   w.hmax = take(sizeof(uint32_t) * P * mfma_row_blocks(I));
   w.h = take(sizeof(float) * P * I);
   w.y = take(sizeof(float) * P * H);
@@ -926,15 +1094,28 @@ qmla_status qmla_moe_forward(const qmla_moe_config *cfg, const float *xs, int32_
 
   uint32_t *xmax = static_cast<uint32_t *>(at(w.xmax));
   uint32_t *hmax = static_cast<uint32_t *>(at(w.hmax));
-  hipLaunchKernelGGL(k_moe_route, dim3(T), dim3(1024), 0, s, xs, gate_weight, c.num_experts, H,
-                     c.top_k, sel, selw, top_experts, top_weights, xmax);
-  QMLA_LAUNCH_CHECK("k_moe_route");
+  float *logits = static_cast<float *>(at(w.logits));
   const bool fast_gu = mfma_ok(H) && aligned16(gate_packed) && aligned16(up_packed) &&
                        aligned16(xs);
   const bool fast_dn = mfma_ok(I) && aligned16(down_packed) && aligned16(hbuf);
   // The MFMA GEMV blocks read their expert's bin from the routing table
   // themselves; the per-row fallback walks prebuilt bins.
   const bool block_bins = fast_gu && fast_dn;
+  // Decode-sized calls (the logits fit the blocks' LDS table): only the
+  // logits are computed up front, over a wide grid, and the gate/up blocks
+  // rank the experts and write the routing table.  Otherwise one block per
+  // token computes logits, ranks and weights.
+  const bool rank_in_gemv =
+      block_bins && T <= kRankTokens && (int64_t)T * c.num_experts <= kSelLds;
+  if (rank_in_gemv) {
+    hipLaunchKernelGGL(k_moe_logits, dim3((unsigned)((c.num_experts + 3) / 4), (unsigned)T),
+                       dim3(256), 0, s, xs, gate_weight, c.num_experts, H, logits, xmax);
+    QMLA_LAUNCH_CHECK("k_moe_logits");
+  } else {
+    hipLaunchKernelGGL(k_moe_route, dim3(T), dim3(1024), 0, s, xs, gate_weight, c.num_experts, H,
+                       c.top_k, sel, selw, top_experts, top_weights, xmax);
+    QMLA_LAUNCH_CHECK("k_moe_route");
+  }
   if (!block_bins) {
     hipLaunchKernelGGL(k_moe_bin, dim3(1), dim3(1024), 0, s, sel, P, c.num_experts, ebin, slots);
     QMLA_LAUNCH_CHECK("k_moe_bin");
@@ -953,8 +1134,17 @@ qmla_status qmla_moe_forward(const qmla_moe_config *cfg, const float *xs, int32_
   gu.src_div = c.top_k;
   gu.ebin = block_bins ? nullptr : ebin;
   gu.slots = block_bins ? nullptr : slots;
-  gu.sel = block_bins ? sel : nullptr;
+  gu.sel = block_bins && !rank_in_gemv ? sel : nullptr;
   gu.npairs = P;
+  if (rank_in_gemv) {
+    gu.logits = logits;
+    gu.n_experts = c.num_experts;
+    gu.topk = c.top_k;
+    gu.sel_out = sel;
+    gu.selw_out = selw;
+    gu.user_idx = top_experts;
+    gu.user_w = top_weights;
+  }
   gu.out = hbuf;
   gu.ld_out = I;
   gu.src_max = xmax;
@@ -973,6 +1163,13 @@ qmla_status qmla_moe_forward(const qmla_moe_config *cfg, const float *xs, int32_
   QMLA_TRY(launch_packed<2>(gu, (int64_t)c.num_experts * gu.slices, fast_gu, s));
 
   PackedArgs dn = gu;
+  // the down GEMV reads the routing table the gate/up launch completed
+  dn.sel = block_bins ? sel : nullptr;
+  dn.logits = nullptr;
+  dn.sel_out = nullptr;
+  dn.selw_out = nullptr;
+  dn.user_idx = nullptr;
+  dn.user_w = nullptr;
   dn.w[0] = dn.w[1] = down_packed;
   dn.scale[0] = dn.scale[1] = down_scales;
   dn.w_stride = (int64_t)H * (I / 4);

@@ -149,7 +149,9 @@ def check_moe(q, W, xs, label):
     (32, 4, 64, 256, 16),     # reference toy dims: gate/up fallback, down MFMA
     (16, 2, 256, 128, 300),   # many tokens per expert: several tiles a bin
     (6, 6, 128, 100, 4),      # top_k = num_experts; down on the fallback
-    (64, 8, 512, 384, 33)])
+    (64, 8, 512, 384, 33),    # 2112 logits: ranked by the routing kernel
+    (128, 8, 256, 128, 16),   # 2048 logits, 128 experts: ranked in the GEMV blocks
+    (8, 2, 128, 128, 256)])   # 256 tokens, the most the GEMV blocks rank
 def test_moe_forward_matches_oracle(qmla_gpu, E, k, H, I, T):
     W = O.random_moe_weights(E, k, H, I, 1000 + E + H)
     xs = O.normal((T, H), 2000 + T)
