@@ -457,6 +457,57 @@ def cpu_baseline_prefill(min_seconds=5.0):
                       f"(oracle.blas_fused_prefill_attn); unmasked-pair flops as the GPU line"}
 
 
+def cpu_baseline_chunked(heads_sample=8, min_seconds=5.0):
+    """The reference's fused_prefill_attn with the chunk's causal offset
+    (src/attention_kernel.rs:64-107, make_causal_mask :14-31) on the host at
+    the chunked workload's shapes (f32, numpy with BLAS matmuls, per-head
+    decompressed K/V): `heads_sample` heads of one of the 8 sequences,
+    scaled to the 8 x 128 (sequence, head) pairs."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O  # checker library, used here only as the CPU baseline
+
+    h, sq, off = heads_sample, 512, 8192
+    sk = off + sq
+    qn, qr = O.normal((1, h, sq, 128), 81), O.normal((1, h, sq, 64), 82)
+    k, kr, v = O.normal((1, h, sk, 128), 83), O.normal((1, h, sk, 64), 84), O.normal((1, h, sk, 128), 85)
+    per, reps = _repeat(lambda: O.blas_fused_prefill_attn(qn, qr, k, kr, v, SCALE, True, q_offset=off),
+                        min_seconds)
+    pairs = 8 * 128
+    full = per * pairs / h
+    flops = pairs * (sq * off + sq * (sq + 1) // 2) * 2 * (192 + 128)
+    th = blas_threads()
+    return {"value": flops / full / 1e12, "unit": "TFLOP/s", "cores": th, "kind": "port", "cpu_model": cpu_model(),
+            "sample": f"{h} of 1024 (sequence, head) pairs x {reps} runs = {per * reps:.1f} s; scaled by "
+                      f"{pairs // h} ({full:.1f} s per call); the reference's tiled form with the chunk's causal "
+                      f"offset (query tiles of {O.tile_size(sq)}, per-head K/V/k_rope) in numpy on {th} BLAS "
+                      f"threads (oracle.blas_fused_prefill_attn); unmasked-pair flops as the GPU line"}
+
+
+def cpu_baseline_layer(sample_seqs=4, batch=32, ctx=4096, min_seconds=5.0):
+    """MlaAttention::forward_with_cache (src/model.rs:256-307) in the
+    reference's own form on the host: f32 projections, the decompressed
+    per-head cache with KVCache::append's cat, attention and o_proj, numpy
+    with BLAS matmuls (oracle.blas_layer_decode_step, checked against the C
+    oracle's layer).  V2-Lite widths; `sample_seqs` of the `batch` sequences,
+    scaled by sequence count."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O  # checker library, used here only as the CPU baseline
+
+    b = sample_seqs
+    w = O.MlaWeights.random(2048, 16, 128, 64, 128, 512, seed=91)
+    k, v = O.normal((b, 16, ctx, 128), 92), O.normal((b, 16, ctx, 128), 93)
+    kr = O.normal((b, 16, ctx, 64), 94)
+    xs = O.normal((b, 1, 2048), 95)
+    per, reps = _repeat(lambda: O.blas_layer_decode_step(w, xs, k, v, kr), min_seconds)
+    full = per * batch / b
+    th = blas_threads()
+    return {"value": batch / full, "unit": "tok/s", "cores": th, "kind": "port", "cpu_model": cpu_model(),
+            "sample": f"{b} of {batch} sequences x {reps} steps = {per * reps:.1f} s; scaled by sequence count "
+                      f"({full * 1e3:.0f} ms per step); the reference's decompressed form (f32 projections, "
+                      f"per-head K/V/k_rope [b,16,{ctx + 1},d] with the cache cat, attention, o_proj; "
+                      f"src/model.rs:256-307) in numpy on {th} BLAS threads (oracle.blas_layer_decode_step)"}
+
+
 def copy_calibration(stream, n=256 << 20, reps=4):
     """A plain streaming kernel of known traffic for scaling the rocprofv3
     FETCH_SIZE / WRITE_SIZE counters: qmla_f32_to_bf16 over n elements reads
@@ -558,6 +609,8 @@ def main():
         p5 = PrefillBench(8, 128, 512, 8704, 8192, stream, seed=41)
         secondary["chunked_prefill"] = {"workload": "batch 8, 8192 cached + 512 new, 128 heads, bf16, causal in chunk",
                                         **p5.run(args.steps, max(1, args.warmup // 2))}
+        if not args.no_cpu_baseline:
+            secondary["chunked_prefill"]["cpu_baseline"] = cpu_baseline_chunked()
         log("chunked prefill", json.dumps(secondary["chunked_prefill"]))
         del p5
         lb = LayerDecodeBench(stream, seed=51)
@@ -566,6 +619,8 @@ def main():
                         "4096 cached + 1, f32 weights, bf16 latent cache in growth mode (256-row pages "
                         "taken from a pre-sized pool)",
             **lb.run(args.steps, args.warmup)}
+        if not args.no_cpu_baseline:
+            secondary["layer_decode_step"]["cpu_baseline"] = cpu_baseline_layer()
         log("layer decode step", json.dumps(secondary["layer_decode_step"]))
         del lb
         mb = MoEBench(stream)

@@ -305,6 +305,33 @@ def blas_decode_step(q_nope, q_rope, k, v, k_rope, k_new, v_new, k_rope_new, sca
     return np.matmul(_softmax_last(sc).astype(np.float32), v), k, v, k_rope
 
 
+def blas_layer_decode_step(L: "MlaWeights", xs, k, v, k_rope):
+    """MlaAttention::forward_with_cache, src/model.rs:256-307, in its own
+    (decompressed) form with the matmuls on BLAS: q_proj, the nope/rope
+    split and RoPE at positions Tc.. (:263-267); kv_a_proj_with_mqa, the
+    LayerNorm of c and compute_kv for the new tokens, RoPE of k_pe
+    (:270-291); KVCache::append's cat and the attention (blas_decode_step,
+    :291-303); o_proj (:304-306).  xs [b, s, hidden]; k, v, k_rope the
+    per-head cache [b, H, Tc, d].  Returns the output [b, s, hidden]."""
+    xs, k, v, k_rope = map(_c, (xs, k, v, k_rope))
+    b, s, hid = xs.shape
+    H, dn, dr, dv, r = L.heads, L.dn, L.dr, L.dv, L.r
+    Tc = k.shape[2]
+    x2 = xs.reshape(b * s, hid)
+    q = (x2 @ L.wq.T + L.bq).reshape(b, s, H, dn + dr).transpose(0, 2, 1, 3)
+    tab = rope_table(Tc, s, dr, L.rope_mscale)
+    q_nope = np.ascontiguousarray(q[..., :dn])
+    q_pe = apply_rope(q[..., dn:], tab)
+    kva = x2 @ L.wkva.T + L.bkva
+    c = layer_norm(kva[:, :r], L.ln_w, L.ln_b, L.ln_eps)
+    kvb = (c @ L.wkvb.T + L.bkvb).reshape(b, s, H, dn + dv).transpose(0, 2, 1, 3)
+    k_pe = apply_rope(kva[:, r:].reshape(b, 1, s, dr), tab)
+    ctx, _, _, _ = blas_decode_step(q_nope, q_pe, k, v, k_rope, np.ascontiguousarray(kvb[..., :dn]),
+                                    np.ascontiguousarray(kvb[..., dn:]), np.broadcast_to(k_pe, (b, H, s, dr)),
+                                    L.softmax_scale)
+    return (ctx.transpose(0, 2, 1, 3).reshape(b * s, H * dv) @ L.wo.T + L.bo).reshape(b, s, hid)
+
+
 def num_threads() -> int:
     return lib().orc_num_threads()
 

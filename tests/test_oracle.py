@@ -313,3 +313,17 @@ def test_blas_restatements_equal_the_c_oracle():
     assert k2.shape == (b, H, T + s, 32) and np.array_equal(k2[:, :, T:], kn)
     ref = O.fused_prefill_attn(qn, qr, k2, kr2, v2, 0.2, False)
     assert np.abs(ctx - ref).max() <= 2e-5 * np.abs(ref).max()
+
+
+def test_blas_layer_step_matches_the_oracle_layer():
+    """The numpy/BLAS restatement of forward_with_cache (used to time the
+    reference's layer decode step) equals the C oracle's layer on the same
+    weights, cache and new tokens, one and three tokens per sequence."""
+    w = O.MlaWeights.random(256, 4, 32, 16, 24, 64, seed=77)
+    for b, T, s in ((2, 50, 1), (1, 20, 3)):
+        k, v, kr = O.normal((b, 4, T, 32), 80), O.normal((b, 4, T, 24), 81), O.normal((b, 4, T, 16), 82)
+        xs = O.normal((b, s, 256), 83)
+        ref = O.mla_forward_with_cache(w, xs, k, v, kr)
+        got = O.blas_layer_decode_step(w, xs, k, v, kr)
+        assert got.shape == ref.shape
+        assert np.abs(got - ref).max() <= 2e-5 * np.abs(ref).max()
