@@ -36,6 +36,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import math
 import os
@@ -53,6 +54,7 @@ from qmla import synth  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+F32_PEAK_TFLOPS = 157.3    # dense f32 MFMA
 ROW_ELEMS = 576            # kv_lora_rank 512 + rope 64
 ROW_BYTES = ROW_ELEMS * 2  # bf16
 SCALE = 192 ** -0.5
@@ -257,6 +259,100 @@ class LayerDecodeBench:
                 "weight_bytes": self.weight_bytes, "bytes_per_step": hbm, "tb_s": hbm / t / 1e12,
                 "hbm_frac": hbm / t / 1e12 / (HBM_PEAK_GBS / 1e3), "pages_taken": int(pages),
                 "step_ms": dict(STATS)}
+
+
+class LayerPrefillBench:
+    """MlaAttention::forward_prefill (src/model.rs:193-253) at the causal
+    prefill workload's shapes: batch 4 x 2048 tokens, hidden 2048, V2-Lite
+    heads (16, dn 128, dr 64, dv 128, r 512), bf16 latent cache; weights
+    N(0, 0.02^2), activations N(0, 1), seeded.  One call runs the f32
+    projections and the kv_b decompression (compute_kv, :178-190), the bf16
+    MFMA causal attention and o_proj, and fills the cache.  The
+    decompression is also timed on its own, through qmla_cache_materialise
+    over the same 4 x 2048 cached latent rows (the same kv_b_proj product,
+    plus its bf16 -> f32 row conversion and the head-broadcast k_rope
+    copy)."""
+
+    def __init__(self, stream, seed, batch=4, seq=2048, hidden=2048, heads=16):
+        rng = np.random.default_rng(seed)
+        H, dn, dr, dv, r = heads, 128, 64, 128, 512
+
+        def nrm(*shape):
+            return (rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+
+        w = types.SimpleNamespace(hidden=hidden, heads=H, dn=dn, dr=dr, dv=dv, r=r, softmax_scale=None)
+        w.wq, w.bq = nrm(H * (dn + dr), hidden), nrm(H * (dn + dr))
+        w.wkva, w.bkva = nrm(r + dr, hidden), nrm(r + dr)
+        w.ln_w, w.ln_b = (1.0 + nrm(r)).astype(np.float32), nrm(r)
+        w.wkvb, w.bkvb = nrm(H * (dn + dv), r), nrm(H * (dn + dv))
+        w.wo, w.bo = nrm(hidden, H * dv), nrm(hidden)
+        self.layer = qmla.MlaLayer(w)
+        self.batch, self.seq, self.heads, self.hidden, self.stream = batch, seq, H, hidden, stream
+        self.caches = [qmla.KVCache([seq] * batch, r, dr, qmla.BF16) for _ in range(2)]
+        self.xs = qmla.DeviceBuffer(batch * seq * hidden * 4)
+        qmla.check(qmla.lib().qmla_fill_normal_f32(self.xs.ptr, batch * seq * hidden, seed + 2, 0.0, 1.0,
+                                                   qmla._sh(stream)))
+        self.out = qmla.DeviceBuffer(batch * seq * hidden * 4)
+        self.ws_bytes = self.layer.prefill_workspace_bytes(self.caches[0], batch, seq)
+        self.ws = qmla.DeviceBuffer(self.ws_bytes)
+        stream.sync()
+
+    def step(self, i):
+        c = self.caches[i % 2]
+        c.set_lengths([0] * self.batch, self.stream)
+        qmla.check(qmla.lib().qmla_layer_forward_prefill(
+            self.layer.handle, self.xs.ptr, self.batch, self.seq, c.handle, self.out.ptr, self.ws.ptr,
+            self.ws_bytes, qmla._sh(self.stream)))
+
+    def run(self, steps, warmup):
+        b, s, H = self.batch, self.seq, self.heads
+        wall, ev = time_steps(self.step, steps, warmup, self.stream)
+        step_ms = dict(STATS)
+        # the decompression alone, over a cache the steps above filled
+        c = self.caches[0]
+        n = C.c_size_t()
+        qmla.check(qmla.lib().qmla_cache_materialise_workspace_bytes(self.layer.handle, c.handle, 0, b,
+                                                                     C.byref(n)))
+        k, v = qmla.DeviceBuffer(b * H * s * 128 * 4), qmla.DeviceBuffer(b * H * s * 128 * 4)
+        kr = qmla.DeviceBuffer(b * H * s * 64 * 4)
+        mws = qmla.DeviceBuffer(max(n.value, 1))
+
+        def mstep(i):
+            qmla.check(qmla.lib().qmla_cache_materialise(self.layer.handle, c.handle, 0, b, k.ptr, v.ptr, kr.ptr,
+                                                         mws.ptr, n.value, qmla._sh(self.stream)))
+
+        _, evm = time_steps(mstep, steps, 2, self.stream)
+        att = b * H * (s * (s + 1) // 2) * 2 * (192 + 128)
+        kvb = 2 * b * s * 512 * H * (128 + 128)
+        proj = 2 * b * s * self.hidden * (H * 192 + 576 + H * 128)
+        return {"tok_s": b * s / (ev * 1e-3), "ms_per_step": ev, "wall_ms_per_step": wall,
+                "gflop": {"attention": att / 1e9, "kv_b_decompress": kvb / 1e9, "projections": proj / 1e9},
+                "step_ms": step_ms,
+                "decompress": {"ms": evm, "gflop": kvb / 1e9, "tflops": kvb / (evm * 1e-3) / 1e12,
+                               "f32_mfma_frac": kvb / (evm * 1e-3) / 1e12 / F32_PEAK_TFLOPS,
+                               "what": "qmla_cache_materialise over the 4 x 2048 cached rows: the kv_b_proj "
+                                       "GEMM (rocBLAS f32) plus the bf16 -> f32 row conversion and the "
+                                       "head-broadcast k_rope copy"}}
+
+
+def cpu_baseline_layer_prefill(min_seconds=5.0):
+    """MlaAttention::forward_prefill (src/model.rs:193-253) in the
+    reference's own form on the host (numpy with BLAS matmuls,
+    oracle.blas_layer_prefill, checked against the C oracle's layer): one of
+    the 4 sequences of 2048 tokens, scaled by 4."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O  # checker library, used here only as the CPU baseline
+
+    w = O.MlaWeights.random(2048, 16, 128, 64, 128, 512, seed=96)
+    xs = O.normal((1, 2048, 2048), 97)
+    per, reps = _repeat(lambda: O.blas_layer_prefill(w, xs), min_seconds)
+    full = per * 4
+    th = blas_threads()
+    return {"value": 4 * 2048 / full, "unit": "tok/s", "cores": th, "kind": "port", "cpu_model": cpu_model(),
+            "sample": f"1 of 4 sequences (2048 tokens) x {reps} runs = {per * reps:.1f} s; scaled by 4 "
+                      f"({full * 1e3:.0f} ms per call); the reference's form (f32 projections, compute_kv, "
+                      f"tiled causal attention over per-head K/V, o_proj; src/model.rs:193-253) in numpy on "
+                      f"{th} BLAS threads (oracle.blas_layer_prefill)"}
 
 
 def ref_bench_packed(out_f: int, in_f: int):
@@ -623,6 +719,15 @@ def main():
             secondary["layer_decode_step"]["cpu_baseline"] = cpu_baseline_layer()
         log("layer decode step", json.dumps(secondary["layer_decode_step"]))
         del lb
+        lp = LayerPrefillBench(stream, seed=61)
+        secondary["layer_prefill"] = {
+            "workload": "MlaAttention forward_prefill, batch 4 x 2048 tokens, hidden 2048, 16 heads, r 512, "
+                        "f32 weights, bf16 latent cache (attention on the bf16 MFMA prefill)",
+            **lp.run(max(3, args.steps // 5), 3)}
+        if not args.no_cpu_baseline:
+            secondary["layer_prefill"]["cpu_baseline"] = cpu_baseline_layer_prefill()
+        log("layer prefill", json.dumps(secondary["layer_prefill"]))
+        del lp
         mb = MoEBench(stream)
         moe = mb.run(args.steps, args.warmup)
         del mb

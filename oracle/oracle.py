@@ -332,6 +332,30 @@ def blas_layer_decode_step(L: "MlaWeights", xs, k, v, k_rope):
     return (ctx.transpose(0, 2, 1, 3).reshape(b * s, H * dv) @ L.wo.T + L.bo).reshape(b, s, hid)
 
 
+def blas_layer_prefill(L: "MlaWeights", xs):
+    """MlaAttention::forward_prefill, src/model.rs:193-253, in its own form
+    with the matmuls on BLAS: q_proj, the nope/rope split and RoPE at
+    positions 0.. (:197-204); kv_a_proj_with_mqa, the LayerNorm of c, RoPE
+    of k_pe and compute_kv (:206-219, :178-190); the tiled causal
+    fused_prefill_attn (blas_fused_prefill_attn, :221-244); o_proj
+    (:246-249).  xs [b, s, hidden].  Returns the output [b, s, hidden]."""
+    xs = _c(xs)
+    b, s, hid = xs.shape
+    H, dn, dr, dv, r = L.heads, L.dn, L.dr, L.dv, L.r
+    x2 = xs.reshape(b * s, hid)
+    q = (x2 @ L.wq.T + L.bq).reshape(b, s, H, dn + dr).transpose(0, 2, 1, 3)
+    tab = rope_table(0, s, dr, L.rope_mscale)
+    q_nope = np.ascontiguousarray(q[..., :dn])
+    q_pe = apply_rope(q[..., dn:], tab)
+    kva = x2 @ L.wkva.T + L.bkva
+    c = layer_norm(kva[:, :r], L.ln_w, L.ln_b, L.ln_eps)
+    k_pe = apply_rope(kva[:, r:].reshape(b, 1, s, dr), tab)
+    kvb = (c @ L.wkvb.T + L.bkvb).reshape(b, s, H, dn + dv).transpose(0, 2, 1, 3)
+    ctx = blas_fused_prefill_attn(q_nope, q_pe, np.ascontiguousarray(kvb[..., :dn]), k_pe,
+                                  np.ascontiguousarray(kvb[..., dn:]), L.softmax_scale, True)
+    return (ctx.transpose(0, 2, 1, 3).reshape(b * s, H * dv) @ L.wo.T + L.bo).reshape(b, s, hid)
+
+
 def num_threads() -> int:
     return lib().orc_num_threads()
 

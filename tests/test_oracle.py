@@ -315,6 +315,18 @@ def test_blas_restatements_equal_the_c_oracle():
     assert np.abs(ctx - ref).max() <= 2e-5 * np.abs(ref).max()
 
 
+def test_blas_layer_prefill_matches_the_oracle_layer():
+    """The numpy/BLAS restatement of forward_prefill (used to time the
+    reference's layer prefill) equals the C oracle's layer prefill."""
+    w = O.MlaWeights.random(256, 4, 32, 16, 24, 64, seed=78)
+    for b, s in ((2, 37), (1, 70)):
+        xs = O.normal((b, s, 256), 84)
+        ref, _ = O.mla_forward_prefill(w, xs)
+        got = O.blas_layer_prefill(w, xs)
+        assert got.shape == ref.shape
+        assert np.abs(got - ref).max() <= 2e-5 * np.abs(ref).max()
+
+
 def test_blas_layer_step_matches_the_oracle_layer():
     """The numpy/BLAS restatement of forward_with_cache (used to time the
     reference's layer decode step) equals the C oracle's layer on the same
