@@ -265,13 +265,13 @@ class LayerPrefillBench:
     """MlaAttention::forward_prefill (src/model.rs:193-253) at the causal
     prefill workload's shapes: batch 4 x 2048 tokens, hidden 2048, V2-Lite
     heads (16, dn 128, dr 64, dv 128, r 512), bf16 latent cache; weights
-    N(0, 0.02^2), activations N(0, 1), seeded.  One call runs the f32
-    projections and the kv_b decompression (compute_kv, :178-190), the bf16
-    MFMA causal attention and o_proj, and fills the cache.  The
-    decompression is also timed on its own, through qmla_cache_materialise
-    over the same 4 x 2048 cached latent rows (the same kv_b_proj product,
-    plus its bf16 -> f32 row conversion and the head-broadcast k_rope
-    copy)."""
+    N(0, 0.02^2), activations N(0, 1), seeded.  One call runs the
+    projections and the kv_b decompression (compute_kv, :178-190) as split
+    bf16 GEMMs with f32 accumulation, the bf16 MFMA causal attention and
+    o_proj, and fills the cache.  The decompression is also timed on its
+    own, through qmla_cache_materialise over the same 4 x 2048 cached latent
+    rows (the kv_b_proj product batched over heads, plus the gather of the
+    rows and the head-broadcast k_rope copy)."""
 
     def __init__(self, stream, seed, batch=4, seq=2048, hidden=2048, heads=16):
         rng = np.random.default_rng(seed)
@@ -331,7 +331,8 @@ class LayerPrefillBench:
                 "decompress": {"ms": evm, "gflop": kvb / 1e9, "tflops": kvb / (evm * 1e-3) / 1e12,
                                "f32_mfma_frac": kvb / (evm * 1e-3) / 1e12 / F32_PEAK_TFLOPS,
                                "what": "qmla_cache_materialise over the 4 x 2048 cached rows: the kv_b_proj "
-                                       "GEMM (rocBLAS f32) plus the bf16 -> f32 row conversion and the "
+                                       "product as split bf16 GEMMs (rocBLAS, f32 accumulation, batched over "
+                                       "heads) plus the gather of the rows into split form and the "
                                        "head-broadcast k_rope copy"}}
 
 
@@ -722,7 +723,8 @@ def main():
         lp = LayerPrefillBench(stream, seed=61)
         secondary["layer_prefill"] = {
             "workload": "MlaAttention forward_prefill, batch 4 x 2048 tokens, hidden 2048, 16 heads, r 512, "
-                        "f32 weights, bf16 latent cache (attention on the bf16 MFMA prefill)",
+                        "f32 weights (projections as split bf16 GEMMs, f32 accumulation), bf16 latent cache "
+                        "(attention on the bf16 MFMA prefill)",
             **lp.run(max(3, args.steps // 5), 3)}
         if not args.no_cpu_baseline:
             secondary["layer_prefill"]["cpu_baseline"] = cpu_baseline_layer_prefill()

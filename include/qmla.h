@@ -375,8 +375,11 @@ QMLA_API qmla_status qmla_layer_forward_prefill(const qmla_layer *layer, const f
  * for sequences seq0 .. seq0 + n_seqs - 1, which must share one length T
  * (a KVCache tensor has one T; materialise a ragged cache one sequence at a
  * time).  f32 device outputs; any of k, v, k_rope may be NULL to skip it.
- * A bf16 cache needs a workspace of n_seqs * T * kv_lora_rank floats for
- * the widened latent (the size query says so; an f32 cache needs none).
+ * The latent rows are gathered into a workspace whose size the query
+ * gives: n_seqs * T * kv_lora_rank floats, or, for T >= 256, the rows in
+ * the split form of the bf16 GEMMs that then compute k and v (about
+ * 3 kv_lora_rank bf16 per row; x w as x_hi w_hi + x_lo w_hi + x_hi w_lo with
+ * f32 accumulation, within the f32 tolerance).
  * The writes are O(T * H * (dn + dv + dr)) per sequence: this is the
  * legacy path for callers that read the decompressed tensors, not the
  * decode path. */

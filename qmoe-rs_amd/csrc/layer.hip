@@ -46,6 +46,11 @@ struct qmla_layer {
   float *b1 = nullptr;   // [bq | bkva]
   float *buv = nullptr;  // [H][dv]: b_V^h
   bool skinny = false;   // the split weights exist (every K a multiple of 16)
+  // Split-form rows of wq, wkva, wkvb and wo for the GEMMs of products with
+  // many rows: row n of a [N][K] weight becomes [w_hi | w_hi | w_lo | b_hi,
+  // b_lo, 0...] in bf16 (split_cols(K) columns; hi = bf16(v), lo = bf16(v -
+  // hi); the bias columns are 0 without a bias).
+  uint16_t *wq_x = nullptr, *wkva_x = nullptr, *wkvb_x = nullptr, *wo_x = nullptr;
   std::vector<void *> allocs;
   // rocBLAS handles for the GEMM path (prefill, and decode shapes the skinny
   // kernel does not take).  A call takes a free one and sets its stream, so
@@ -179,6 +184,108 @@ qmla_status linear(const qmla_layer *L, const float *x, int M, int K, const floa
 }
 
 
+// ------------------------------------------------------- split bf16 GEMM
+// A product with many rows runs on bf16 GEMMs with f32 accumulation instead
+// of an f32 GEMM:  x w = x_hi w_hi + x_lo w_hi + x_hi w_lo, with hi =
+// bf16(v) (round to nearest even) and lo = bf16(v - hi) for both operands.
+// The dropped x_lo w_lo and the bits past lo keep ~2^-16 of each product,
+// the same f32-exact form as the skinny decode-step GEMM.  The three
+// products and the bias are one GEMM over K' = split_cols(K) columns:
+//   x' = [x_hi | x_lo | x_hi | 1, 1, 0...],  w' = [w_hi | w_hi | w_lo | b_hi, b_lo, 0...]
+// so the output is written once.  On this part bf16 GEMMs run ~5-10x
+// faster than f32 ones at prefill sizes.
+constexpr int kSplitRows = 256;  // products with at least this many rows split
+
+// 3K columns of halves, the two bias columns, zeros up to a multiple of 64
+// (the GEMM kernels' K tile).
+__host__ __device__ inline int split_cols(int K) { return (3 * K + 2 + 63) / 64 * 64; }
+
+// x'[m] (split_cols(K) bf16 per row, contiguous) from x[m * ldx + k].
+__global__ __launch_bounds__(256) void k_split_rows(const float *__restrict__ x, int64_t ldx,
+                                                    int64_t M, int K, uint16_t *__restrict__ xs) {
+  const int KX = split_cols(K);
+  const int64_t n = M * K;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t m = i / K, k = i - m * K;
+    const float v = x[m * ldx + k];
+    const uint16_t h = f32_to_bf16_bits(v);
+    uint16_t *row = xs + m * KX;
+    row[k] = h;
+    row[K + k] = f32_to_bf16_bits(v - bf16_bits_to_f32(h));
+    row[2 * K + k] = h;
+    if (k < KX - 3 * K) row[3 * K + k] = k < 2 ? (uint16_t)0x3f80 : (uint16_t)0;  // 1.0, 1.0, 0...
+  }
+}
+
+// Bytes of scratch the split of an [M][K] activation needs.
+inline size_t split_bytes(int64_t M, int64_t K) {
+  return (size_t)M * split_cols((int)K) * sizeof(uint16_t);
+}
+
+qmla_status split_act(const float *x, int64_t ldx, int M, int K, void *xs, hipStream_t s) {
+  const int64_t n = (int64_t)M * K;
+  if (n == 0) return QMLA_OK;
+  const unsigned blocks = (unsigned)std::min<int64_t>((n + 255) / 256, 16384);
+  k_split_rows<<<dim3(blocks), dim3(256), 0, s>>>(x, ldx, M, K, static_cast<uint16_t *>(xs));
+  QMLA_LAUNCH_CHECK("k_split_rows");
+  return QMLA_OK;
+}
+
+// A free rocBLAS handle of the layer (or this thread's, when all are busy),
+// locked for the caller.
+qmla_layer::BlasSlot *take_blas(const qmla_layer *L, std::unique_lock<std::mutex> &lock) {
+  for (auto &bs : L->blas) {
+    std::unique_lock<std::mutex> l(bs.mu, std::try_to_lock);
+    if (l.owns_lock()) {
+      lock = std::move(l);
+      return &bs;
+    }
+  }
+  auto *slot = &L->blas[std::hash<std::thread::id>{}(std::this_thread::get_id()) %
+                        qmla_layer::kBlasHandles];
+  lock = std::unique_lock<std::mutex>(slot->mu);
+  return slot;
+}
+
+// C[z][m][n] = x'[z][m] . w'[z][n] (the split product with its bias), all
+// row-major: x' [M][K'] per z at stride sX, w' [N][K'] per z at stride sW
+// (ld ldw), C [M][N] (ld ldc) at stride sC, K' = split_cols(K).
+qmla_status gemm_split(const qmla_layer *L, const uint16_t *xs, int64_t sX, int M, int K,
+                       const uint16_t *wx, int64_t ldw, int64_t sW, int N, float *C, int64_t ldc,
+                       int64_t sC, int batch, hipStream_t s) {
+  if (M == 0 || N == 0) return QMLA_OK;
+  QMLA_REQUIRE(batch >= 1 && batch <= 65535, QMLA_ERR_SHAPE, "GEMM batch %d", batch);
+  const int KX = split_cols(K);
+  std::unique_lock<std::mutex> lock;
+  qmla_layer::BlasSlot *slot = take_blas(L, lock);
+  rocblas_status st = rocblas_set_stream(slot->h, s);
+  const float one = 1.f, zero = 0.f;
+  // row-major C = x' w'^T is column-major C^T = w' x'^T: (m, n, k) = (N, M, K')
+  if (st == rocblas_status_success)
+    st = rocblas_gemm_strided_batched_ex(
+        slot->h, rocblas_operation_transpose, rocblas_operation_none, N, M, KX, &one, wx,
+        rocblas_datatype_bf16_r, (rocblas_int)ldw, sW, xs, rocblas_datatype_bf16_r, KX, sX,
+        &zero, C, rocblas_datatype_f32_r, (rocblas_int)ldc, sC, C, rocblas_datatype_f32_r,
+        (rocblas_int)ldc, sC, batch, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+  QMLA_REQUIRE(st == rocblas_status_success, QMLA_ERR_HIP, "rocBLAS gemm_ex: %s",
+               rocblas_status_to_string(st));
+  return QMLA_OK;
+}
+
+// y = x W^T + b: the split form for many rows when the split weight exists
+// (x' already in xs when `split` is false), else linear().
+qmla_status project(const qmla_layer *L, const float *x, int M, int K, const float *W,
+                    const uint16_t *Wx, const float *b, int N, float *y, hipStream_t s,
+                    float *part, size_t part_elems, void *xs, bool split = true) {
+  if (M >= kSplitRows && K >= 64 && Wx && xs) {
+    if (split) QMLA_TRY(split_act(x, K, M, K, xs, s));
+    return gemm_split(L, static_cast<const uint16_t *>(xs), 0, M, K, Wx, split_cols(K), 0, N, y,
+                      N, 0, 1, s);
+  }
+  return linear(L, x, M, K, W, b, N, y, s, part, part_elems);
+}
+
 // Latent rows of new tokens, written straight into the cache (the append of
 // src/model.rs:99-104 fused in): one block per token (latent_rows.hpp).
 __global__ __launch_bounds__(256) void k_latent_rows(LatentRowsArgs a) {
@@ -305,6 +412,31 @@ __global__ __launch_bounds__(256) void k_latent_c_f32(PageTable tab, int seq0, i
   }
 }
 
+// The c_kv part of the cache rows in split form ([n, T] rows of
+// split_cols(r) bf16: [c_hi | c_lo | c_hi | 1, 1, 0...]), the activations
+// of the split kv_b_proj GEMMs.
+template <typename SrcT>
+__global__ __launch_bounds__(256) void k_latent_c_split(PageTable tab, int seq0, int T, int r,
+                                                        int dr, uint16_t *__restrict__ xs) {
+  const int t = blockIdx.x, b = blockIdx.y;
+  const SrcT *src =
+      reinterpret_cast<const SrcT *>(tab.row(seq0 + b, t, (int64_t)(r + dr) * sizeof(SrcT)));
+  uint16_t *row = xs + ((int64_t)b * T + t) * split_cols(r);
+  for (int c = threadIdx.x; c < r; c += blockDim.x) {
+    float x;
+    if constexpr (sizeof(SrcT) == 2)
+      x = bf16_bits_to_f32(src[c]);
+    else
+      x = src[c];
+    const uint16_t h = f32_to_bf16_bits(x);
+    row[c] = h;
+    row[r + c] = f32_to_bf16_bits(x - bf16_bits_to_f32(h));
+    row[2 * r + c] = h;
+  }
+  for (int c = threadIdx.x; c < split_cols(r) - 3 * r; c += blockDim.x)
+    row[3 * r + c] = c < 2 ? (uint16_t)0x3f80 : (uint16_t)0;
+}
+
 // k_rope [n, H, T, dr]: the stored (roped) k_pe of each token broadcast to
 // every head, as the reference's expand at src/model.rs:217-219 / :281-285.
 template <typename SrcT>
@@ -410,7 +542,8 @@ SkinnyGemmArgs skinny_args(const void *w_frag, const float *x, int64_t ldx, int6
 inline size_t al(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct LayerWs {
-  size_t q, kva, rows, qn, qr, qlat, olat, o, dec, kvb, k, v, kr, ctx, part, part_elems, total;
+  size_t q, kva, rows, qn, qr, qlat, olat, o, dec, kvb, k, v, kr, ctx, part, part_elems, xsplit,
+      total;
 };
 
 // Which forward call a carve-up serves.  The two calls share the
@@ -443,6 +576,9 @@ LayerWs layer_ws(const qmla_layer *L, int32_t batch, int32_t seq, size_t dec_byt
                                           (size_t)(g.kv_lora_rank + g.qk_rope), (size_t)g.hidden});
   w.part_elems = n <= (size_t)kSkinnyRows ? 16 * n * widest : 0;
   w.part = take(sizeof(float) * (w.part_elems ? w.part_elems : 1));
+  // bf16 halves of a projection's activations (split GEMMs, many rows)
+  const size_t kmax = std::max<size_t>({(size_t)g.hidden, H * g.v_dim, (size_t)g.kv_lora_rank});
+  w.xsplit = take(n >= (size_t)kSplitRows ? split_bytes((int64_t)n, (int64_t)kmax) : 1);
   const size_t shared = off;
   size_t dec_end = shared, pre_end = shared;
   if (use != WsFor::kPrefill) {
@@ -500,7 +636,12 @@ qmla_status check_materialise(const qmla_layer *L, const qmla_kv_cache *c, int32
   return QMLA_OK;
 }
 
-size_t materialise_ws_bytes(const qmla_kv_cache *c, int32_t n, int32_t T) {
+// Whether materialise runs compute_kv in split form (sequences of many
+// tokens), and its scratch: the c_kv rows as f32 or in split form.
+bool materialise_split(const qmla_layer *L, int32_t T) { return T >= kSplitRows && L->wkvb_x; }
+
+size_t materialise_ws_bytes(const qmla_layer *L, const qmla_kv_cache *c, int32_t n, int32_t T) {
+  if (materialise_split(L, T)) return split_bytes((int64_t)n * T, c->r);
   return sizeof(float) * (size_t)n * T * c->r;
 }
 
@@ -608,6 +749,51 @@ qmla_status qmla_layer_create(const qmla_layer_config *cfg, const float *wq, con
       st = fail(QMLA_ERR_HIP, "inv_freq upload failed");
     if (p) L->allocs.push_back(p);
     L->inv_freq = static_cast<float *>(p);
+  }
+  if (st == QMLA_OK) {
+    // split-form rows of the four projections (with their biases)
+    struct Half {
+      uint16_t **dst;
+      const float *w, *b;
+      int N, K;
+    } hs[] = {
+        {&L->wq_x, wq, bq, H * (g.qk_nope + g.qk_rope), g.hidden},
+        {&L->wkva_x, wkva, bkva, g.kv_lora_rank + g.qk_rope, g.hidden},
+        {&L->wkvb_x, wkvb, bkvb, H * (g.qk_nope + g.v_dim), g.kv_lora_rank},
+        {&L->wo_x, wo, bo, g.hidden, H * g.v_dim},
+    };
+    std::vector<uint16_t> hl;
+    for (auto &h : hs) {
+      const int KX = split_cols(h.K);
+      hl.assign((size_t)h.N * KX, 0);
+      for (int n = 0; n < h.N; ++n) {
+        uint16_t *row = hl.data() + (size_t)n * KX;
+        for (int k = 0; k < h.K; ++k) {
+          const float v = h.w[(size_t)n * h.K + k];
+          const uint16_t hi = f32_to_bf16_bits(v);
+          row[k] = hi;
+          row[h.K + k] = hi;
+          row[2 * h.K + k] = f32_to_bf16_bits(v - bf16_bits_to_f32(hi));
+        }
+        if (h.b) {
+          const uint16_t bh = f32_to_bf16_bits(h.b[n]);
+          row[3 * h.K] = bh;
+          row[3 * h.K + 1] = f32_to_bf16_bits(h.b[n] - bf16_bits_to_f32(bh));
+        }
+      }
+      void *p = nullptr;
+      if (hipMalloc(&p, hl.size() * sizeof(uint16_t)) != hipSuccess) {
+        st = fail(QMLA_ERR_OOM, "weight allocation failed");
+        break;
+      }
+      L->allocs.push_back(p);
+      if (hipMemcpy(p, hl.data(), hl.size() * sizeof(uint16_t), hipMemcpyHostToDevice) !=
+          hipSuccess) {
+        st = fail(QMLA_ERR_HIP, "weight upload failed");
+        break;
+      }
+      *h.dst = static_cast<uint16_t *>(p);
+    }
   }
   if (st == QMLA_OK && g.hidden % 16 == 0 && g.qk_nope % 16 == 0 && g.kv_lora_rank % 16 == 0 &&
       (g.heads * g.v_dim) % 16 == 0)
@@ -734,8 +920,12 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
     return QMLA_OK;
   }
 
-  QMLA_TRY(linear(L, xs, n, g.hidden, L->wq, L->bq, H * (dn + dr), q, s, part, w.part_elems));
-  QMLA_TRY(linear(L, xs, n, g.hidden, L->wkva, L->bkva, r + dr, kva, s, part, w.part_elems));
+  void *xsp = ws + w.xsplit;
+  // q_proj and kv_a_proj_with_mqa share one split of xs
+  QMLA_TRY(project(L, xs, n, g.hidden, L->wq, L->wq_x, L->bq, H * (dn + dr), q, s, part,
+                   w.part_elems, xsp));
+  QMLA_TRY(project(L, xs, n, g.hidden, L->wkva, L->wkva_x, L->bkva, r + dr, kva, s, part,
+                   w.part_elems, xsp, false));
   // q's positions are the lengths before this step's append (src/model.rs:267)
   k_split_rope_q<float><<<dim3(n, H), dim3(64), 0, s>>>(q, seq, H, dn, dr, L->inv_freq,
                                                        (float)g.rope_mscale, cache->d_lens, 0, qn,
@@ -758,7 +948,8 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
                (int64_t)(dn + dv)};
     QMLA_TRY(gemm(L, a, H, true, s));
   }
-  QMLA_TRY(linear(L, o, n, H * dv, L->wo, L->bo, g.hidden, out, s, part, w.part_elems));
+  QMLA_TRY(project(L, o, n, H * dv, L->wo, L->wo_x, L->bo, g.hidden, out, s, part,
+                   w.part_elems, xsp));
   return QMLA_OK;
 }
 
@@ -786,8 +977,12 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
   hipStream_t s = as_stream(stream);
   const int n = batch * seq;
 
-  QMLA_TRY(linear(L, xs, n, g.hidden, L->wq, L->bq, H * (dn + dr), q, s, part, w.part_elems));
-  QMLA_TRY(linear(L, xs, n, g.hidden, L->wkva, L->bkva, r + dr, kva, s, part, w.part_elems));
+  void *xsp = ws + w.xsplit;
+  // q_proj and kv_a_proj_with_mqa share one split of xs
+  QMLA_TRY(project(L, xs, n, g.hidden, L->wq, L->wq_x, L->bq, H * (dn + dr), q, s, part,
+                   w.part_elems, xsp));
+  QMLA_TRY(project(L, xs, n, g.hidden, L->wkva, L->wkva_x, L->bkva, r + dr, kva, s, part,
+                   w.part_elems, xsp, false));
   // With a bf16 cache the attention runs on the bf16 MFMA prefill: q, k, v
   // and k_rope are written in bf16 (round to nearest even) into the same
   // regions, and the bf16 context is widened again when the heads merge.
@@ -805,7 +1000,11 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
   // f32 rows also feed compute_kv below)
   QMLA_TRY(latent_to_cache(L, kva, batch, seq, rows, cache, s));
   // compute_kv on the LayerNorm'd latent (src/model.rs:178-190)
-  {
+  if (n >= kSplitRows && r >= 64) {
+    QMLA_TRY(split_act(rows, r + dr, n, r, xsp, s));
+    QMLA_TRY(gemm_split(L, static_cast<const uint16_t *>(xsp), 0, n, r, L->wkvb_x, split_cols(r),
+                        0, H * (dn + dv), kvb, H * (dn + dv), 0, 1, s));
+  } else {
     GemmArgs a{rows, L->wkvb, L->bkvb, kvb, n, H * (dn + dv), r, r + dr, r, (int64_t)H * (dn + dv),
                0, 0, 0, 0};
     QMLA_TRY(gemm(L, a, 1, true, s));
@@ -834,7 +1033,8 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
     k_merge_heads<float><<<dim3(n, H), dim3(128), 0, s>>>(ctx, seq, H, dv, o);
   }
   QMLA_LAUNCH_CHECK("k_merge_heads");
-  QMLA_TRY(linear(L, o, n, H * dv, L->wo, L->bo, g.hidden, out, s, part, w.part_elems));
+  QMLA_TRY(project(L, o, n, H * dv, L->wo, L->wo_x, L->bo, g.hidden, out, s, part,
+                   w.part_elems, xsp));
   return QMLA_OK;
 }
 
@@ -844,7 +1044,7 @@ qmla_status qmla_cache_materialise_workspace_bytes(const qmla_layer *layer,
   QMLA_REQUIRE(bytes, QMLA_ERR_INVALID_ARG, "bytes is NULL");
   int32_t T = 0;
   QMLA_TRY(check_materialise(layer, cache, seq0, n_seqs, &T));
-  *bytes = materialise_ws_bytes(cache, n_seqs, T);
+  *bytes = materialise_ws_bytes(layer, cache, n_seqs, T);
   return QMLA_OK;
 }
 
@@ -854,7 +1054,7 @@ qmla_status qmla_cache_materialise(const qmla_layer *L, const qmla_kv_cache *cac
                                    qmla_stream stream) {
   int32_t T = 0;
   QMLA_TRY(check_materialise(L, cache, seq0, n_seqs, &T));
-  const size_t need = materialise_ws_bytes(cache, n_seqs, T);
+  const size_t need = materialise_ws_bytes(L, cache, n_seqs, T);
   QMLA_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), QMLA_ERR_WORKSPACE,
                "workspace of %zu bytes < required %zu", workspace_bytes, need);
   if (T == 0) return QMLA_OK;
@@ -873,6 +1073,30 @@ qmla_status qmla_cache_materialise(const qmla_layer *L, const qmla_kv_cache *cac
     QMLA_LAUNCH_CHECK("k_broadcast_rope");
   }
   if (!k && !v) return QMLA_OK;
+  if (materialise_split(L, T)) {
+    // the c_kv rows in split form, then compute_kv (src/model.rs:178-190)
+    // per sequence as one split GEMM batched over heads (bias included)
+    uint16_t *xs = static_cast<uint16_t *>(workspace);
+    if (bf)
+      k_latent_c_split<uint16_t><<<dim3(T, n_seqs), dim3(256), 0, s>>>(cache->table(), seq0, T, r,
+                                                                        dr, xs);
+    else
+      k_latent_c_split<float><<<dim3(T, n_seqs), dim3(256), 0, s>>>(cache->table(), seq0, T, r, dr,
+                                                                     xs);
+    QMLA_LAUNCH_CHECK("k_latent_c_split");
+    const int KX = split_cols(r);
+    const int64_t sW = (int64_t)(dn + dv) * KX;
+    for (int32_t b = 0; b < n_seqs; ++b) {
+      const uint16_t *xb = xs + (size_t)b * T * KX;
+      if (k)
+        QMLA_TRY(gemm_split(L, xb, 0, T, r, L->wkvb_x, KX, sW, dn, k + (size_t)b * H * T * dn, dn,
+                            (int64_t)T * dn, H, s));
+      if (v)
+        QMLA_TRY(gemm_split(L, xb, 0, T, r, L->wkvb_x + (size_t)dn * KX, KX, sW, dv,
+                            v + (size_t)b * H * T * dv, dv, (int64_t)T * dv, H, s));
+    }
+    return QMLA_OK;
+  }
   // the c_kv rows, gathered from the pages into [n, T, r] f32
   float *lat = static_cast<float *>(workspace);
   if (bf)

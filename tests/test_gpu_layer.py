@@ -231,6 +231,62 @@ def test_rejected_layer_call_leaves_the_cache_unchanged(qmla_gpu):
     del C
 
 
+def test_split_projections_keep_f32_parity(qmla_gpu):
+    """Products of at least 256 token rows run as split bf16 hi/lo GEMMs
+    (x w = x_hi w_hi + x_lo w_hi + x_hi w_lo, f32 accumulation): with an f32
+    cache, forward_prefill over 2 x 160 tokens and a 130-token
+    forward_with_cache step (260 rows, the GEMM path) stay within the f32
+    tolerance of the oracle's decompressed path."""
+    q = qmla_gpu
+    hidden, H, dn, dr, dv, r = 512, 16, 128, 64, 128, 512
+    w = O.MlaWeights.random(hidden, H, dn, dr, dv, r, seed=1750)
+    layer = q.MlaLayer(w)
+    b, s, s2 = 2, 160, 130
+    cache = q.KVCache([s + s2] * b, r, dr, q.F32)
+    xs = O.normal((b, s, hidden), 1751)
+    out = layer.forward_prefill(xs, cache)
+    ref, (k, v, kr) = O.mla_forward_prefill(w, xs)
+    err = rel_err(out, ref)
+    print(f"prefill {b}x{s} f32 cache rel_err={err:.2e}")
+    assert err < TOL
+    x2 = O.normal((b, s2, hidden), 1752)
+    out2 = layer.forward_with_cache(x2, cache)
+    ref2 = O.mla_forward_with_cache(w, x2, k, v, kr)
+    err2 = rel_err(out2, ref2)
+    print(f"decode step {b}x{s2} f32 cache rel_err={err2:.2e}")
+    assert err2 < TOL
+    assert list(cache.lengths()) == [s + s2] * b
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_materialise_long_sequences_split_gemm(qmla_gpu, dt):
+    """qmla_cache_materialise over sequences of at least 256 tokens runs
+    compute_kv as split bf16 GEMMs batched over heads: k and v equal the
+    oracle's decompression of the same latent rows within the f32
+    tolerance, k_rope is the rows' k_pe broadcast to every head."""
+    q = qmla_gpu
+    hidden, H, dn, dr, dv, r = 256, 8, 64, 32, 48, 128
+    w = O.MlaWeights.random(hidden, H, dn, dr, dv, r, seed=1760)
+    layer = q.MlaLayer(w)
+    b, T = 2, 300
+    dtype = q.F32 if dt == "f32" else q.BF16
+    cache = q.KVCache([T] * b, r, dr, dtype)
+    rows = O.normal((b * T, r + dr), 1761)
+    if dtype == q.BF16:
+        bits = O.to_bf16_bits(rows)
+        cache.write_pool(bits)
+        rows = O.bf16_bits_to_f32(bits)
+    else:
+        cache.write_pool(rows)
+    cache.set_lengths([T] * b)
+    gk, gv, gkr = layer.materialise(cache)
+    ek, ev, ekr = O.decompress_cache(w, rows.reshape(b, T, r + dr))
+    for name, got, ref in (("k", gk, ek), ("v", gv, ev), ("k_rope", gkr, ekr)):
+        err = rel_err(got, ref)
+        print(f"{dt} {name} rel_err={err:.2e}")
+        assert err < TOL
+
+
 def test_prefill_workspace_is_its_own_and_is_enforced(qmla_gpu):
     """qmla_layer_prefill_workspace_bytes sizes forward_prefill alone: at
     most the size that serves both calls, and far below it where the decode
