@@ -226,6 +226,8 @@ inline size_t split_bytes(int64_t M, int64_t K) {
 qmla_status split_act(const float *x, int64_t ldx, int M, int K, void *xs, hipStream_t s) {
   const int64_t n = (int64_t)M * K;
   if (n == 0) return QMLA_OK;
+  // k_split_rows writes the pad columns from the first K lanes of a row
+  QMLA_REQUIRE(split_cols(K) - 3 * K <= K, QMLA_ERR_SHAPE, "split of K = %d", K);
   const unsigned blocks = (unsigned)std::min<int64_t>((n + 255) / 256, 16384);
   k_split_rows<<<dim3(blocks), dim3(256), 0, s>>>(x, ldx, M, K, static_cast<uint16_t *>(xs));
   QMLA_LAUNCH_CHECK("k_split_rows");
