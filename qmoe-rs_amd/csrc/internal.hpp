@@ -199,6 +199,18 @@ struct SkinnyGemmArgs {
   const int32_t *lens;
   const float *inv_freq;
   float mscale;
+  // K split over `groups` (1 or 2) blocks per 32-output tile; group 0 adds
+  // the bias.  With 2 groups (QKV only) group 1 writes its half to
+  // q_nope1, q_rope1 and kva1, and the consumers add the two halves.
+  int groups;
+  float *q_nope1, *q_rope1, *kva1;
+  // optional second plane of x (f32, x's strides): the operand is x + x2
+  const float *x2;
+  // Optional elementwise work spread over the product's blocks (about one
+  // element per thread): add_dst[i] += add_src[i] for i < add_n.
+  float *add_dst;
+  const float *add_src;
+  int64_t add_n;
 };
 struct LatentRowsArgs;
 int skinny_waves(int K);

@@ -21,6 +21,7 @@ struct LatentRowsArgs {
   bool bf16;
   const int32_t *lens;     // [sequences] current length (the new rows go after it)
   float *rows;             // optional f32 copy [tokens][r + dr], or null
+  const float *kva1;       // optional second K-half of kva: the row is kva + kva1
 };
 
 // Sum over the block (all waves call it; blockDim.x a multiple of 64).
@@ -48,8 +49,9 @@ __host__ __device__ inline size_t latent_row_lds_bytes(int r, int dr) {
 __device__ inline void latent_row(const LatentRowsArgs &a, int tok, float *lds) {
   const int b = tok / a.s, i = tok % a.s, r = a.r, dr = a.dr;
   const float *src = a.kva + (int64_t)tok * (r + dr);
+  const float *src1 = a.kva1 ? a.kva1 + (int64_t)tok * (r + dr) : nullptr;
   float *x = lds, *red = lds + r + dr;
-  for (int c = threadIdx.x; c < r + dr; c += blockDim.x) x[c] = src[c];
+  for (int c = threadIdx.x; c < r + dr; c += blockDim.x) x[c] = src1 ? src[c] + src1[c] : src[c];
   __syncthreads();
   float *y = a.rows ? a.rows + (int64_t)tok * (r + dr) : nullptr;
   const int32_t len = a.lens[b];

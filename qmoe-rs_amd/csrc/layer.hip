@@ -513,9 +513,10 @@ qmla_status make_skinny_weights(qmla_layer *L, const float *wq, const float *bq,
 // product has a K the kernel takes and the token count is small.
 bool use_skinny(const qmla_layer *L, int n) {
   const auto &g = L->cfg;
-  return L->skinny && n <= kSkinnyRows && skinny_supported(32, g.hidden) &&
-         skinny_supported(32, g.qk_nope) && skinny_supported(32, g.kv_lora_rank) &&
-         skinny_supported(32, g.heads * g.v_dim);
+  // q_proj | kv_a splits its K (hidden) in two halves
+  return L->skinny && n <= kSkinnyRows && g.hidden % 32 == 0 &&
+         skinny_supported(32, g.hidden / 2) && skinny_supported(32, g.qk_nope) &&
+         skinny_supported(32, g.kv_lora_rank) && skinny_supported(32, g.heads * g.v_dim);
 }
 
 // Arguments of a skinny product y = x W^T (+ bias) with the FINAL store:
@@ -545,6 +546,7 @@ inline size_t al(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct LayerWs {
   size_t q, kva, rows, qn, qr, qlat, olat, o, dec, kvb, k, v, kr, ctx, part, part_elems, xsplit,
+      qn1, qr1, kva1,
       total;
 };
 
@@ -587,6 +589,12 @@ LayerWs layer_ws(const qmla_layer *L, int32_t batch, int32_t seq, size_t dec_byt
     w.qlat = take(sizeof(float) * n * H * g.kv_lora_rank);
     w.olat = take(sizeof(float) * n * H * g.kv_lora_rank);
     w.dec = take(dec_bytes);
+    // the second K-half of the skinny q_proj | kv_a product
+    if (n <= (size_t)kSkinnyRows) {
+      w.qn1 = take(sizeof(float) * n * H * g.qk_nope);
+      w.qr1 = take(sizeof(float) * n * H * g.qk_rope);
+      w.kva1 = take(sizeof(float) * n * (g.kv_lora_rank + g.qk_rope));
+    }
     dec_end = off;
   }
   if (use != WsFor::kDecode) {
@@ -872,6 +880,12 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
     //   q_proj | kv_a (q split and roped in the epilogue) -> W_UK absorption
     //   with the new latent cache rows in extra blocks -> decode core ->
     //   merge (+ length advance) -> W_UV -> o_proj
+    // q_proj | kv_a runs with its K range split over two block groups; its
+    // two halves land in two planes that the next launch adds (the
+    // absorption's operand load, the latent row blocks for kv_a, and its
+    // GEMM blocks for the roped q_rope).
+    float *qn1 = (float *)(ws + w.qn1), *qr1 = (float *)(ws + w.qr1);
+    float *kva1 = (float *)(ws + w.kva1);
     for (int m0 = 0; m0 < n; m0 += 32) {
       SkinnyGemmArgs a = skinny_args(L->w1f, xs + (size_t)m0 * g.hidden, g.hidden, 0, L->b1, 0,
                                      nullptr, 0, 0, std::min(32, n - m0), H * (dn + dr) + r + dr,
@@ -889,17 +903,29 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
       a.lens = cache->d_lens;
       a.inv_freq = L->inv_freq;
       a.mscale = (float)g.rope_mscale;
+      a.groups = 2;
+      a.q_nope1 = qn1;
+      a.q_rope1 = qr1;
+      a.kva1 = kva1;
       QMLA_TRY(launch_skinny_gemm(a, s));
     }
     // q_lat[t, h, :] = W_UK^h^T q_nope[t, h, :]   (z = head), and the latent
     // rows [LayerNorm(c) | rope(k_pe)] of the n new tokens into the cache
-    const LatentRowsArgs rows = latent_rows_args(L, kva, seq, nullptr, cache);
-    for (int m0 = 0; m0 < n; m0 += 32)
-      QMLA_TRY(launch_skinny_gemm(
-          skinny_args(L->wukf, qn + (size_t)m0 * H * dn, (int64_t)H * dn, dn, nullptr, 0,
-                      qlat + (size_t)m0 * H * r, (int64_t)H * r, r, std::min(32, n - m0), r, dn,
-                      H),
-          s, m0 == 0 ? &rows : nullptr, n));
+    LatentRowsArgs rows = latent_rows_args(L, kva, seq, nullptr, cache);
+    rows.kva1 = kva1;
+    for (int m0 = 0; m0 < n; m0 += 32) {
+      SkinnyGemmArgs uk = skinny_args(L->wukf, qn + (size_t)m0 * H * dn, (int64_t)H * dn, dn,
+                                      nullptr, 0, qlat + (size_t)m0 * H * r, (int64_t)H * r, r,
+                                      std::min(32, n - m0), r, dn, H);
+      uk.x2 = qn1 + (size_t)m0 * H * dn;
+      if (m0 == 0) {
+        // the roped q_rope's two halves
+        uk.add_dst = qr;
+        uk.add_src = qr1;
+        uk.add_n = (int64_t)n * H * dr;
+      }
+      QMLA_TRY(launch_skinny_gemm(uk, s, m0 == 0 ? &rows : nullptr, n));
+    }
     // the new rows sit past the device lengths: the decode attends
     // lens + seq tokens and its merge advances the lengths
     for (int32_t i = 0; i < batch; ++i) cache->h_lens[i] += seq;

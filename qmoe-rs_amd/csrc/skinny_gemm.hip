@@ -24,7 +24,10 @@
 // and a wave's whole K-slice is one contiguous run.
 //
 // Work split: block (nb, z) owns 32 outputs (n) of one z (a head for the
-// batched per-head products); its NW (<= 16) waves take consecutive
+// batched per-head products), or half of their K range when the product is
+// split over two block groups (twice the blocks: the 114-tile q_proj |
+// kv_a product otherwise leaves more than half of the 256 CUs idle, and
+// its consumers add the two halves); its NW (<= 8) waves take consecutive
 // K-slices.  Each wave streams its A fragments (hi and lo) from HBM into
 // registers, two chunks of kChunk steps in flight, reads its B fragments
 // (16 k x 32 tokens) from the f32 activations, and accumulates
@@ -43,6 +46,7 @@
 // the absorption product's launch instead of a launch of its own.
 
 #include <algorithm>
+#include <type_traits>
 
 #include "latent_rows.hpp"
 
@@ -74,7 +78,11 @@ __device__ __forceinline__ int64_t packed_b_offset(int m, int64_t k) {
   return (k >> 4) * 2048 + (int64_t)(m + 32 * ((k >> 3) & 1)) * 16 + (k & 7) * 2;
 }
 
-template <int NW, bool XP>
+// XM: how the B operand is read -- kXF32 f32 x, kXPacked the pre-split
+// fragment-major records, kXSum the f32 sum x + x2 of two planes.
+constexpr int kXF32 = 0, kXPacked = 1, kXSum = 2;
+
+template <int NW, int XM>
 __global__ __launch_bounds__(NW * 64) void k_skinny_gemm(SkinnyGemmArgs a, LatentRowsArgs rows,
                                                          int n_rows) {
   // LDS: the waves' partial tiles, or a latent row block's row
@@ -87,17 +95,25 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_gemm(SkinnyGemmArgs a, Laten
     if (blockIdx.y == 0) latent_row(rows, blockIdx.x, smem);
     return;
   }
-  const int nb = blockIdx.x - n_rows, z = blockIdx.y;
+  // tile nb, K-half grp (groups = 2) of plane z
+  const int nbg = blockIdx.x - n_rows, z = blockIdx.y;
+  if (a.add_n) {
+    const int64_t stride = (int64_t)(gridDim.x - n_rows) * gridDim.y * blockDim.x;
+    const int64_t i0 = ((int64_t)z * (gridDim.x - n_rows) + nbg) * blockDim.x + threadIdx.x;
+    for (int64_t i = i0; i < a.add_n; i += stride) a.add_dst[i] += a.add_src[i];
+  }
+  const int nb = nbg / a.groups, grp = nbg - nb * a.groups;
   const int n0 = nb * 32;
   const int row = lane & 31, h = lane >> 5;
   const int KS = a.K / 16;
-  const int steps = KS / NW;  // this wave's k-steps
-  const int ks0 = wave * steps;
+  const int steps = KS / a.groups / NW;  // this wave's k-steps
+  const int ks0 = grp * (KS / a.groups) + wave * steps;
   // B columns (tokens) past M load a clamped copy whose outputs are dropped.
   const int64_t brow = min(row, a.M - 1);
   const uint8_t *wf = reinterpret_cast<const uint8_t *>(a.w_frag) +
                       (((int64_t)z * NB + nb) * KS + ks0) * 2048 + lane * 16;
   const float *xp = a.x + z * a.sx + brow * a.ldx + ks0 * 16 + 8 * h;
+  const float *xp2 = XM == kXSum ? a.x2 + z * a.sx + brow * a.ldx + ks0 * 16 + 8 * h : nullptr;
   // XP: the activations come pre-split in the fragment-major B layout
   const uint8_t *xf = reinterpret_cast<const uint8_t *>(a.x) + (int64_t)ks0 * 2048 + lane * 16;
 
@@ -116,9 +132,14 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_gemm(SkinnyGemmArgs a, Laten
       const uint8_t *f = wf + (int64_t)st * 2048;
       ah[buf][c] = *reinterpret_cast<const bf16x8_t *>(f);
       al[buf][c] = *reinterpret_cast<const bf16x8_t *>(f + 1024);
-      if constexpr (XP) {
+      if constexpr (XM == kXPacked) {
         xa[buf][c] = *reinterpret_cast<const floatx4_t *>(xf + (int64_t)st * 2048);
         xb[buf][c] = *reinterpret_cast<const floatx4_t *>(xf + (int64_t)st * 2048 + 1024);
+      } else if constexpr (XM == kXSum) {
+        xa[buf][c] = *reinterpret_cast<const floatx4_t *>(xp + st * 16) +
+                     *reinterpret_cast<const floatx4_t *>(xp2 + st * 16);
+        xb[buf][c] = *reinterpret_cast<const floatx4_t *>(xp + st * 16 + 4) +
+                     *reinterpret_cast<const floatx4_t *>(xp2 + st * 16 + 4);
       } else {
         xa[buf][c] = *reinterpret_cast<const floatx4_t *>(xp + st * 16);
         xb[buf][c] = *reinterpret_cast<const floatx4_t *>(xp + st * 16 + 4);
@@ -130,7 +151,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_gemm(SkinnyGemmArgs a, Laten
     for (int c = 0; c < kChunk; ++c) {
       if (s0 + c < steps) {
         bf16x8_t xh, xl;
-        if constexpr (XP) {
+        if constexpr (XM == kXPacked) {
           xh = __builtin_bit_cast(bf16x8_t, xa[buf][c]);
           xl = __builtin_bit_cast(bf16x8_t, xb[buf][c]);
         } else {
@@ -163,7 +184,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_gemm(SkinnyGemmArgs a, Laten
 #pragma unroll
   for (int j = 0; j < 16; ++j) red[wave][j][lane] = acc[j];
   __syncthreads();
-  const float *bias = a.bias ? a.bias + z * a.sb : nullptr;
+  const float *bias = a.bias && grp == 0 ? a.bias + z * a.sb : nullptr;
   // epilogue over pairs (j, j + 1), j even: adjacent outputs of one token
   for (int e = threadIdx.x; e < 8 * 64; e += NW * 64) {
     const int j = 2 * (e >> 6), l = e & 63;
@@ -204,24 +225,25 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_gemm(SkinnyGemmArgs a, Laten
     const int qw = a.dn + a.dr, hq = a.heads * qw;
     const int mg = a.m0 + m;  // token index in the whole call
     if (n >= hq) {
-      float *y = a.kva + (int64_t)mg * a.kva_ld + (n - hq);
+      float *y = (grp ? a.kva1 : a.kva) + (int64_t)mg * a.kva_ld + (n - hq);
       y[0] = v0;
       y[1] = v1;
       continue;
     }
     const int hd = n / qw, d = n - hd * qw;
     if (d < a.dn) {
-      float *y = a.q_nope + ((int64_t)mg * a.heads + hd) * a.dn + d;
+      float *y = (grp ? a.q_nope1 : a.q_nope) + ((int64_t)mg * a.heads + hd) * a.dn + d;
       y[0] = v0;
       y[1] = v1;
     } else {
-      // interleaved pair (2p, 2p + 1) of q_rope (src/model.rs:70-84)
+      // interleaved pair (2p, 2p + 1) of q_rope (src/model.rs:70-84); the
+      // rotation is linear, so each K-half is rotated on its own
       const int p = (d - a.dn) >> 1;
       const int b = mg / a.seq, i = mg - b * a.seq;
       const float pos = (float)(a.lens[b] + i);
       const float ang = pos * a.inv_freq[p];
       const float cs = cosf(ang) * a.mscale, sn = sinf(ang) * a.mscale;
-      float *y = a.q_rope + ((int64_t)mg * a.heads + hd) * a.dr + 2 * p;
+      float *y = (grp ? a.q_rope1 : a.q_rope) + ((int64_t)mg * a.heads + hd) * a.dr + 2 * p;
       y[0] = v0 * cs - v1 * sn;
       y[1] = v1 * cs + v0 * sn;
     }
@@ -230,13 +252,13 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_gemm(SkinnyGemmArgs a, Laten
 
 }  // namespace
 
-// Waves per block: the K split, up to 16, with each wave's range a multiple
-// of 16 and at least 64 wide when K allows.  At 16 waves a K of 2048 leaves
-// each wave 8 k-steps, all of them in flight at once.  (A block's time is
-// set by what one CU moves -- its weight slab plus the activations -- not by
-// the number of waits: 8 and 16 waves time alike.)
+// Waves per block: the split of a block's K range, up to 8, with each
+// wave's range a multiple of 16 and at least 64 wide when K allows.  Eight
+// waves time ~10% below sixteen at K = 2048 (a block's time is set by what
+// one CU moves -- its weight slab plus the activations -- and sixteen waves
+// only add the reduction through LDS).
 int skinny_waves(int K) {
-  int nw = 16;
+  int nw = 8;
   while (nw > 1 && (K % (16 * nw) != 0 || K / nw < 64)) nw >>= 1;
   return K % (16 * nw) == 0 ? nw : 0;
 }
@@ -267,37 +289,42 @@ bool skinny_supported(int M, int K) { return M >= 1 && M <= 32 && K > 0 && skinn
 
 qmla_status launch_skinny_gemm(const SkinnyGemmArgs &a, hipStream_t stream,
                                const LatentRowsArgs *rows, int n_rows) {
-  QMLA_REQUIRE(skinny_supported(a.M, a.K), QMLA_ERR_UNSUPPORTED, "skinny GEMM M %d K %d", a.M,
-               a.K);
+  const int G = a.groups ? a.groups : 1;
+  QMLA_REQUIRE(G == 1 || G == 2, QMLA_ERR_SHAPE, "skinny GEMM groups %d", G);
+  QMLA_REQUIRE(a.K % (16 * G) == 0 && skinny_supported(a.M, a.K / G), QMLA_ERR_UNSUPPORTED,
+               "skinny GEMM M %d K %d groups %d", a.M, a.K, G);
   QMLA_REQUIRE(a.N > 0 && a.Z > 0 && a.Z <= 65535, QMLA_ERR_SHAPE, "skinny GEMM N %d Z %d", a.N,
                a.Z);
   QMLA_REQUIRE(a.mode != kSkinnyQkv || (a.N % 2 == 0 && a.dn % 2 == 0 && a.dr % 2 == 0),
                QMLA_ERR_SHAPE, "q/kv split needs even widths");
-  const int nw = skinny_waves(a.K);
+  QMLA_REQUIRE(G == 1 || (a.mode == kSkinnyQkv && a.q_nope1 && a.q_rope1 && a.kva1),
+               QMLA_ERR_SHAPE, "a K split in two needs the second half's destination");
+  QMLA_REQUIRE(!(a.x_packed && a.x2), QMLA_ERR_SHAPE, "packed activations have one plane");
+  const int nw = skinny_waves(a.K / G);
   const int extra = rows ? n_rows : 0;
   LatentRowsArgs ra{};
   if (rows) ra = *rows;
-  dim3 grid((unsigned)((a.N + 31) / 32 + extra), (unsigned)a.Z);
+  SkinnyGemmArgs args = a;
+  args.groups = G;
+  dim3 grid((unsigned)((a.N + 31) / 32 * G + extra), (unsigned)a.Z);
   const size_t lds = std::max(sizeof(float) * nw * 16 * 64,
                               rows ? latent_row_lds_bytes(rows->r, rows->dr) : 0);
-  if (a.x_packed) {
-    QMLA_REQUIRE(a.Z == 1, QMLA_ERR_SHAPE, "packed activations need Z = 1");
+  if (a.x_packed) QMLA_REQUIRE(a.Z == 1, QMLA_ERR_SHAPE, "packed activations need Z = 1");
+  auto go = [&](auto xm) {
+    constexpr int XM = decltype(xm)::value;
     switch (nw) {
-      case 16: k_skinny_gemm<16, true><<<grid, dim3(1024), lds, stream>>>(a, ra, extra); break;
-      case 8: k_skinny_gemm<8, true><<<grid, dim3(512), lds, stream>>>(a, ra, extra); break;
-      case 4: k_skinny_gemm<4, true><<<grid, dim3(256), lds, stream>>>(a, ra, extra); break;
-      case 2: k_skinny_gemm<2, true><<<grid, dim3(128), lds, stream>>>(a, ra, extra); break;
-      default: k_skinny_gemm<1, true><<<grid, dim3(64), lds, stream>>>(a, ra, extra); break;
+      case 8: k_skinny_gemm<8, XM><<<grid, dim3(512), lds, stream>>>(args, ra, extra); break;
+      case 4: k_skinny_gemm<4, XM><<<grid, dim3(256), lds, stream>>>(args, ra, extra); break;
+      case 2: k_skinny_gemm<2, XM><<<grid, dim3(128), lds, stream>>>(args, ra, extra); break;
+      default: k_skinny_gemm<1, XM><<<grid, dim3(64), lds, stream>>>(args, ra, extra); break;
     }
-  } else {
-    switch (nw) {
-      case 16: k_skinny_gemm<16, false><<<grid, dim3(1024), lds, stream>>>(a, ra, extra); break;
-      case 8: k_skinny_gemm<8, false><<<grid, dim3(512), lds, stream>>>(a, ra, extra); break;
-      case 4: k_skinny_gemm<4, false><<<grid, dim3(256), lds, stream>>>(a, ra, extra); break;
-      case 2: k_skinny_gemm<2, false><<<grid, dim3(128), lds, stream>>>(a, ra, extra); break;
-      default: k_skinny_gemm<1, false><<<grid, dim3(64), lds, stream>>>(a, ra, extra); break;
-    }
-  }
+  };
+  if (a.x_packed)
+    go(std::integral_constant<int, kXPacked>{});
+  else if (a.x2)
+    go(std::integral_constant<int, kXSum>{});
+  else
+    go(std::integral_constant<int, kXF32>{});
   QMLA_LAUNCH_CHECK("k_skinny_gemm");
   return QMLA_OK;
 }
