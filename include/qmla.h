@@ -19,9 +19,13 @@
  *    qmla_cache_set_growth; qmla_cache_reserve_pool avoids it).
  *  - Tensors are row-major and contiguous, in the layouts documented at
  *    each call.  bf16 values are stored as uint16 bit patterns.
- *  - No global mutable state apart from the per-thread error string and a
- *    per-device cached CU count, so calls on different streams may run from
- *    different threads.  A cache object must not be mutated concurrently.
+ *  - Global mutable state: the per-thread error string, a per-device cached
+ *    CU count, and the allocation-free decode's scratch array (one per GPU,
+ *    with its device address cached per device; see
+ *    qmla_decode_absorbed_noalloc: calls of that entry point that overlap on
+ *    one GPU race and must be serialised by the caller).  Every other call
+ *    on different streams may run from different threads.  A cache object
+ *    must not be mutated concurrently.
  *    A layer object may be used from several threads at once: its GEMM path
  *    (prefill, and decode shapes the skinny kernel does not take) takes one
  *    of 4 rocBLAS handles created with the layer, so up to 4 such calls run

@@ -164,25 +164,39 @@ qmla_status ensure_capacity(qmla_kv_cache *c, int32_t seq0, const std::vector<in
     const int64_t grow = std::max<int64_t>(1, std::min(c->pool_pages / 2, cap_pages));
     QMLA_TRY(add_chunk(c, std::max(extra - (int64_t)c->free_pages.size(), grow)));
   }
-  TableWriter tw(c, s);
+  // Stage the new pages and capacities, launch every table write, and only
+  // then commit them to the host mirror and the free list: a failed launch
+  // leaves the host state as it was (the pages it staged stay free).
+  struct Grant {
+    int32_t seq, npages, cap;
+  };
+  std::vector<Grant> grants;
+  std::vector<std::pair<int64_t, uint64_t>> pages;  // (table slot, page address)
+  size_t taken = 0;
   for (int32_t i = 0; i < n; ++i) {
     const int32_t q = seq0 + i;
     if (want[i] <= c->h_cap[q]) continue;
     const int32_t need = (int32_t)ceil_div(want[i], P);
-    for (int32_t j = c->h_npages[q]; j < need; ++j) {
-      const uint64_t page = c->free_pages.back();
-      c->free_pages.pop_back();
-      const int64_t slot = (int64_t)q * c->table_width + j;
-      c->h_pages[slot] = page;
-      QMLA_TRY(tw.page(slot, page));
-      c->contiguous = false;
-    }
-    c->h_npages[q] = std::max(c->h_npages[q], need);
-    c->h_cap[q] = exact ? (int32_t)want[i]
-                        : (int32_t)std::min<int64_t>((int64_t)c->h_npages[q] * P, 0x7fffffff);
-    QMLA_TRY(tw.cap(q, c->h_cap[q]));
+    for (int32_t j = c->h_npages[q]; j < need; ++j)
+      pages.emplace_back((int64_t)q * c->table_width + j,
+                         c->free_pages[c->free_pages.size() - 1 - taken++]);
+    const int32_t npages = std::max(c->h_npages[q], need);
+    grants.push_back({q, npages,
+                      exact ? (int32_t)want[i]
+                            : (int32_t)std::min<int64_t>((int64_t)npages * P, 0x7fffffff)});
   }
-  return tw.flush();
+  TableWriter tw(c, s);
+  for (const auto &p : pages) QMLA_TRY(tw.page(p.first, p.second));
+  for (const Grant &g : grants) QMLA_TRY(tw.cap(g.seq, g.cap));
+  QMLA_TRY(tw.flush());
+  for (const auto &p : pages) c->h_pages[p.first] = p.second;
+  c->free_pages.resize(c->free_pages.size() - taken);
+  if (taken > 0) c->contiguous = false;
+  for (const Grant &g : grants) {
+    c->h_npages[g.seq] = g.npages;
+    c->h_cap[g.seq] = g.cap;
+  }
+  return QMLA_OK;
 }
 
 }  // namespace

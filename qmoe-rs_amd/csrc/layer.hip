@@ -927,11 +927,18 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
       QMLA_TRY(launch_skinny_gemm(uk, s, m0 == 0 ? &rows : nullptr, n));
     }
     // the new rows sit past the device lengths: the decode attends
-    // lens + seq tokens and its merge advances the lengths
+    // lens + seq tokens and its merge advances the lengths.  The host
+    // mirror moves with them (the split plan counts the new tokens); if the
+    // decode is not launched, the merge never advances the device lengths,
+    // so the mirror goes back and both keep the old lengths.
     for (int32_t i = 0; i < batch; ++i) cache->h_lens[i] += seq;
     qmla_decode_dims dd{batch, seq * H, r, dr};
-    QMLA_TRY(decode_launch(&dd, cache, QMLA_F32, qlat, qr, g.softmax_scale, olat, nullptr, 0,
-                           ws + w.dec, dec_bytes, seq, true, s));
+    const qmla_status st = decode_launch(&dd, cache, QMLA_F32, qlat, qr, g.softmax_scale, olat,
+                                         nullptr, 0, ws + w.dec, dec_bytes, seq, true, s);
+    if (st != QMLA_OK) {
+      for (int32_t i = 0; i < batch; ++i) cache->h_lens[i] -= seq;
+      return st;
+    }
     // o[t, h, :] = W_UV^h o_lat[t, h, :] + b_V^h, written as o_proj's
     // packed B operand (32 token rows x H dv: 4 (H dv) bytes), then o_proj
     for (int m0 = 0; m0 < n; m0 += 32) {

@@ -48,6 +48,36 @@ fn ok(st: qmla_status) -> Result<()> {
     }
 }
 
+/// A size the caller got wrong, caught before the call reaches C (which
+/// would read or write past the end of the slice or buffer).
+fn shape_err(message: String) -> Error {
+    Error { status: QMLA_ERR_SHAPE, message }
+}
+
+/// Host slice `what` must hold exactly `want` elements.
+fn check_len(what: &str, got: usize, want: usize) -> Result<()> {
+    if got == want { Ok(()) } else { Err(shape_err(format!("{what}: {got} elements, expected {want}"))) }
+}
+
+/// Optional host slice: absent, or exactly `want` elements.
+fn check_opt_len(what: &str, got: Option<&[f32]>, want: usize) -> Result<()> {
+    got.map_or(Ok(()), |s| check_len(what, s.len(), want))
+}
+
+/// Device buffer `what` must hold at least `want` bytes.
+fn check_bytes(what: &str, b: &DeviceBuffer, want: usize) -> Result<()> {
+    if b.bytes() >= want {
+        Ok(())
+    } else {
+        Err(shape_err(format!("{what}: {}-byte buffer, need {want} bytes", b.bytes())))
+    }
+}
+
+/// A dimension as usize: negative values are a shape error.
+fn dim(what: &str, v: i32) -> Result<usize> {
+    usize::try_from(v).map_err(|_| shape_err(format!("{what} = {v} is negative")))
+}
+
 /// Element types of device tensors (bf16 as u16 bit patterns).
 #[derive(Clone, Copy, Debug, PartialEq, Eq)]
 pub enum DType {
@@ -131,10 +161,21 @@ impl DeviceBuffer {
         }
         Ok(b)
     }
+    /// Overwrites the start of the buffer with a host slice (synchronous);
+    /// allocates nothing.
+    pub fn copy_from_slice<T: Copy>(&mut self, data: &[T], stream: &Stream) -> Result<()> {
+        let bytes = std::mem::size_of_val(data);
+        check_bytes("copy destination", self, bytes)?;
+        if bytes > 0 {
+            ok(unsafe { qmla_memcpy_h2d(self.ptr, data.as_ptr() as *const c_void, bytes, stream.raw()) })?;
+            stream.synchronize()?;
+        }
+        Ok(())
+    }
     /// Copies the first `out.len()` elements back to the host (synchronous).
     pub fn copy_to<T: Copy>(&self, out: &mut [T], stream: &Stream) -> Result<()> {
         let bytes = std::mem::size_of_val(out);
-        assert!(bytes <= self.bytes, "copy of {} bytes from a {}-byte buffer", bytes, self.bytes);
+        check_bytes("copy source", self, bytes)?;
         if bytes > 0 {
             ok(unsafe { qmla_memcpy_d2h(out.as_mut_ptr() as *mut c_void, self.ptr, bytes, stream.raw()) })?;
             stream.synchronize()?;
@@ -167,8 +208,10 @@ impl Drop for DeviceBuffer {
     }
 }
 
-/// The latent KV cache: sequence i holds its tokens' `[c_kv | k_pe]` rows
-/// in one contiguous range of an HBM pool, with a device length table.
+/// The latent KV cache: one `[c_kv | k_pe]` row per token, held in HBM
+/// pages that a device block table lists per sequence (token t of sequence
+/// i is row t % page_rows of its page t / page_rows), with a device length
+/// table.  Growth adds pages and never moves a row.
 pub struct KVCache {
     raw: *mut qmla_kv_cache,
     num_seqs: usize,
@@ -213,7 +256,7 @@ impl KVCache {
     /// Rows [t0, t0 + n) of sequence `seq` into `out` ([n, r + dr] in the
     /// cache dtype), wherever its pages are.
     pub fn gather(&self, seq: usize, t0: usize, n: usize, out: &mut DeviceBuffer, stream: &Stream) -> Result<()> {
-        assert!(out.bytes() >= n * (self.kv_lora_rank + self.rope_dim) * self.dtype.size(), "out too small");
+        check_bytes("gather out", out, n * (self.kv_lora_rank + self.rope_dim) * self.dtype.size())?;
         ok(unsafe { qmla_cache_gather(self.raw, seq as i32, t0 as i32, n as i32, out.ptr_mut(), stream.raw()) })
     }
     /// Returns the pages of sequences seq0..seq0 + n beyond their lengths to
@@ -245,7 +288,7 @@ impl KVCache {
     pub fn append(&mut self, rows: &DeviceBuffer, rows_dtype: DType, n_seqs: usize, n_new: usize,
                   stream: &Stream) -> Result<()> {
         let need = n_seqs * n_new * (self.kv_lora_rank + self.rope_dim) * rows_dtype.size();
-        assert!(rows.bytes() >= need, "rows buffer too small");
+        check_bytes("rows", rows, need)?;
         ok(unsafe {
             qmla_cache_append(self.raw, rows.ptr(), rows_dtype.raw(), n_seqs as i32, n_new as i32, stream.raw())
         })
@@ -257,11 +300,11 @@ impl KVCache {
         Ok(v)
     }
     pub fn set_lengths(&mut self, lengths: &[i32], stream: &Stream) -> Result<()> {
-        assert_eq!(lengths.len(), self.num_seqs);
+        check_len("lengths", lengths.len(), self.num_seqs)?;
         ok(unsafe { qmla_cache_set_lengths(self.raw, lengths.as_ptr(), stream.raw()) })
     }
     pub fn reserve(&mut self, min_capacity: &[i32], stream: &Stream) -> Result<()> {
-        assert_eq!(min_capacity.len(), self.num_seqs);
+        check_len("min_capacity", min_capacity.len(), self.num_seqs)?;
         ok(unsafe { qmla_cache_reserve(self.raw, min_capacity.as_ptr(), stream.raw()) })
     }
     /// `#[derive(Clone)]` (src/model.rs:87) on a stream.
@@ -339,6 +382,21 @@ impl MlaAttention {
     }
 
     pub fn new(config: qmla_layer_config, w: &MlaWeights) -> Result<Self> {
+        let c = &config;
+        let hid = dim("hidden", c.hidden)?;
+        let h = dim("heads", c.heads)?;
+        let (dn, dr, dv) = (dim("qk_nope", c.qk_nope)?, dim("qk_rope", c.qk_rope)?, dim("v_dim", c.v_dim)?);
+        let r = dim("kv_lora_rank", c.kv_lora_rank)?;
+        check_len("q_proj weight", w.wq.len(), h * (dn + dr) * hid)?;
+        check_opt_len("q_proj bias", w.bq, h * (dn + dr))?;
+        check_len("kv_a_proj_with_mqa weight", w.wkva.len(), (r + dr) * hid)?;
+        check_opt_len("kv_a_proj_with_mqa bias", w.bkva, r + dr)?;
+        check_len("kv_a_layernorm weight", w.ln_w.len(), r)?;
+        check_opt_len("kv_a_layernorm bias", w.ln_b, r)?;
+        check_len("kv_b_proj weight", w.wkvb.len(), h * (dn + dv) * r)?;
+        check_opt_len("kv_b_proj bias", w.bkvb, h * (dn + dv))?;
+        check_len("o_proj weight", w.wo.len(), hid * h * dv)?;
+        check_opt_len("o_proj bias", w.bo, hid)?;
         let mut raw: *mut qmla_layer = ptr::null_mut();
         ok(unsafe {
             qmla_layer_create(&config, w.wq.as_ptr(), opt_ptr(w.bq), w.wkva.as_ptr(), opt_ptr(w.bkva),
@@ -364,10 +422,18 @@ impl MlaAttention {
         Ok(n)
     }
 
+    /// xs and out hold [batch, seq, hidden] f32 each.
+    fn check_io(&self, xs: &DeviceBuffer, out: &DeviceBuffer, batch: usize, seq: usize) -> Result<()> {
+        let n = 4 * batch * seq * self.config.hidden.max(0) as usize;
+        check_bytes("xs", xs, n)?;
+        check_bytes("out", out, n)
+    }
+
     /// forward_with_cache (src/model.rs:256-307): xs [batch, seq, hidden]
     /// -> out, appending the new tokens to sequences 0..batch of `cache`.
     pub fn forward_with_cache(&self, xs: &DeviceBuffer, batch: usize, seq: usize, cache: &mut KVCache,
                               out: &mut DeviceBuffer, workspace: &mut DeviceBuffer, stream: &Stream) -> Result<()> {
+        self.check_io(xs, out, batch, seq)?;
         ok(unsafe {
             qmla_layer_forward_with_cache(self.raw, xs.ptr() as *const f32, batch as i32, seq as i32, cache.raw,
                                           out.ptr_mut() as *mut f32, workspace.ptr_mut(), workspace.bytes(),
@@ -378,6 +444,7 @@ impl MlaAttention {
     /// forward_prefill (src/model.rs:193-253) into empty sequences.
     pub fn forward_prefill(&self, xs: &DeviceBuffer, batch: usize, seq: usize, cache: &mut KVCache,
                            out: &mut DeviceBuffer, workspace: &mut DeviceBuffer, stream: &Stream) -> Result<()> {
+        self.check_io(xs, out, batch, seq)?;
         ok(unsafe {
             qmla_layer_forward_prefill(self.raw, xs.ptr() as *const f32, batch as i32, seq as i32, cache.raw,
                                        out.ptr_mut() as *mut f32, workspace.ptr_mut(), workspace.bytes(),
@@ -390,11 +457,15 @@ impl MlaAttention {
     /// T: (k [n, H, T, dn], v [n, H, T, dv], k_rope [n, H, T, dr]) in f32.
     pub fn materialise(&self, cache: &KVCache, seq0: usize, n: usize, stream: &Stream)
                        -> Result<(DeviceBuffer, DeviceBuffer, DeviceBuffer, usize)> {
+        let lens = cache.lengths()?;
+        if seq0 + n > lens.len() || n == 0 {
+            return Err(shape_err(format!("sequences {seq0}..{} of a {}-sequence cache", seq0 + n, lens.len())));
+        }
+        let t = lens[seq0] as usize;
         let mut ws_bytes = 0usize;
         ok(unsafe {
             qmla_cache_materialise_workspace_bytes(self.raw, cache.raw, seq0 as i32, n as i32, &mut ws_bytes)
         })?;
-        let t = cache.lengths()?[seq0] as usize;
         let c = &self.config;
         let (h, dn, dv, dr) = (c.heads as usize, c.qk_nope as usize, c.v_dim as usize, c.qk_rope as usize);
         let mut k = DeviceBuffer::new(4 * n * h * t * dn)?;
@@ -427,6 +498,17 @@ impl Drop for MlaAttention {
 pub fn fused_prefill_attn(dims: &qmla_prefill_dims, dtype: DType, q_nope: &DeviceBuffer, q_rope: &DeviceBuffer,
                           k: &DeviceBuffer, k_rope: &DeviceBuffer, v: &DeviceBuffer, scale: f64, causal: bool,
                           out: &mut DeviceBuffer, stream: &Stream) -> Result<()> {
+    let (b, h, sq, sk) = (dim("batch", dims.batch)?, dim("heads", dims.heads)?, dim("seq_q", dims.seq_q)?,
+                          dim("seq_k", dims.seq_k)?);
+    let (dn, dr, dv) = (dim("qk_nope", dims.qk_nope)?, dim("qk_rope", dims.qk_rope)?, dim("v_dim", dims.v_dim)?);
+    let krh = dim("k_rope_heads", dims.k_rope_heads)?;
+    let es = dtype.size();
+    check_bytes("q_nope", q_nope, b * h * sq * dn * es)?;
+    check_bytes("q_rope", q_rope, b * h * sq * dr * es)?;
+    check_bytes("k", k, b * h * sk * dn * es)?;
+    check_bytes("k_rope", k_rope, b * krh * sk * dr * es)?;
+    check_bytes("v", v, b * h * sk * dv * es)?;
+    check_bytes("out", out, b * h * sq * dv * es)?;
     ok(unsafe {
         qmla_fused_prefill_attn(dims, dtype.raw(), q_nope.ptr(), q_rope.ptr(), k.ptr(), k_rope.ptr(), v.ptr(),
                                 scale, causal as i32, out.ptr_mut(), stream.raw())
@@ -439,6 +521,14 @@ pub fn decode_absorbed(dims: &qmla_decode_dims, cache: &KVCache, q_dtype: DType,
                        q_rope: &DeviceBuffer, scale: f64, out_latent: &mut DeviceBuffer,
                        out_lse: Option<&mut DeviceBuffer>, workspace: &mut DeviceBuffer,
                        stream: &Stream) -> Result<()> {
+    let (b, rows) = (dim("batch", dims.batch)?, dim("rows", dims.rows)?);
+    let (r, dr) = (dim("kv_lora_rank", dims.kv_lora_rank)?, dim("rope_dim", dims.rope_dim)?);
+    check_bytes("q_latent", q_latent, b * rows * r * q_dtype.size())?;
+    check_bytes("q_rope", q_rope, b * rows * dr * q_dtype.size())?;
+    check_bytes("out_latent", out_latent, b * rows * r * 4)?;
+    if let Some(l) = out_lse.as_deref() {
+        check_bytes("out_lse", l, b * rows * 4)?;
+    }
     let lse = out_lse.map_or(ptr::null_mut(), |b| b.ptr_mut() as *mut f32);
     ok(unsafe {
         qmla_decode_absorbed(dims, cache.raw, q_dtype.raw(), q_latent.ptr(), q_rope.ptr(), scale,
@@ -464,7 +554,8 @@ pub struct PackedQMoETensor {
 impl PackedQMoETensor {
     pub fn from_bytes(packed: &[u8], out_features: usize, in_features: usize, scales: &[f32],
                       stream: &Stream) -> Result<Self> {
-        assert!(packed.len() >= out_features * (in_features / 4) && scales.len() >= out_features);
+        check_len("packed bytes", packed.len(), out_features * (in_features / 4))?;
+        check_len("scales", scales.len(), out_features)?;
         Ok(PackedQMoETensor {
             data: DeviceBuffer::from_slice(packed, stream)?,
             scales: DeviceBuffer::from_slice(scales, stream)?,
@@ -474,6 +565,8 @@ impl PackedQMoETensor {
     }
     /// forward_simd (src/tensor.rs:64-95): x [batch, in] -> out [batch, out].
     pub fn forward(&self, x: &DeviceBuffer, batch: usize, out: &mut DeviceBuffer, stream: &Stream) -> Result<()> {
+        check_bytes("x", x, 4 * batch * self.in_features)?;
+        check_bytes("out", out, 4 * batch * self.out_features)?;
         let mut n = 0usize;
         ok(unsafe {
             qmla_packed_forward_workspace_bytes(self.out_features as i32, self.in_features as i32, batch as i32,
@@ -502,6 +595,15 @@ impl QMoELayer {
     /// [E, I], [E, I, H/4] / [E, I], [E, H, I/4] / [E, H].
     pub fn new(config: qmla_moe_config, gate_weight: &[f32], packed: [&[u8]; 3], scales: [&[f32]; 3],
                stream: &Stream) -> Result<Self> {
+        let e = dim("num_experts", config.num_experts)?;
+        let (hd, id) = (dim("hidden_dim", config.hidden_dim)?, dim("intermediate_dim", config.intermediate_dim)?);
+        check_len("gate weight", gate_weight.len(), e * hd)?;
+        check_len("gate packed", packed[0].len(), e * id * (hd / 4))?;
+        check_len("up packed", packed[1].len(), e * id * (hd / 4))?;
+        check_len("down packed", packed[2].len(), e * hd * (id / 4))?;
+        check_len("gate scales", scales[0].len(), e * id)?;
+        check_len("up scales", scales[1].len(), e * id)?;
+        check_len("down scales", scales[2].len(), e * hd)?;
         Ok(QMoELayer {
             config,
             gate_weight: DeviceBuffer::from_slice(gate_weight, stream)?,
@@ -519,6 +621,9 @@ impl QMoELayer {
     /// forward (src/moe.rs:40-130): xs [seq_len, hidden] -> out.
     pub fn forward(&self, xs: &DeviceBuffer, seq_len: usize, out: &mut DeviceBuffer, workspace: &mut DeviceBuffer,
                    stream: &Stream) -> Result<()> {
+        let n = 4 * seq_len * self.config.hidden_dim.max(0) as usize;
+        check_bytes("xs", xs, n)?;
+        check_bytes("out", out, n)?;
         ok(unsafe {
             qmla_moe_forward(&self.config, xs.ptr() as *const f32, seq_len as i32,
                              self.gate_weight.ptr() as *const f32, self.packed[0].ptr() as *const u8,

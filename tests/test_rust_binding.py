@@ -145,3 +145,121 @@ def test_build_script_compiles_for_gfx950_and_links_the_runtime():
     for lib in ("qmla", "amdhip64", "rocblas"):
         assert f"rustc-link-lib=dylib={lib}" in b
     assert 'Command::new("make")' in b
+
+
+# ---- the candle drop-ins against the reference's public API -------------
+# The reference's signatures, written out from qmoe-rs src/model.rs and
+# src/attention_kernel.rs (whitespace-normalised): the engine calls these,
+# so the drop-ins must accept the same calls.
+MODEL_RS = os.path.join(ROOT, "qmoe-rs_amd", "rust", "qmla", "src", "model.rs")
+KERNEL_RS = os.path.join(ROOT, "qmoe-rs_amd", "rust", "qmla", "src", "attention_kernel.rs")
+LIB_RS = os.path.join(ROOT, "qmoe-rs_amd", "rust", "qmla", "src", "lib.rs")
+
+REF_METHODS = {  # src/model.rs:125, :193, :256
+    "new": "(vb: VarBuilder, config: &ModelConfig) -> Result<Self>",
+    "forward_prefill": "(&self, xs: &Tensor) -> Result<(Tensor, KVCache)>",
+    "forward_with_cache": "(&self, xs: &Tensor, cache: &mut KVCache) -> Result<Tensor>",
+}
+REF_FIELDS = [  # pub fields of MlaAttention, src/model.rs:108-122
+    ("q_proj", "candle_nn::Linear"), ("kv_a_proj_with_mqa", "candle_nn::Linear"),
+    ("kv_a_layernorm", "candle_nn::LayerNorm"), ("kv_b_proj", "candle_nn::Linear"),
+    ("o_proj", "candle_nn::Linear"), ("num_heads", "usize"), ("num_kv_heads", "usize"),
+    ("qk_nope_head_dim", "usize"), ("qk_rope_head_dim", "usize"), ("v_head_dim", "usize"),
+    ("kv_lora_rank", "usize"), ("rope_mscale", "f64"), ("softmax_scale", "f64"),
+]
+REF_CONFIG_FIELDS = ["hidden_size", "num_attention_heads", "num_key_value_heads", "qk_nope_head_dim",
+                     "qk_rope_head_dim", "v_head_dim", "kv_lora_rank"]  # src/model.rs:8-20
+REF_KERNELS = {  # src/attention_kernel.rs:34, :64, :110
+    "eager_prefill_attn": "(q: &Tensor, k: &Tensor, v: &Tensor, scale: f64, causal: bool) -> Result<Tensor>",
+    "fused_prefill_attn": "(q_nope: &Tensor, q_rope: &Tensor, k: &Tensor, k_rope: &Tensor, v: &Tensor, "
+                          "scale: f64, causal: bool) -> Result<Tensor>",
+    "reference_eager_attn": "(q: &Tensor, k: &Tensor, v: &Tensor, scale: f64, causal: bool) -> Result<Tensor>",
+}
+
+
+def _pub_fns(text, impl_of=None):
+    """{name: normalised '(args) -> ret'} of the `pub fn`s (inside `impl impl_of` if given)."""
+    if impl_of:
+        m = re.search(rf"\nimpl {impl_of} \{{\n(.*?)\n\}}\n", text, flags=re.S)
+        text = m.group(1)
+    out = {}
+    for m in re.finditer(r"pub fn (\w+)\s*(<[^>]*>)?\s*(\(.*?\))\s*->\s*([^{]+?)\s*\{", text, flags=re.S):
+        args = " ".join(m.group(3).split()).replace("( ", "(").replace(", )", ")")
+        out[m.group(1)] = (m.group(2) or "", f"{args} -> {' '.join(m.group(4).split())}")
+    return out
+
+
+def test_mla_attention_keeps_the_reference_constructor_and_methods():
+    t = open(MODEL_RS).read()
+    fns = _pub_fns(t, "MlaAttention")
+    for name in ("forward_prefill", "forward_with_cache"):
+        assert fns[name][1] == REF_METHODS[name], (name, fns[name])
+    # new(vb, config): the engine's &ModelConfig is accepted through MlaConfig
+    generics, sig = fns["new"]
+    assert generics.replace(" ", "") == "<C:MlaConfig+?Sized>", generics
+    assert sig.replace("&C", "&ModelConfig") == REF_METHODS["new"], sig
+    # the reference's VarBuilder paths and module constructors, :126-146
+    for path, ctor in (("q_proj", "linear"), ("kv_a_proj_with_mqa", "linear"),
+                       ("kv_a_layernorm", "layer_norm"), ("kv_b_proj", "linear"), ("o_proj", "linear")):
+        assert re.search(rf"candle_nn::{ctor}\([^;]*vb\.pp\(\"{path}\"\)\)", t), path
+    assert "layer_norm(r, 1e-6," in t  # LayerNorm eps 1e-6, :136
+
+
+def test_mla_attention_keeps_the_reference_pub_fields():
+    t = open(MODEL_RS).read()
+    body = re.search(r"pub struct MlaAttention \{(.*?)\n\}", t, flags=re.S).group(1)
+    fields = re.findall(r"^\s*pub (\w+): ([\w:]+),", body, flags=re.M)
+    got = dict(fields)
+    for name, ty in REF_FIELDS:
+        assert got.get(name) == ty, (name, got.get(name))
+    # the field order of the reference comes first
+    assert [n for n, _ in fields[:len(REF_FIELDS)]] == [n for n, _ in REF_FIELDS]
+
+
+def test_config_macro_reads_the_reference_model_config_fields():
+    t = open(MODEL_RS).read()
+    mac = re.search(r"macro_rules! impl_mla_config \{(.*?)\n\}", t, flags=re.S).group(1)
+    trait = re.search(r"pub trait MlaConfig \{(.*?)\n\}", t, flags=re.S).group(1)
+    for f in REF_CONFIG_FIELDS:
+        assert f"fn {f}(&self) -> usize" in trait, f
+        assert re.search(rf"fn {f}\(&self\) -> usize \{{ self\.{f} \}}", mac), f
+
+
+def test_kv_cache_is_clone_and_reads_the_reference_tensors():
+    t = open(MODEL_RS).read()
+    assert re.search(r"impl Clone for KVCache \{", t)
+    fns = _pub_fns(t, "KVCache")
+    for name in ("k", "v", "k_rope"):
+        assert fns[name][1] == "(&self, layer: &MlaAttention) -> Result<Tensor>", (name, fns[name])
+    assert "empty" in fns and "append" not in fns and "new" not in fns
+
+
+def test_attention_kernel_drop_in_keeps_the_reference_signatures():
+    fns = _pub_fns(open(KERNEL_RS).read())
+    for name, sig in REF_KERNELS.items():
+        assert fns[name][1] == sig, (name, fns[name])
+
+
+def test_safe_wrappers_check_sizes_before_calling_c():
+    """Every safe wrapper that hands caller slices or buffers to C checks
+    their sizes first (a short one would be read or written past its end)."""
+    t = open(LIB_RS).read()
+    wanted = {"MlaAttention": ["new", "forward_with_cache", "forward_prefill", "materialise"],
+              "KVCache": ["gather", "append", "set_lengths", "reserve"],
+              "PackedQMoETensor": ["from_bytes", "forward"],
+              "QMoELayer": ["new", "forward"],
+              None: ["fused_prefill_attn", "decode_absorbed"]}
+    for owner, names in wanted.items():
+        scope = t
+        if owner:
+            scope = re.search(rf"\nimpl {owner} \{{\n(.*?)\n\}}\n", t, flags=re.S).group(1) + "\n"
+        for name in names:
+            end = r"\n    \}\n" if owner else r"\n\}\n"
+            m = re.search(rf"pub fn {name}\b.*?\{{(.*?){end}", scope, flags=re.S)
+            body = m.group(1)
+            calls = [c for c in (body.find("unsafe"), body.find("from_slice(")) if c >= 0]
+            first_unsafe = min(calls)
+            checks = [body.find(k) for k in ("check_len(", "check_bytes(", "check_opt_len(",
+                                              "self.check_io(", "shape_err(")]
+            checks = [c for c in checks if c >= 0]
+            assert checks and min(checks) < first_unsafe, f"{owner}::{name} calls C before checking sizes"
