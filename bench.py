@@ -109,7 +109,11 @@ def time_steps(step, steps: int, warmup: int, stream):
     STATS.clear()
     STATS.update({"p10_ms": float(np.percentile(per, 10)), "median_ms": float(np.median(per)),
                   "p90_ms": float(np.percentile(per, 90)), "min_ms": float(per.min()), "max_ms": float(per.max()),
-                  "per_step_events": True})
+                  "per_step_events": True,
+                  "pass": "a second pass of the same K steps with an event after every step; each event leaves "
+                          "the GPU idle ~3 us before the next step, and the clock runs a little higher across "
+                          "those gaps, so this distribution differs from ms_per_step (the first pass, no events "
+                          "between steps)"})
     return wall, mean
 
 
@@ -197,67 +201,89 @@ class PrefillBench:
                 "tflops_at_median": self.flops / (STATS["median_ms"] * 1e-3) / 1e12, "step_ms": dict(STATS)}
 
 
+def v2lite_weights(seed, hidden=2048, heads=16):
+    """Host f32 weights of one MlaAttention at V2-Lite head shapes (dn 128,
+    dr 64, dv 128, r 512): N(0, 0.02^2), LayerNorm weight 1 + N(0, 0.02^2)."""
+    rng = np.random.default_rng(seed)
+    H, dn, dr, dv, r = heads, 128, 64, 128, 512
+
+    def nrm(*shape):
+        return (rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+
+    w = types.SimpleNamespace(hidden=hidden, heads=H, dn=dn, dr=dr, dv=dv, r=r, softmax_scale=None)
+    w.wq, w.bq = nrm(H * (dn + dr), hidden), nrm(H * (dn + dr))
+    w.wkva, w.bkva = nrm(r + dr, hidden), nrm(r + dr)
+    w.ln_w, w.ln_b = (1.0 + nrm(r)).astype(np.float32), nrm(r)
+    w.wkvb, w.bkvb = nrm(H * (dn + dv), r), nrm(H * (dn + dv))
+    w.wo, w.bo = nrm(hidden, H * dv), nrm(hidden)
+    return w
+
+
+def weight_bytes_of(w):
+    return 4 * (w.wq.size + w.wkva.size + w.wkvb.size + w.wo.size)
+
+
 class LayerDecodeBench:
     """MlaAttention::forward_with_cache (src/model.rs:256-307), one new token
     per sequence: f32 projections, LayerNorm + RoPE of the new latent rows
     into a bf16 latent cache, the absorbed decode core, W_UV and o_proj.
     V2-Lite head shapes (hidden 2048, 16 heads, dn 128, dr 64, dv 128,
     r 512), batch 32, 4096 cached tokens per sequence; weights N(0, 0.02^2),
-    activations N(0, 1), seeded.  The cache grows by one token per step in
-    growth mode: each sequence holds exactly its 4096 rows (16 pages of 256)
-    and takes a page from the pool's free list (sized for 512 more tokens per
-    sequence at creation) when it crosses a page boundary, inside the timed
-    steps once steps + warmup > 256."""
+    activations N(0, 1), seeded.  Steps rotate over `layers` layer copies
+    and `caches` caches (caches >= 512 MB in all, with the weights
+    ~0.7 GB), so no step re-reads weights or rows the 256 MB Infinity Cache
+    could still hold.  Each cache grows by one token per use in growth mode:
+    each sequence holds exactly its 4096 rows (16 pages of 256) and takes a
+    page from the pool's free list (sized for 512 more tokens per sequence
+    at creation) when it crosses a page boundary."""
 
-    def __init__(self, stream, seed, batch=32, ctx=4096, hidden=2048, heads=16):
-        rng = np.random.default_rng(seed)
-        H, dn, dr, dv, r = heads, 128, 64, 128, 512
-
-        def nrm(*shape):
-            return (rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)).astype(np.float32)
-
-        w = types.SimpleNamespace(hidden=hidden, heads=H, dn=dn, dr=dr, dv=dv, r=r, softmax_scale=None)
-        w.wq, w.bq = nrm(H * (dn + dr), hidden), nrm(H * (dn + dr))
-        w.wkva, w.bkva = nrm(r + dr, hidden), nrm(r + dr)
-        w.ln_w, w.ln_b = (1.0 + nrm(r)).astype(np.float32), nrm(r)
-        w.wkvb, w.bkvb = nrm(H * (dn + dv), r), nrm(H * (dn + dv))
-        w.wo, w.bo = nrm(hidden, H * dv), nrm(hidden)
-        self.layer = qmla.MlaLayer(w)
-        self.weight_bytes = 4 * (w.wq.size + w.wkva.size + w.wkvb.size + w.wo.size)
+    def __init__(self, stream, seed, batch=32, ctx=4096, hidden=2048, heads=16, layers=2,
+                 min_cache_bytes=512 << 20):
+        r, dr = 512, 64
+        ws = [v2lite_weights(seed + 7 * i, hidden, heads) for i in range(layers)]
+        self.layers = [qmla.MlaLayer(w) for w in ws]
+        self.weight_bytes = weight_bytes_of(ws[0])
         self.batch, self.ctx, self.stream = batch, ctx, stream
-        self.cache = qmla.KVCache([ctx] * batch, r, dr, qmla.BF16, grow=True,
-                                  pool_rows=batch * (ctx + 512))
+        ncache = max(2, math.ceil(min_cache_bytes / (batch * ctx * ROW_BYTES)))
         tmp = qmla.DeviceBuffer(64 << 20)
-        d = self.cache.describe()
-        fill_bf16(d.rows, d.total_rows * ROW_ELEMS, seed + 1, tmp, stream)
+        self.caches = []
+        for i in range(ncache):
+            c = qmla.KVCache([ctx] * batch, r, dr, qmla.BF16, grow=True, pool_rows=batch * (ctx + 512))
+            d = c.describe()
+            fill_bf16(d.rows, d.total_rows * ROW_ELEMS, seed + 1 + 1000003 * i, tmp, stream)
+            c.set_lengths([ctx] * batch, stream)
+            self.caches.append(c)
         stream.sync()
         tmp.free()
-        self.cache.set_lengths([ctx] * batch, stream)
         self.xs = qmla.DeviceBuffer(batch * hidden * 4)
         qmla.check(qmla.lib().qmla_fill_normal_f32(self.xs.ptr, batch * hidden, seed + 2, 0.0, 1.0,
                                                    qmla._sh(stream)))
         self.out = qmla.DeviceBuffer(batch * hidden * 4)
-        self.ws_bytes = self.layer.workspace_bytes(self.cache, batch, 1)
+        self.ws_bytes = self.layers[0].workspace_bytes(self.caches[0], batch, 1)
         self.ws = qmla.DeviceBuffer(self.ws_bytes)
         stream.sync()
 
     def step(self, i):
+        layer, cache = self.layers[i % len(self.layers)], self.caches[i % len(self.caches)]
         qmla.check(qmla.lib().qmla_layer_forward_with_cache(
-            self.layer.handle, self.xs.ptr, self.batch, 1, self.cache.handle, self.out.ptr, self.ws.ptr,
+            layer.handle, self.xs.ptr, self.batch, 1, cache.handle, self.out.ptr, self.ws.ptr,
             self.ws_bytes, qmla._sh(self.stream)))
 
     def run(self, steps, warmup):
-        assert warmup + 2 * steps <= 512, "the page pool has room for 512 new tokens per sequence"
-        pool0 = self.cache.pool_info()
+        nc = len(self.caches)
+        assert (warmup + 2 * steps) / nc <= 512, "each page pool has room for 512 new tokens per sequence"
+        pools0 = [c.pool_info() for c in self.caches]
         wall, ev = time_steps(self.step, steps, warmup, self.stream)
-        assert self.cache.pool_info()[0] == pool0[0], "the pool grew: a step allocated"
+        assert all(c.pool_info()[0] == p[0] for c, p in zip(self.caches, pools0)), "a pool grew: a step allocated"
         t = ev * 1e-3
-        mean_ctx = self.ctx + warmup + (steps + 1) / 2.0
+        mean_ctx = self.ctx + (warmup + (steps + 1) / 2.0) / nc
         hbm = self.weight_bytes + self.batch * mean_ctx * ROW_BYTES
-        pages = (pool0[1] - self.cache.pool_info()[1]) // 256
+        pages = sum((p[1] - c.pool_info()[1]) // 256 for c, p in zip(self.caches, pools0))
         return {"tok_s": self.batch / t, "ms_per_step": ev, "wall_ms_per_step": wall,
                 "weight_bytes": self.weight_bytes, "bytes_per_step": hbm, "tb_s": hbm / t / 1e12,
                 "hbm_frac": hbm / t / 1e12 / (HBM_PEAK_GBS / 1e3), "pages_taken": int(pages),
+                "rotation": {"layers": len(self.layers), "caches": nc,
+                             "bytes": nc * self.batch * self.ctx * ROW_BYTES + len(self.layers) * self.weight_bytes},
                 "step_ms": dict(STATS)}
 
 
@@ -274,19 +300,8 @@ class LayerPrefillBench:
     rows and the head-broadcast k_rope copy)."""
 
     def __init__(self, stream, seed, batch=4, seq=2048, hidden=2048, heads=16):
-        rng = np.random.default_rng(seed)
-        H, dn, dr, dv, r = heads, 128, 64, 128, 512
-
-        def nrm(*shape):
-            return (rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)).astype(np.float32)
-
-        w = types.SimpleNamespace(hidden=hidden, heads=H, dn=dn, dr=dr, dv=dv, r=r, softmax_scale=None)
-        w.wq, w.bq = nrm(H * (dn + dr), hidden), nrm(H * (dn + dr))
-        w.wkva, w.bkva = nrm(r + dr, hidden), nrm(r + dr)
-        w.ln_w, w.ln_b = (1.0 + nrm(r)).astype(np.float32), nrm(r)
-        w.wkvb, w.bkvb = nrm(H * (dn + dv), r), nrm(H * (dn + dv))
-        w.wo, w.bo = nrm(hidden, H * dv), nrm(hidden)
-        self.layer = qmla.MlaLayer(w)
+        H, dr, r = heads, 64, 512
+        self.layer = qmla.MlaLayer(v2lite_weights(seed, hidden, heads))
         self.batch, self.seq, self.heads, self.hidden, self.stream = batch, seq, H, hidden, stream
         self.caches = [qmla.KVCache([seq] * batch, r, dr, qmla.BF16) for _ in range(2)]
         self.xs = qmla.DeviceBuffer(batch * seq * hidden * 4)
@@ -325,15 +340,145 @@ class LayerPrefillBench:
         att = b * H * (s * (s + 1) // 2) * 2 * (192 + 128)
         kvb = 2 * b * s * 512 * H * (128 + 128)
         proj = 2 * b * s * self.hidden * (H * 192 + 576 + H * 128)
+        # the split form runs x w = x_hi w_hi + x_lo w_hi + x_hi w_lo (+ the
+        # bias columns) as one bf16 GEMM over K' = 3 K + 2 columns padded to
+        # a multiple of 64: the bf16 flops the MFMAs execute
+        kp = -(-(3 * 512 + 2) // 64) * 64
+        kvb_bf16 = kvb * kp / 512
         return {"tok_s": b * s / (ev * 1e-3), "ms_per_step": ev, "wall_ms_per_step": wall,
                 "gflop": {"attention": att / 1e9, "kv_b_decompress": kvb / 1e9, "projections": proj / 1e9},
                 "step_ms": step_ms,
-                "decompress": {"ms": evm, "gflop": kvb / 1e9, "tflops": kvb / (evm * 1e-3) / 1e12,
-                               "f32_mfma_frac": kvb / (evm * 1e-3) / 1e12 / F32_PEAK_TFLOPS,
+                "decompress": {"ms": evm, "gflop": kvb / 1e9,
+                               "f32_equivalent_tflops": kvb / (evm * 1e-3) / 1e12,
+                               "bf16_gflop_executed": kvb_bf16 / 1e9,
+                               "bf16_tflops": kvb_bf16 / (evm * 1e-3) / 1e12,
+                               "bf16_mfma_frac": kvb_bf16 / (evm * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
                                "what": "qmla_cache_materialise over the 4 x 2048 cached rows: the kv_b_proj "
-                                       "product as split bf16 GEMMs (rocBLAS, f32 accumulation, batched over "
-                                       "heads) plus the gather of the rows into split form and the "
-                                       "head-broadcast k_rope copy"}}
+                                       "product as split bf16 GEMMs (x w = x_hi w_hi + x_lo w_hi + x_hi w_lo, "
+                                       "f32 accumulation, K' = 3K + 2 padded to 64, batched over heads) plus "
+                                       "the gather of the rows into split form and the head-broadcast k_rope "
+                                       "copy; bf16_mfma_frac counts the executed bf16 flops against 2.5 PF"}}
+
+
+class Batch1Sweeps:
+    """The reference's batch-1 sweeps (benches/attention.rs:375-429), the
+    product's own call shape (src/main.rs:120-135 decodes one token at
+    batch 1): MlaAttention::forward_with_cache of one token over a cache of
+    `cache_len` tokens, and forward_prefill of `seq_len` tokens, at the
+    bench's widths (hidden 2048, 16 heads, kv_lora_rank 512, dn 128, dr 64,
+    dv 128), bf16 latent cache, f32 weights and activations.
+
+    Every timed call gets a cache of its own, filled to exactly the point's
+    length (the reference times cache.clone() + forward_with_cache, so each
+    iteration decodes against the same length), and the calls rotate over
+    `layers` layer copies (~1 GB of weights in all), so each call streams
+    its weights from HBM as a multi-layer model's step does rather than from
+    the 256 MB Infinity Cache."""
+
+    DECODE_LENS = (0, 64, 256, 1024, 4096)   # benches/attention.rs:406
+    PREFILL_LENS = (32, 64, 128, 256, 512, 1024, 2048)  # benches/attention.rs:380
+
+    def __init__(self, stream, seed, layers=6, hidden=2048):
+        self.stream, self.hidden = stream, hidden
+        ws = [v2lite_weights(seed + 11 * i, hidden) for i in range(layers)]
+        self.layers = [qmla.MlaLayer(w) for w in ws]
+        self.weight_bytes = weight_bytes_of(ws[0])
+        self.x = qmla.DeviceBuffer(2048 * hidden * 4)
+        qmla.check(qmla.lib().qmla_fill_normal_f32(self.x.ptr, 2048 * hidden, seed + 3, 0.0, 1.0,
+                                                   qmla._sh(stream)))
+        self.out = qmla.DeviceBuffer(2048 * hidden * 4)
+
+    def _caches(self, n, cap, fill_len):
+        tmp = qmla.DeviceBuffer(8 << 20)
+        cs = []
+        for i in range(n):
+            c = qmla.KVCache([cap], 512, 64, qmla.BF16)
+            if fill_len:
+                d = c.describe()
+                fill_bf16(d.rows, d.total_rows * ROW_ELEMS, 9000 + i, tmp, self.stream)
+                c.set_lengths([fill_len], self.stream)
+            cs.append(c)
+        self.stream.sync()
+        tmp.free()
+        return cs
+
+    def _point(self, fn, steps, warmup):
+        wall, ev = time_steps(fn, steps, warmup, self.stream)
+        return wall, ev, dict(STATS)
+
+    def decode(self, steps, warmup):
+        n = warmup + 2 * steps
+        pts = []
+        for L in self.DECODE_LENS:
+            caches = self._caches(n, L + 1, L)
+            wsb = self.layers[0].workspace_bytes(caches[0], 1, 1)
+            ws = qmla.DeviceBuffer(wsb)
+
+            def step(i, caches=caches, ws=ws, wsb=wsb):
+                qmla.check(qmla.lib().qmla_layer_forward_with_cache(
+                    self.layers[i % len(self.layers)].handle, self.x.ptr, 1, 1, caches[i].handle, self.out.ptr,
+                    ws.ptr, wsb, qmla._sh(self.stream)))
+
+            wall, ev, st = self._point(step, steps, warmup)
+            assert all(list(c.lengths()) == [L + 1] for c in caches)
+            pts.append({"cache_len": L, "us_per_token": ev * 1e3, "tok_s": 1e3 / ev,
+                        "median_us": st["median_ms"] * 1e3, "p10_us": st["p10_ms"] * 1e3,
+                        "p90_us": st["p90_ms"] * 1e3, "wall_us": wall * 1e3,
+                        "hbm_bytes": self.weight_bytes + (L + 1) * ROW_BYTES})
+            del caches, ws
+        return pts
+
+    def prefill(self, steps, warmup):
+        n = warmup + 2 * steps
+        pts = []
+        for S in self.PREFILL_LENS:
+            caches = self._caches(n, S, 0)
+            wsb = self.layers[0].prefill_workspace_bytes(caches[0], 1, S)
+            ws = qmla.DeviceBuffer(wsb)
+
+            def step(i, caches=caches, ws=ws, wsb=wsb, S=S):
+                qmla.check(qmla.lib().qmla_layer_forward_prefill(
+                    self.layers[i % len(self.layers)].handle, self.x.ptr, 1, S, caches[i].handle, self.out.ptr,
+                    ws.ptr, wsb, qmla._sh(self.stream)))
+
+            wall, ev, st = self._point(step, steps, warmup)
+            assert all(list(c.lengths()) == [S] for c in caches)
+            flops = (2 * S * self.hidden * (16 * 192 + 576 + 16 * 128) + 2 * S * 512 * 16 * 256
+                     + 16 * (S * (S + 1) // 2) * 2 * 320)
+            pts.append({"seq_len": S, "us_per_call": ev * 1e3, "tok_s": S / (ev * 1e-3),
+                        "median_us": st["median_ms"] * 1e3, "p10_us": st["p10_ms"] * 1e3,
+                        "p90_us": st["p90_ms"] * 1e3, "wall_us": wall * 1e3,
+                        "f32_equivalent_tflops": flops / (ev * 1e-3) / 1e12})
+            del caches, ws
+        return pts
+
+
+def cpu_baseline_batch1(min_seconds=1.0):
+    """The batch-1 sweeps on the host in the reference's own form (numpy
+    with BLAS matmuls: oracle.blas_layer_decode_step over the decompressed
+    per-head cache with KVCache::append's cat, oracle.blas_layer_prefill),
+    each point repeated for at least `min_seconds`."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O  # checker library, used here only as the CPU baseline
+
+    w = O.MlaWeights.random(2048, 16, 128, 64, 128, 512, seed=98)
+    th = blas_threads()
+    dec, pre = {}, {}
+    x1 = O.normal((1, 1, 2048), 99)
+    for L in Batch1Sweeps.DECODE_LENS:
+        k, v, kr = O.normal((1, 16, L, 128), 100), O.normal((1, 16, L, 128), 101), O.normal((1, 16, L, 64), 102)
+        per, reps = _repeat(lambda: O.blas_layer_decode_step(w, x1, k, v, kr), min_seconds)
+        dec[L] = {"us_per_token": per * 1e6, "runs": reps}
+    for S in Batch1Sweeps.PREFILL_LENS:
+        xs = O.normal((1, S, 2048), 103)
+        per, reps = _repeat(lambda: O.blas_layer_prefill(w, xs), min_seconds)
+        pre[S] = {"us_per_call": per * 1e6, "tok_s": S / per, "runs": reps}
+    return {"cores": th, "kind": "port", "cpu_model": cpu_model(),
+            "what": f"the reference's form in numpy on {th} BLAS threads: forward_with_cache with the "
+                    f"per-head f32 cache and its cat (oracle.blas_layer_decode_step), forward_prefill with "
+                    f"compute_kv and the tiled causal attention (oracle.blas_layer_prefill); each point "
+                    f"repeated for >= {min_seconds:.0f} s",
+            "decode": dec, "prefill": pre}
 
 
 def cpu_baseline_layer_prefill(min_seconds=5.0):
@@ -651,6 +796,8 @@ def main():
                     help="only run the MLA layer decode step line (for profiling)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only run the two prefill lines (for profiling)")
+    ap.add_argument("--sweeps-only", action="store_true",
+                    help="only run the batch-1 decode and prefill sweeps (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the decode path shards by batch "
@@ -670,6 +817,11 @@ def main():
     if args.layer_only:
         lb = LayerDecodeBench(stream, seed=51)
         print(json.dumps({"layer_decode_step": lb.run(args.steps, args.warmup)}), flush=True)
+        return
+    if args.sweeps_only:
+        sw = Batch1Sweeps(stream, seed=71)
+        print(json.dumps({"batch1_decode_sweep": sw.decode(args.steps, args.warmup),
+                          "batch1_prefill_sweep": sw.prefill(max(3, args.steps // 2), 3)}), flush=True)
         return
     if args.prefill_only:
         res = {}
@@ -730,6 +882,29 @@ def main():
             secondary["layer_prefill"]["cpu_baseline"] = cpu_baseline_layer_prefill()
         log("layer prefill", json.dumps(secondary["layer_prefill"]))
         del lp
+        sw = Batch1Sweeps(stream, seed=71)
+        dsw = sw.decode(args.steps, args.warmup)
+        psw = sw.prefill(max(3, args.steps // 2), 3)
+        del sw
+        cb1 = None if args.no_cpu_baseline else cpu_baseline_batch1()
+        if cb1:
+            for p in dsw:
+                p["cpu_baseline_us_per_token"] = cb1["decode"][p["cache_len"]]["us_per_token"]
+            for p in psw:
+                p["cpu_baseline_us_per_call"] = cb1["prefill"][p["seq_len"]]["us_per_call"]
+        secondary["batch1_decode_sweep"] = {
+            "workload": "batch 1, one new token, forward_with_cache at cache_len tokens (benches/attention.rs "
+                        "decode_throughput), hidden 2048, 16 heads, r 512, bf16 latent cache, f32 weights "
+                        "rotating over 6 layer copies; every call on its own cache of exactly cache_len tokens",
+            "points": dsw,
+            "cpu_baseline": None if cb1 is None else {k: cb1[k] for k in ("cores", "kind", "cpu_model", "what")}}
+        secondary["batch1_prefill_sweep"] = {
+            "workload": "batch 1, forward_prefill of seq_len tokens (benches/attention.rs prefill_throughput), "
+                        "hidden 2048, 16 heads, r 512, bf16 latent cache, f32 weights rotating over 6 layer "
+                        "copies",
+            "points": psw,
+            "cpu_baseline": None if cb1 is None else {k: cb1[k] for k in ("cores", "kind", "cpu_model", "what")}}
+        log("batch-1 sweeps", json.dumps({"decode": dsw, "prefill": psw}))
         mb = MoEBench(stream)
         moe = mb.run(args.steps, args.warmup)
         del mb

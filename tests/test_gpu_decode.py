@@ -135,8 +135,9 @@ def test_decode_bf16_v2lite_full(qmla_gpu):
 
 def test_decode_bf16_v3_ragged_full_size(qmla_gpu):
     """C4: batch 64, 128 heads, contexts U[1024, 32768] + 1 (seeded), bf16.
-    Full-size run; the oracle checks ten sequences (the shortest, the
-    longest and every ninth); split-count invariance covers the rest."""
+    Full-size run, every sequence checked against the oracle (~330 GFLOP of
+    host work, a few seconds on the oracle's OpenMP loops), then again with
+    another split count."""
     q = qmla_gpu
     lens = (O.uniform_int(64, 4, 1024, 32768) + 1).astype(np.int32)
     print(f"C4 tokens={int(lens.sum())} min={lens.min()} max={lens.max()}", flush=True)
@@ -154,8 +155,9 @@ def test_decode_bf16_v3_ragged_full_size(qmla_gpu):
     assert np.isfinite(out).all() and np.isfinite(lse).all()
     pool = cache.read_rows()
     offs = cache.offsets()
-    pick = [int(np.argmin(lens)), int(np.argmax(lens))] + list(range(0, 64, 9))
+    pick = list(range(64))
     rows = np.concatenate([bf16_to_f32(pool[offs[b]:offs[b] + lens[b]]) for b in pick])
+    del pool
     sel_lens = lens[pick]
     sel_offs = np.concatenate([[0], np.cumsum(sel_lens)[:-1]]).astype(np.int64)
     ref, rlse = O.decode_absorbed(ql[pick], qr[pick], rows, sel_offs, sel_lens, s)
@@ -170,6 +172,7 @@ def test_decode_bf16_v3_ragged_full_size(qmla_gpu):
     out2, lse2 = run(q, cache, ql, qr, s, splits=97)
     for i, b in enumerate(pick):
         assert rel_err(out2[b], ref[i]) < TOL_BF16
+        np.testing.assert_allclose(lse2[b], rlse[i], atol=2e-2)
     per_seq = [rel_err(out2[b], out[b]) for b in range(64)]
     print(f"C4 splits=97 vs default: max per-sequence rel_err={max(per_seq):.2e}", flush=True)
     assert max(per_seq) < 1e-2

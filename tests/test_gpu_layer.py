@@ -460,3 +460,33 @@ def test_layer_calls_from_several_threads(qmla_gpu):
     assert not errs, errs
     for i in range(4):
         np.testing.assert_array_equal(got[i], want[i])
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_layer_prefill_at_bench_widths(qmla_gpu, dt):
+    """forward_prefill at the widths the layer-prefill bench line runs:
+    hidden 2048, 16 heads, kv_lora_rank 512, dn 128 / dr 64 / dv 128, one
+    sequence of 2048 tokens (the split GEMM projections, the kv_b
+    decompression and the attention at full size), against the oracle's
+    decompressed path: 1e-4 with an f32 cache, 2e-2 with a bf16 cache.
+    Then one decode step on the filled cache."""
+    q = qmla_gpu
+    hidden, H, dn, dr, dv, r = 2048, 16, 128, 64, 128, 512
+    w = O.MlaWeights.random(hidden, H, dn, dr, dv, r, seed=1900)
+    layer = q.MlaLayer(w)
+    b, s = 1, 2048
+    xs = O.normal((b, s, hidden), 1901)
+    cache = q.KVCache([s + 1] * b, r, dr, q.F32 if dt == "f32" else q.BF16)
+    out = layer.forward_prefill(xs, cache)
+    ref, (k, v, kr) = O.mla_forward_prefill(w, xs)
+    tol = TOL if dt == "f32" else 2e-2
+    err = rel_err(out, ref)
+    print(f"layer prefill {b}x{s} hidden {hidden} {dt} cache rel_err={err:.2e}", flush=True)
+    assert err < tol
+    x1 = O.normal((b, 1, hidden), 1902)
+    out1 = layer.forward_with_cache(x1, cache)
+    ref1 = O.mla_forward_with_cache(w, x1, k, v, kr)
+    err1 = rel_err(out1, ref1)
+    print(f"decode step after it, {dt} cache rel_err={err1:.2e}", flush=True)
+    assert err1 < tol
+    assert list(cache.lengths()) == [s + 1] * b
