@@ -796,6 +796,8 @@ def main():
                     help="only run the MLA layer decode step line (for profiling)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only run the two prefill lines (for profiling)")
+    ap.add_argument("--layer-prefill-only", action="store_true",
+                    help="only run the MLA layer prefill line (for profiling)")
     ap.add_argument("--sweeps-only", action="store_true",
                     help="only run the batch-1 decode and prefill sweeps (for profiling)")
     args = ap.parse_args()
@@ -817,6 +819,10 @@ def main():
     if args.layer_only:
         lb = LayerDecodeBench(stream, seed=51)
         print(json.dumps({"layer_decode_step": lb.run(args.steps, args.warmup)}), flush=True)
+        return
+    if args.layer_prefill_only:
+        lp = LayerPrefillBench(stream, seed=61)
+        print(json.dumps({"layer_prefill": lp.run(max(3, args.steps // 5), 3)}), flush=True)
         return
     if args.sweeps_only:
         sw = Batch1Sweeps(stream, seed=71)

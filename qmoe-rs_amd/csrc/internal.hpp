@@ -224,6 +224,47 @@ bool skinny_supported(int M, int K);
 qmla_status launch_skinny_gemm(const SkinnyGemmArgs &a, hipStream_t stream,
                                const LatentRowsArgs *rows = nullptr, int n_rows = 0);
 
+// Projections of many token rows (split_gemm.hip): y[m][n] = sum_k x[m][k]
+// W[n][k] + bias[n], W in the fragment-major layout of skinny_pack (Z = 1),
+// f32-exact on bf16 MFMA.  Epilogue modes:
+constexpr int kSgEpiFinal = 0;  // y[m ldy + n], f32
+constexpr int kSgEpiQkv = 1;    // [q_proj | kv_a]: out0 = q_nope, out1 = roped q_rope
+                                //   ([b, H, s, d], bf16 or f32), kva f32 rows
+constexpr int kSgEpiKvb = 2;    // kv_b_proj: out0 = k [b, H, s, dn], out1 = v [b, H, s, dv]
+struct SplitGemmArgs {
+  const void *w_frag;  // fragment-major bf16 hi/lo records of W [N][K]
+  int M, N, K;
+  // x: f32 rows x[m ldx + k] (x_heads = 0), or the attention context
+  // [b, heads, seq, dv] as rows [b seq][heads dv] (x_heads = 1; bf16 when
+  // x_bf16, else f32)
+  const void *x;
+  int64_t ldx;
+  int x_heads, x_bf16;
+  const float *bias;  // [N] or null
+  int epi;
+  float *y;           // FINAL
+  int64_t ldy;
+  int out_bf16;       // QKV / KVB outputs in bf16 (else f32)
+  // row m is token s = m % seq of sequence b = m / seq
+  int seq, heads, dn, dr, dv;
+  void *out0, *out1;
+  float *kva;         // QKV: kv_a rows [M][kva_ld]
+  int64_t kva_ld;
+  const int32_t *lens;     // QKV: token s of sequence b sits at position lens[b] + s
+  const float *inv_freq;   // [dr / 2]
+  float mscale;
+};
+bool split_gemm_supported(int N, int K);
+// Rows from which the split GEMM runs its 256 x 256 tiles, and below which
+// the layer keeps its rocBLAS path (few rows stream the weights; the split
+// GEMM's tiles would leave most of the device idle).
+constexpr int kSplitGemmBigRows = 4096;
+constexpr int kSplitGemmMinRows = 128;
+// Scratch for the activation records of an [M][K] product.
+size_t split_gemm_pack_bytes(int M, int K);
+// Packs x into `pack` (split_gemm_pack_bytes(M, K) bytes), then runs the GEMM.
+qmla_status launch_split_gemm(const SplitGemmArgs &a, void *pack, hipStream_t stream);
+
 // Cache row writer shared by the cache API and the layer: copies/converts
 // n_seqs x n_new rows (row-major [n_seqs, n_new, row_elems]) into sequences
 // seq0 .. seq0 + n_seqs - 1 at their current device lengths, then advances

@@ -42,7 +42,8 @@ struct qmla_layer {
   //   wuk  [H][r][dn]                   W_UK^h transposed (kv_b rows h(dn+dv) .. +dn)
   //   wuv  [H][dv][r]                   W_UV^h (kv_b rows h(dn+dv)+dn .. +dv)
   //   wo   [hidden][H dv]               o_proj
-  void *w1f = nullptr, *wukf = nullptr, *wuvf = nullptr, *wof = nullptr;
+  //   wkvb [H(dn+dv)][r]               kv_b_proj (the prefill's compute_kv)
+  void *w1f = nullptr, *wukf = nullptr, *wuvf = nullptr, *wof = nullptr, *wkvbf = nullptr;
   float *b1 = nullptr;   // [bq | bkva]
   float *buv = nullptr;  // [H][dv]: b_V^h
   bool skinny = false;   // the split weights exist (every K a multiple of 16)
@@ -505,8 +506,19 @@ qmla_status make_skinny_weights(qmla_layer *L, const float *wq, const float *bq,
       for (int i = 0; i < dv; ++i) b[(size_t)h * dv + i] = bkvb[(size_t)h * (dn + dv) + dn + i];
   QMLA_TRY(upload(b.data(), b.size() * 4, (void **)&L->buv));
   QMLA_TRY(put(wo, (int64_t)H * dv, 0, hid, H * dv, 1, &L->wof));
+  QMLA_TRY(put(wkvb, r, 0, H * (dn + dv), r, 1, &L->wkvbf));
   L->skinny = true;
   return QMLA_OK;
+}
+
+// forward_prefill runs its projections on the split GEMM (split_gemm.hip)
+// when the fragment-major weights exist and every product's widths suit it.
+bool use_split_gemm(const qmla_layer *L) {
+  const auto &g = L->cfg;
+  const int H = g.heads, dn = g.qk_nope, dr = g.qk_rope, dv = g.v_dim, r = g.kv_lora_rank;
+  return L->skinny && L->wkvbf && split_gemm_supported(H * (dn + dr) + r + dr, g.hidden) &&
+         split_gemm_supported(H * (dn + dv), r) && split_gemm_supported(g.hidden, H * dv) &&
+         dn % 4 == 0 && dr % 4 == 0 && dv % 32 == 0;
 }
 
 // The decode step runs its projections on the skinny kernel when every
@@ -545,7 +557,7 @@ SkinnyGemmArgs skinny_args(const void *w_frag, const float *x, int64_t ldx, int6
 inline size_t al(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct LayerWs {
-  size_t q, kva, rows, qn, qr, qlat, olat, o, dec, kvb, k, v, kr, ctx, part, part_elems, xsplit,
+  size_t q, kva, rows, qn, qr, qlat, olat, o, dec, kvb, k, v, kr, ctx, pack, part, part_elems, xsplit,
       qn1, qr1, kva1,
       total;
 };
@@ -580,7 +592,7 @@ LayerWs layer_ws(const qmla_layer *L, int32_t batch, int32_t seq, size_t dec_byt
                                           (size_t)(g.kv_lora_rank + g.qk_rope), (size_t)g.hidden});
   w.part_elems = n <= (size_t)kSkinnyRows ? 16 * n * widest : 0;
   w.part = take(sizeof(float) * (w.part_elems ? w.part_elems : 1));
-  // bf16 halves of a projection's activations (split GEMMs, many rows)
+  // bf16 halves of a projection's activations (rocBLAS split GEMMs, many rows)
   const size_t kmax = std::max<size_t>({(size_t)g.hidden, H * g.v_dim, (size_t)g.kv_lora_rank});
   w.xsplit = take(n >= (size_t)kSplitRows ? split_bytes((int64_t)n, (int64_t)kmax) : 1);
   const size_t shared = off;
@@ -605,6 +617,10 @@ LayerWs layer_ws(const qmla_layer *L, int32_t batch, int32_t seq, size_t dec_byt
     w.v = take(sizeof(float) * n * H * g.v_dim);
     w.kr = take(sizeof(float) * n * g.qk_rope + 4);
     w.ctx = take(sizeof(float) * n * H * g.v_dim);
+    // the activation records of the hand-written split GEMM
+    w.pack = take(use_split_gemm(L) && n >= (size_t)kSplitGemmMinRows
+                      ? split_gemm_pack_bytes((int)n, (int)kmax)
+                      : 1);
     pre_end = off;
   }
   w.total = std::max(dec_end, pre_end);
@@ -1012,17 +1028,89 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
   hipStream_t s = as_stream(stream);
   const int n = batch * seq;
 
+  // With a bf16 cache the attention runs on the bf16 MFMA prefill: q, k, v
+  // and k_rope are written in bf16 (round to nearest even) into the same
+  // regions.  An f32 cache keeps the f32 path throughout.
+  const bool bfa = cache->dtype == QMLA_BF16 && prefill_bf16_supported(dn, dr, dv);
+  if (use_split_gemm(L) && n >= kSplitGemmMinRows) {
+    // Four launches around the attention, all hand-written:
+    //   q_proj | kv_a (q split per head and roped in the epilogue, kv_a rows
+    //   raw) -> latent rows (LayerNorm, RoPE, cache write) -> kv_b_proj (k, v
+    //   per head in the epilogue) -> attention -> o_proj (reading the
+    //   head-major context directly)
+    SplitGemmArgs a{};
+    a.M = n;
+    a.seq = seq;
+    a.heads = H;
+    a.dn = dn;
+    a.dr = dr;
+    a.dv = dv;
+    a.out_bf16 = bfa ? 1 : 0;
+    SplitGemmArgs qa = a;
+    qa.w_frag = L->w1f;
+    qa.N = H * (dn + dr) + r + dr;
+    qa.K = g.hidden;
+    qa.x = xs;
+    qa.ldx = g.hidden;
+    qa.bias = L->b1;
+    qa.epi = kSgEpiQkv;
+    qa.out0 = qn;
+    qa.out1 = qr;
+    qa.kva = kva;
+    qa.kva_ld = r + dr;
+    qa.lens = cache->d_lens;  // 0 here: forward_prefill starts its sequences
+    qa.inv_freq = L->inv_freq;
+    qa.mscale = (float)g.rope_mscale;
+    void *pack = ws + w.pack;
+    QMLA_TRY(launch_split_gemm(qa, pack, s));
+    QMLA_TRY(latent_to_cache(L, kva, batch, seq, rows, cache, s));
+    SplitGemmArgs ka = a;
+    ka.w_frag = L->wkvbf;
+    ka.N = H * (dn + dv);
+    ka.K = r;
+    ka.x = rows;
+    ka.ldx = r + dr;
+    ka.bias = L->bkvb;
+    ka.epi = kSgEpiKvb;
+    ka.out0 = k;
+    ka.out1 = v;
+    QMLA_TRY(launch_split_gemm(ka, pack, s));
+    qmla_prefill_dims pd{batch, H, seq, seq, dn, dr, dv, 1, 0};
+    if (bfa) {
+      if (dr > 0) {
+        k_rows_rope<uint16_t><<<dim3(n), dim3(64), 0, s>>>(rows, r, dr, (uint16_t *)kr);
+        QMLA_LAUNCH_CHECK("k_rows_rope");
+      }
+      QMLA_TRY(launch_prefill_bf16(pd, (const uint16_t *)qn, (const uint16_t *)qr,
+                                   (const uint16_t *)k, (const uint16_t *)kr, (const uint16_t *)v,
+                                   (float)g.softmax_scale, 1, (uint16_t *)ctx, s));
+    } else {
+      if (dr > 0) {
+        k_rows_rope<float><<<dim3(n), dim3(64), 0, s>>>(rows, r, dr, kr);
+        QMLA_LAUNCH_CHECK("k_rows_rope");
+      }
+      QMLA_TRY(launch_prefill_f32(pd, qn, qr, k, kr, v, (float)g.softmax_scale, 1, ctx, s));
+    }
+    SplitGemmArgs oa = a;
+    oa.w_frag = L->wof;
+    oa.N = g.hidden;
+    oa.K = H * dv;
+    oa.x = ctx;
+    oa.x_heads = 1;
+    oa.x_bf16 = bfa ? 1 : 0;
+    oa.bias = L->bo;
+    oa.epi = kSgEpiFinal;
+    oa.y = out;
+    oa.ldy = g.hidden;
+    return launch_split_gemm(oa, pack, s);
+  }
+
   void *xsp = ws + w.xsplit;
   // q_proj and kv_a_proj_with_mqa share one split of xs
   QMLA_TRY(project(L, xs, n, g.hidden, L->wq, L->wq_x, L->bq, H * (dn + dr), q, s, part,
                    w.part_elems, xsp));
   QMLA_TRY(project(L, xs, n, g.hidden, L->wkva, L->wkva_x, L->bkva, r + dr, kva, s, part,
                    w.part_elems, xsp, false));
-  // With a bf16 cache the attention runs on the bf16 MFMA prefill: q, k, v
-  // and k_rope are written in bf16 (round to nearest even) into the same
-  // regions, and the bf16 context is widened again when the heads merge.
-  // An f32 cache keeps the f32 path throughout.
-  const bool bfa = cache->dtype == QMLA_BF16 && prefill_bf16_supported(dn, dr, dv);
   if (bfa)
     k_split_rope_q<uint16_t><<<dim3(n, H), dim3(64), 0, s>>>(
         q, seq, H, dn, dr, L->inv_freq, (float)g.rope_mscale, cache->d_lens, 1, (uint16_t *)qn,

@@ -1,0 +1,401 @@
+// split_gemm.hip -- the projections of an MLA layer call over many token
+// rows (MlaAttention::forward_prefill, src/model.rs:197-249: q_proj with
+// kv_a_proj_with_mqa, kv_b_proj inside compute_kv, o_proj) as f32-exact
+// GEMMs on bf16 MFMA, with the layer's layout work fused into the epilogue.
+//
+// y[m][n] = sum_k x[m][k] W[n][k] + b[n] in the split form of
+// skinny_gemm.hip: every operand is stored as bf16 halves, hi = bf16(v) and
+// lo = bf16(v - hi), and every 32 x 32 x 16 step is three
+// v_mfma_f32_32x32x16_bf16 with f32 accumulation:
+//   x w = x_hi w_hi + x_lo w_hi + x_hi w_lo   (x_lo w_lo < 2^-16 |x w|)
+// When x is bf16 (the bf16 attention's context) x_lo is zero: the x records
+// carry no lo half and the second product is skipped.
+//
+// Operands as fragment-major records.  A record is one MFMA operand of a
+// 32-row block and a 16-wide k-step, exactly as the wave's lanes read it:
+// lane l's 16 bytes are the 8 bf16 values of row 32 b + l % 32 at k = 16 ks
+// + 8 (l / 32) .. + 7, first the hi halves of the 64 lanes (1 KB), then the
+// lo halves (1 KB).  The weights are packed once when the layer is created
+// (skinny_pack); the activations are packed per call by k_pack_rows (a
+// pass that reads x once), so that the GEMM moves both operands with
+// direct-to-LDS DMA of contiguous 1 KB runs and holds nothing in flight in
+// registers.
+//
+// Block: 8 waves (two per SIMD) on a BN x BM output tile; wave (wn, wm)
+// owns NBW 32-output blocks x MBW 32-row blocks (BN = 32 NBW WN, BM = 32
+// MBW WM).  K goes in chunks of KSC k-steps through an NST-deep LDS ring:
+// the DMA of chunk c + NST - 1 is issued while chunk c is multiplied,
+// spread over its MFMAs, and one barrier per chunk publishes the next
+// stage and frees the oldest.  Blocks are dealt to XCDs in groups of tiles
+// that share weights and activations (see the tile order below).  Many
+// rows run 256 x 256 tiles (each wave 128 outputs x 64 rows, one k-step per
+// chunk, three stages: 96 KB of LDS); fewer rows 64 x 128 tiles.
+//
+// Epilogues (lane l of a 32 x 32 accumulator holds row m = l % 32 and
+// outputs n = 8 (j / 4) + 4 (l / 32) + j % 4, j < 16: four runs of 4
+// consecutive outputs):
+//   FINAL  y[m ldy + n] (+ bias), f32
+//   QKV    [q_proj | kv_a_proj_with_mqa]: q_nope and the roped q_rope in
+//          the attention's [b, H, s, d] layout (positions lens[b] + s,
+//          src/model.rs:199-203), bf16 or f32; the raw kv_a rows f32
+//   KVB    kv_b_proj: k [b, H, s, dn] and v [b, H, s, dv] (compute_kv's
+//          reshape and transpose, src/model.rs:181-188, :213-215)
+#include <cmath>
+#include <type_traits>
+#include <utility>
+
+#include "mfma_pipe.hpp"
+
+namespace qmla {
+
+namespace {
+
+constexpr int kSgThreads = 512;      // 8 waves
+constexpr int kSgGn = 4, kSgGm = 8;  // tiles of an XCD group (n x m)
+constexpr int kFrag = 2048;          // one record: hi 1 KB, lo 1 KB
+
+// Barrier after this wave's LDS traffic has completed, without a memory
+// fence (the DMA in flight stays in flight).
+__device__ __forceinline__ void sg_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+}
+
+template <typename T>
+__device__ __forceinline__ void sg_put4(T *p, const float (&v)[4]);
+
+template <>
+__device__ __forceinline__ void sg_put4<float>(float *p, const float (&v)[4]) {
+  *reinterpret_cast<floatx4_t *>(p) = floatx4_t{v[0], v[1], v[2], v[3]};
+}
+
+template <>
+__device__ __forceinline__ void sg_put4<uint16_t>(uint16_t *p, const float (&v)[4]) {
+  u32x2_t w;
+  w[0] = pack_bf16x2(v[0], v[1]);
+  w[1] = pack_bf16x2(v[2], v[3]);
+  *reinterpret_cast<u32x2_t *>(p) = w;
+}
+
+// ---- activation records.  Record (mb, ks) of x: lane l holds x[32 mb + l %
+// 32][16 ks + 8 (l / 32) .. + 7]; rows past M are zero.  One thread per
+// lane of a record, 4 records per 256-thread block.  XM: kSgXRow f32 rows
+// x[m ldx + k]; kSgXHeads* the attention context [b, H, s, dv] read as the
+// row [b s][H dv] (k = h dv + d), bf16 (records without lo halves) or f32.
+constexpr int kSgXRow = 0, kSgXHeadsBf16 = 1, kSgXHeadsF32 = 2;
+
+template <int XM>
+__global__ __launch_bounds__(256) void k_pack_rows(SplitGemmArgs a, uint8_t *__restrict__ rec) {
+  constexpr bool LO = XM != kSgXHeadsBf16;
+  constexpr int RB = LO ? 2048 : 1024;  // bytes per record
+  const int KS = a.K / 16;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t nrec = (int64_t)((a.M + 31) / 32) * KS;
+  if (r >= nrec) return;
+  const int lane = threadIdx.x & 63;
+  const int mb = (int)(r / KS), ks = (int)(r - (int64_t)mb * KS);
+  const int m = mb * 32 + (lane & 31), k = ks * 16 + 8 * (lane >> 5);
+  uint8_t *dst = rec + r * RB + lane * 16;
+  if (m >= a.M) {
+    *reinterpret_cast<u32x4_t *>(dst) = u32x4_t{0, 0, 0, 0};
+    if constexpr (LO) *reinterpret_cast<u32x4_t *>(dst + 1024) = u32x4_t{0, 0, 0, 0};
+    return;
+  }
+  if constexpr (XM == kSgXHeadsBf16) {
+    const int b = m / a.seq, s = m - b * a.seq, hd = k / a.dv;
+    const uint16_t *src = reinterpret_cast<const uint16_t *>(a.x) +
+                          (((int64_t)b * a.heads + hd) * a.seq + s) * a.dv + (k - hd * a.dv);
+    *reinterpret_cast<u32x4_t *>(dst) = *reinterpret_cast<const u32x4_t *>(src);
+  } else {
+    const float *src;
+    if constexpr (XM == kSgXRow) {
+      src = reinterpret_cast<const float *>(a.x) + (int64_t)m * a.ldx + k;
+    } else {
+      const int b = m / a.seq, s = m - b * a.seq, hd = k / a.dv;
+      src = reinterpret_cast<const float *>(a.x) + (((int64_t)b * a.heads + hd) * a.seq + s) * a.dv +
+            (k - hd * a.dv);
+    }
+    const floatx4_t v0 = *reinterpret_cast<const floatx4_t *>(src);
+    const floatx4_t v1 = *reinterpret_cast<const floatx4_t *>(src + 4);
+    const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+    u32x4_t hi, lo;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t h0 = f32_to_bf16_bits(v[2 * i]), h1 = f32_to_bf16_bits(v[2 * i + 1]);
+      hi[i] = h0 | ((uint32_t)h1 << 16);
+      const uint16_t l0 = f32_to_bf16_bits(v[2 * i] - bf16_bits_to_f32(h0));
+      const uint16_t l1 = f32_to_bf16_bits(v[2 * i + 1] - bf16_bits_to_f32(h1));
+      lo[i] = l0 | ((uint32_t)l1 << 16);
+    }
+    *reinterpret_cast<u32x4_t *>(dst) = hi;
+    *reinterpret_cast<u32x4_t *>(dst + 1024) = lo;
+  }
+}
+
+// Tile shape and pipeline of one instantiation: NBW x MBW 32-blocks per
+// wave, WN waves along N (8 / WN along M), KSC k-steps of 16 per chunk and
+// NST chunks in the LDS ring.
+template <int NBW_, int MBW_, int WN_, int KSC_, int NST_>
+struct SgCfg {
+  static constexpr int NBW = NBW_, MBW = MBW_, WN = WN_, KSC = KSC_, NST = NST_;
+};
+
+template <class CF, bool XLO, int EPI, typename OutT>
+__global__ __launch_bounds__(kSgThreads) void k_split_gemm(SplitGemmArgs a, const uint8_t *xrec) {
+  constexpr int NBW = CF::NBW, MBW = CF::MBW, WN = CF::WN, KSC = CF::KSC, NST = CF::NST;
+  constexpr int WM = 8 / WN;
+  constexpr int MBT = MBW * WM, NBT = NBW * WN;  // 32-row / 32-output blocks of the tile
+  constexpr int BM = 32 * MBT, BN = 32 * NBT;
+  constexpr int XR = XLO ? 2048 : 1024;           // bytes per activation record
+  constexpr int WSEG = KSC * NBT * kFrag;         // a stage's weight records
+  constexpr int STAGE = WSEG + KSC * MBT * XR;    // ... and activation records
+  constexpr int NDMA = STAGE / 1024;              // DMA instructions per chunk
+  static_assert(NDMA % 8 == 0, "DMA slots per wave");
+  constexpr int DW = NDMA / 8;                    // ... per wave
+  extern __shared__ __attribute__((aligned(16))) char sg_lds[];
+  const uint32_t ring_u = (uint32_t)(uintptr_t)(sg_lds);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave % WN, wm = wave / WN;
+  // XCD-aware tile order: blocks are dealt to the 8 XCDs round-robin, so
+  // the k-th block of XCD x is blockIdx.x = 8 k + x.  Each XCD takes groups
+  // of kSgGn x kSgGm tiles (group g = 8 (k / G) + x, G = kSgGn kSgGm); the G
+  // blocks of a group run together on one XCD and advance through K side by
+  // side, so each chunk of a weight tile or activation tile comes from
+  // memory once and is re-read from that XCD's L2 by the group's other
+  // blocks.
+  const int NT = (a.N + BN - 1) / BN, MT = (a.M + BM - 1) / BM;
+  const int GNT = (NT + kSgGn - 1) / kSgGn;
+  const int L = blockIdx.x, xcd = L & 7, kk = L >> 3;
+  const int grp = (kk / (kSgGn * kSgGm)) * 8 + xcd, pos = kk % (kSgGn * kSgGm);
+  const int bn = (grp % GNT) * kSgGn + pos % kSgGn, bm = (grp / GNT) * kSgGm + pos / kSgGn;
+  if (bn >= NT || bm >= MT) return;  // a slot of a partial group
+  const int NB = (a.N + 31) / 32, MB = (a.M + 31) / 32, KS = a.K / 16, NC = KS / KSC;
+
+  // DMA slot u of this wave: instruction i = wave DW + u of the chunk.
+  // Instructions [0, 2 KSC NBT) move weight records (record j KSC + ks of
+  // tile block j, hi then lo), the rest activation records (tile row block
+  // j, k-step ks, hi [then lo]).  Tile blocks past N or M re-load the last
+  // block (their outputs are dropped).
+  auto dma_one = [&](int c, int u) __attribute__((always_inline)) {
+    const uint32_t st = ring_u + (uint32_t)((c % NST) * STAGE);
+    {
+      const int i = wave * DW + u;
+      const uint8_t *src;
+      if (i < 2 * KSC * NBT) {
+        const int rec = i >> 1, half = i & 1, j = rec / KSC, ks = rec % KSC;
+        const int nb = min(bn * NBT + j, NB - 1);
+        src = reinterpret_cast<const uint8_t *>(a.w_frag) +
+              ((int64_t)nb * KS + KSC * c + ks) * kFrag + half * 1024;
+      } else {
+        const int xi = i - 2 * KSC * NBT;
+        const int rec = XLO ? xi >> 1 : xi, half = XLO ? xi & 1 : 0;
+        const int j = rec / KSC, ks = rec % KSC;
+        const int mb = min(bm * MBT + j, MB - 1);
+        src = xrec + ((int64_t)mb * KS + KSC * c + ks) * XR + half * 1024;
+      }
+      pipe::dma16(pipe::fresh(src), (uint32_t)(lane * 16), pipe::fresh(st + (uint32_t)(i * 1024)));
+    }
+  };
+  auto dma = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < DW; ++u) dma_one(c, u);
+  };
+
+  floatx16_t acc[NBW][MBW];
+#pragma unroll
+  for (int i = 0; i < NBW; ++i)
+#pragma unroll
+    for (int j = 0; j < MBW; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Chunk c's products.  With dc >= 0, the DMA slots of chunk dc are spread
+  // over the products (slot u after output pair u * PAIRS / DW): a DMA
+  // instruction stalls its wave's issue while the memory system is busy,
+  // and spread out it stalls between MFMAs instead of ahead of them.
+  constexpr int PAIRS = KSC * NBW * MBW;
+  auto compute = [&](int c, int dc) __attribute__((always_inline)) {
+    const char *st = sg_lds + (c % NST) * STAGE + lane * 16;
+#pragma unroll
+    for (int ks = 0; ks < KSC; ++ks) {
+      bf16x8_t xh[MBW], xl[MBW], wh[NBW], wl[NBW];
+#pragma unroll
+      for (int i = 0; i < NBW; ++i) {
+        const char *f = st + ((wn * NBW + i) * KSC + ks) * kFrag;
+        wh[i] = *reinterpret_cast<const bf16x8_t *>(f);
+        wl[i] = *reinterpret_cast<const bf16x8_t *>(f + 1024);
+      }
+#pragma unroll
+      for (int j = 0; j < MBW; ++j) {
+        const char *f = st + WSEG + ((wm * MBW + j) * KSC + ks) * XR;
+        xh[j] = *reinterpret_cast<const bf16x8_t *>(f);
+        if constexpr (XLO) xl[j] = *reinterpret_cast<const bf16x8_t *>(f + 1024);
+      }
+#pragma unroll
+      for (int i = 0; i < NBW; ++i)
+#pragma unroll
+        for (int j = 0; j < MBW; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wh[i], xh[j], acc[i][j], 0, 0, 0);
+          if constexpr (XLO)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wh[i], xl[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wl[i], xh[j], acc[i][j], 0, 0, 0);
+          const int pr = (ks * NBW + i) * MBW + j;
+#pragma unroll
+          for (int u = 0; u < DW; ++u)
+            if (dc >= 0 && (u * PAIRS) / DW == pr) dma_one(dc, u);
+        }
+    }
+  };
+
+  // ---- pipeline: before chunk c is multiplied, this wave's DMA for it
+  // must be done (the DW instructions of each of the up to NST - 2 later
+  // chunks already requested may stay in flight), then a barrier publishes
+  // every wave's share and, since every wave is past chunk c - 1, frees its
+  // stage for chunk c + NST - 1.
+  static_assert((NST - 2) * DW < 64, "vmcnt range");
+#pragma unroll
+  for (int p = 0; p < NST - 1; ++p)
+    if (p < NC) dma(p);
+  for (int c = 0; c < NC; ++c) {
+    pipe::wait_vmcnt_dyn(min(NST - 2, NC - 1 - c) * DW);
+    sg_barrier();
+    compute(c, c + NST - 1 < NC ? c + NST - 1 : -1);
+  }
+
+  // ---- epilogue: one call per (output block, row block), with
+  // compile-time indices so that the accumulators stay in registers
+  const int half = lane >> 5, mr = lane & 31;
+  auto emit = [&](const floatx16_t &v16, int nb, int m) __attribute__((always_inline)) {
+    if (m >= a.M) return;
+    const int b = m / a.seq, s = m - b * a.seq;
+#pragma unroll
+    for (int jq = 0; jq < 4; ++jq) {
+      const int n0 = nb * 32 + 8 * jq + 4 * half;
+      if (n0 >= a.N) continue;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = v16[4 * jq + e] + (a.bias ? a.bias[n0 + e] : 0.f);
+      if constexpr (EPI == kSgEpiFinal) {
+        sg_put4<float>(a.y + (int64_t)m * a.ldy + n0, v);
+      } else if constexpr (EPI == kSgEpiQkv) {
+        const int qw = a.dn + a.dr, nq = a.heads * qw;
+        if (n0 >= nq) {
+          sg_put4<float>(a.kva + (int64_t)m * a.kva_ld + (n0 - nq), v);
+          continue;
+        }
+        const int hd = n0 / qw, d = n0 - hd * qw;
+        const int64_t row = ((int64_t)b * a.heads + hd) * a.seq + s;
+        if (d < a.dn) {
+          sg_put4<OutT>(reinterpret_cast<OutT *>(a.out0) + row * a.dn + d, v);
+        } else {
+          // interleaved pairs (2p, 2p + 1) of q_rope (src/model.rs:70-84)
+          const int p = (d - a.dn) >> 1;
+          const float pos = (float)(a.lens[b] + s);
+          float r[4];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const float ang = pos * a.inv_freq[p + u];
+            const float cs = cosf(ang) * a.mscale, sn = sinf(ang) * a.mscale;
+            r[2 * u] = v[2 * u] * cs - v[2 * u + 1] * sn;
+            r[2 * u + 1] = v[2 * u + 1] * cs + v[2 * u] * sn;
+          }
+          sg_put4<OutT>(reinterpret_cast<OutT *>(a.out1) + row * a.dr + (d - a.dn), r);
+        }
+      } else {  // kSgEpiKvb
+        const int kw = a.dn + a.dv;
+        const int hd = n0 / kw, d = n0 - hd * kw;
+        const int64_t row = ((int64_t)b * a.heads + hd) * a.seq + s;
+        if (d < a.dn)
+          sg_put4<OutT>(reinterpret_cast<OutT *>(a.out0) + row * a.dn + d, v);
+        else
+          sg_put4<OutT>(reinterpret_cast<OutT *>(a.out1) + row * a.dv + (d - a.dn), v);
+      }
+    }
+  };
+  [&]<int... IJ>(std::integer_sequence<int, IJ...>) {
+    (emit(acc[IJ / MBW][IJ % MBW], bn * NBT + wn * NBW + IJ / MBW,
+          bm * BM + (wm * MBW + IJ % MBW) * 32 + mr),
+     ...);
+  }(std::make_integer_sequence<int, NBW * MBW>{});
+}
+
+template <class CF, bool XLO>
+constexpr size_t sg_lds_bytes() {
+  constexpr int MBT = CF::MBW * (8 / CF::WN), NBT = CF::NBW * CF::WN;
+  return (size_t)CF::NST * CF::KSC * (NBT * kFrag + MBT * (XLO ? 2048 : 1024));
+}
+
+template <class CF, bool XLO>
+qmla_status sg_launch(const SplitGemmArgs &a, const uint8_t *xrec, hipStream_t s) {
+  constexpr int BN = 32 * CF::NBW * CF::WN, BM = 32 * CF::MBW * (8 / CF::WN);
+  static_assert(sg_lds_bytes<CF, XLO>() <= 160 * 1024, "LDS");
+  // whole groups of kSgGn x kSgGm tile slots, dealt to the 8 XCDs
+  const int64_t gn = ((a.N + BN - 1) / BN + kSgGn - 1) / kSgGn;
+  const int64_t gm = ((a.M + BM - 1) / BM + kSgGm - 1) / kSgGm;
+  const int64_t groups = (gn * gm + 7) / 8 * 8;
+  const int64_t blocks = groups * kSgGn * kSgGm;
+  QMLA_REQUIRE(blocks <= 0x7fffffff, QMLA_ERR_SHAPE, "split GEMM grid of %lld blocks",
+               (long long)blocks);
+  const size_t lds = sg_lds_bytes<CF, XLO>();
+  auto go = [&](auto kern) -> qmla_status {
+    QMLA_TRY(ensure_dynamic_lds((const void *)kern, lds));
+    kern<<<dim3((unsigned)blocks), dim3(kSgThreads), lds, s>>>(a, xrec);
+    QMLA_LAUNCH_CHECK("k_split_gemm");
+    return QMLA_OK;
+  };
+  switch (a.epi) {
+    case kSgEpiQkv:
+      if (a.out_bf16) return go(k_split_gemm<CF, XLO, kSgEpiQkv, uint16_t>);
+      return go(k_split_gemm<CF, XLO, kSgEpiQkv, float>);
+    case kSgEpiKvb:
+      if (a.out_bf16) return go(k_split_gemm<CF, XLO, kSgEpiKvb, uint16_t>);
+      return go(k_split_gemm<CF, XLO, kSgEpiKvb, float>);
+    default:
+      return go(k_split_gemm<CF, XLO, kSgEpiFinal, float>);
+  }
+}
+
+}  // namespace
+
+bool split_gemm_supported(int N, int K) { return N > 0 && N % 4 == 0 && K > 0 && K % 32 == 0; }
+
+size_t split_gemm_pack_bytes(int M, int K) {
+  return (size_t)((M + 31) / 32) * (K / 16) * kFrag;
+}
+
+qmla_status launch_split_gemm(const SplitGemmArgs &a, void *pack, hipStream_t s) {
+  QMLA_REQUIRE(split_gemm_supported(a.N, a.K) && a.M > 0, QMLA_ERR_UNSUPPORTED,
+               "split GEMM M %d N %d K %d", a.M, a.N, a.K);
+  QMLA_REQUIRE(a.seq > 0 && pack, QMLA_ERR_SHAPE, "split GEMM seq %d / no pack buffer", a.seq);
+  QMLA_REQUIRE(a.x_heads == 0 || (a.dv > 0 && a.dv % 16 == 0 && a.K == a.heads * a.dv),
+               QMLA_ERR_SHAPE, "split GEMM head-major x: dv %d, K %d", a.dv, a.K);
+  QMLA_REQUIRE(a.epi != kSgEpiQkv || (a.dn % 4 == 0 && a.dr % 4 == 0 && a.lens && a.inv_freq),
+               QMLA_ERR_SHAPE, "split GEMM q split needs widths that are multiples of 4");
+  QMLA_REQUIRE(a.epi != kSgEpiKvb || (a.dn % 4 == 0 && a.dv % 4 == 0), QMLA_ERR_SHAPE,
+               "split GEMM k/v split needs widths that are multiples of 4");
+  // the activations as records (one pass over x)
+  const int64_t recs = (int64_t)((a.M + 31) / 32) * (a.K / 16);
+  QMLA_REQUIRE(recs / 4 + 1 <= 0x7fffffff, QMLA_ERR_SHAPE, "split GEMM pack grid");
+  uint8_t *xrec = static_cast<uint8_t *>(pack);
+  const dim3 pg((unsigned)((recs + 3) / 4)), pb(256);
+  const bool xlo = !(a.x_heads && a.x_bf16);
+  if (a.x_heads == 0)
+    k_pack_rows<kSgXRow><<<pg, pb, 0, s>>>(a, xrec);
+  else if (a.x_bf16)
+    k_pack_rows<kSgXHeadsBf16><<<pg, pb, 0, s>>>(a, xrec);
+  else
+    k_pack_rows<kSgXHeadsF32><<<pg, pb, 0, s>>>(a, xrec);
+  QMLA_LAUNCH_CHECK("k_pack_rows");
+  // Many rows: 256 x 256 tiles; fewer: 64 x 128 tiles, so that the grid
+  // still fills the device (at 2048 rows a 256 x 256 tiling of q_proj |
+  // kv_a has 120 blocks).
+  using Big = SgCfg<4, 2, 2, 1, 3>;
+  using Small = SgCfg<1, 1, 2, 2, 3>;
+  if (a.M >= kSplitGemmBigRows)
+    return xlo ? sg_launch<Big, true>(a, xrec, s) : sg_launch<Big, false>(a, xrec, s);
+  return xlo ? sg_launch<Small, true>(a, xrec, s) : sg_launch<Small, false>(a, xrec, s);
+}
+
+}  // namespace qmla
