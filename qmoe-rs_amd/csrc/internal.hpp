@@ -264,6 +264,9 @@ constexpr int kSplitGemmMinRows = 128;
 size_t split_gemm_pack_bytes(int M, int K);
 // Packs x into `pack` (split_gemm_pack_bytes(M, K) bytes), then runs the GEMM.
 qmla_status launch_split_gemm(const SplitGemmArgs &a, void *pack, hipStream_t stream);
+// The GEMM over activation records a producer already wrote (f32 x split
+// into hi/lo records of split_gemm_pack_bytes(M, K) bytes; a.x unused).
+qmla_status launch_split_gemm_packed(const SplitGemmArgs &a, const void *xrec, hipStream_t stream);
 
 // Cache row writer shared by the cache API and the layer: copies/converts
 // n_seqs x n_new rows (row-major [n_seqs, n_new, row_elems]) into sequences

@@ -296,6 +296,117 @@ __global__ __launch_bounds__(256) void k_latent_rows(LatentRowsArgs a) {
   latent_row(a, blockIdx.x, lds);
 }
 
+// forward_prefill's latent rows (src/model.rs:206-219), one wave per token:
+// the cache row [LayerNorm(c) | rope(k_pe)] at position i of its (empty)
+// sequence; the split GEMM's activation records of LayerNorm(c) (kv_b_proj's
+// input, K = r: record (tok / 32, c / 16), lane tok % 32 + 32 ((c / 8) % 2),
+// hi and lo halves); and rope(k_pe) as the attention's k_rope [b, 1, s, dr]
+// in bf16 or f32.  The sequences start empty (forward_prefill checks it),
+// so positions are the token indices, lens is not read, and the wave of
+// each sequence's token 0 sets its length to s.  The grid covers n rounded
+// up to 32 tokens (the padding rows of the records are zeroed).  r % 32 == 0,
+// r <= 2048, dr % 8 == 0.
+template <typename KT>
+__global__ __launch_bounds__(256) void k_prefill_rows(LatentRowsArgs a, int n, uint8_t *rec,
+                                                      KT *k_rope, int32_t *lens) {
+  const int tok = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int r = a.r, dr = a.dr, C8 = r / 8, KS = r / 16;
+  if (tok >= n) {
+    // the padding rows of the last 32-row record group: zeros
+    if (tok >= (n + 31) / 32 * 32) return;
+    for (int c8 = lane; c8 < C8; c8 += 64) {
+      uint8_t *rp =
+          rec + ((int64_t)(tok >> 5) * KS + (c8 >> 1)) * 2048 + ((tok & 31) + 32 * (c8 & 1)) * 16;
+      *reinterpret_cast<u32x4_t *>(rp) = u32x4_t{0, 0, 0, 0};
+      *reinterpret_cast<u32x4_t *>(rp + 1024) = u32x4_t{0, 0, 0, 0};
+    }
+    return;
+  }
+  const int b = tok / a.s, i = tok - b * a.s;
+  const float *src = a.kva + (int64_t)tok * (r + dr);
+  uint8_t *dst = a.table.row(b, i, (int64_t)(r + dr) * (a.bf16 ? 2 : 4));
+  // LayerNorm as candle_nn::LayerNorm (src/model.rs:136): mean, biased
+  // variance of the centred values, divide by sqrt(var + eps), weight, bias
+  constexpr int kMaxC8 = 4;  // r <= 2048
+  floatx4_t x[kMaxC8][2];
+  float sum = 0.f;
+#pragma unroll
+  for (int u = 0; u < kMaxC8; ++u) {
+    const int c8 = lane + 64 * u;
+    if (c8 < C8) {
+      x[u][0] = *reinterpret_cast<const floatx4_t *>(src + 8 * c8);
+      x[u][1] = *reinterpret_cast<const floatx4_t *>(src + 8 * c8 + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum += x[u][0][e] + x[u][1][e];
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  const float mean = sum / (float)r;
+  float sq = 0.f;
+#pragma unroll
+  for (int u = 0; u < kMaxC8; ++u)
+    if (lane + 64 * u < C8)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = x[u][e >> 2][e & 3] - mean;
+        sq += d * d;
+      }
+  for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+  const float den = sqrtf(sq / (float)r + a.eps);
+#pragma unroll
+  for (int u = 0; u < kMaxC8; ++u) {
+    const int c8 = lane + 64 * u;
+    if (c8 >= C8) continue;
+    float v[8];
+    uint16_t hi[8], lo[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int c = 8 * c8 + e;
+      const float t = (x[u][e >> 2][e & 3] - mean) / den * a.ln_w[c];
+      v[e] = a.ln_b ? t + a.ln_b[c] : t;
+      hi[e] = f32_to_bf16_bits(v[e]);
+      lo[e] = f32_to_bf16_bits(v[e] - bf16_bits_to_f32(hi[e]));
+    }
+    if (a.bf16) {
+      *reinterpret_cast<u32x4_t *>(dst + 16 * c8) =
+          u32x4_t{hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16),
+                  hi[4] | ((uint32_t)hi[5] << 16), hi[6] | ((uint32_t)hi[7] << 16)};
+    } else {
+      *reinterpret_cast<floatx4_t *>(dst + 32 * c8) = floatx4_t{v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<floatx4_t *>(dst + 32 * c8 + 16) = floatx4_t{v[4], v[5], v[6], v[7]};
+    }
+    uint8_t *rp = rec + ((int64_t)(tok >> 5) * KS + (c8 >> 1)) * 2048 + ((tok & 31) + 32 * (c8 & 1)) * 16;
+    *reinterpret_cast<u32x4_t *>(rp) =
+        u32x4_t{hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16),
+                hi[4] | ((uint32_t)hi[5] << 16), hi[6] | ((uint32_t)hi[7] << 16)};
+    *reinterpret_cast<u32x4_t *>(rp + 1024) =
+        u32x4_t{lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16),
+                lo[4] | ((uint32_t)lo[5] << 16), lo[6] | ((uint32_t)lo[7] << 16)};
+  }
+  const float pos = (float)i;
+  for (int p = lane; p < dr / 2; p += 64) {
+    const float ang = pos * a.inv_freq[p];
+    const float cs = cosf(ang) * a.mscale, sn = sinf(ang) * a.mscale;
+    const float e = src[r + 2 * p], o = src[r + 2 * p + 1];
+    const float re = e * cs - o * sn, ro = o * cs + e * sn;
+    if (a.bf16) {
+      reinterpret_cast<uint16_t *>(dst)[r + 2 * p] = f32_to_bf16_bits(re);
+      reinterpret_cast<uint16_t *>(dst)[r + 2 * p + 1] = f32_to_bf16_bits(ro);
+    } else {
+      reinterpret_cast<float *>(dst)[r + 2 * p] = re;
+      reinterpret_cast<float *>(dst)[r + 2 * p + 1] = ro;
+    }
+    if constexpr (sizeof(KT) == 2) {
+      k_rope[(int64_t)tok * dr + 2 * p] = f32_to_bf16_bits(re);
+      k_rope[(int64_t)tok * dr + 2 * p + 1] = f32_to_bf16_bits(ro);
+    } else {
+      k_rope[(int64_t)tok * dr + 2 * p] = re;
+      k_rope[(int64_t)tok * dr + 2 * p + 1] = ro;
+    }
+  }
+  if (i == 0 && lane == 0) lens[b] = a.s;
+}
+
 LatentRowsArgs latent_rows_args(const qmla_layer *L, const float *kva, int seq, float *rows,
                                 qmla_kv_cache *cache) {
   const auto &g = L->cfg;
@@ -516,9 +627,10 @@ qmla_status make_skinny_weights(qmla_layer *L, const float *wq, const float *bq,
 bool use_split_gemm(const qmla_layer *L) {
   const auto &g = L->cfg;
   const int H = g.heads, dn = g.qk_nope, dr = g.qk_rope, dv = g.v_dim, r = g.kv_lora_rank;
-  return L->skinny && L->wkvbf && split_gemm_supported(H * (dn + dr) + r + dr, g.hidden) &&
+  return L->skinny && L->wkvbf && r <= 2048 &&
+         split_gemm_supported(H * (dn + dr) + r + dr, g.hidden) &&
          split_gemm_supported(H * (dn + dv), r) && split_gemm_supported(g.hidden, H * dv) &&
-         dn % 4 == 0 && dr % 4 == 0 && dv % 32 == 0;
+         dn % 4 == 0 && dr % 8 == 0 && dv % 32 == 0;
 }
 
 // The decode step runs its projections on the skinny kernel when every
@@ -557,7 +669,8 @@ SkinnyGemmArgs skinny_args(const void *w_frag, const float *x, int64_t ldx, int6
 inline size_t al(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct LayerWs {
-  size_t q, kva, rows, qn, qr, qlat, olat, o, dec, kvb, k, v, kr, ctx, pack, part, part_elems, xsplit,
+  size_t q, kva, rows, qn, qr, qlat, olat, o, dec, kvb, k, v, kr, ctx, pack, pack2, part, part_elems,
+      xsplit,
       qn1, qr1, kva1,
       total;
 };
@@ -617,10 +730,11 @@ LayerWs layer_ws(const qmla_layer *L, int32_t batch, int32_t seq, size_t dec_byt
     w.v = take(sizeof(float) * n * H * g.v_dim);
     w.kr = take(sizeof(float) * n * g.qk_rope + 4);
     w.ctx = take(sizeof(float) * n * H * g.v_dim);
-    // the activation records of the hand-written split GEMM
-    w.pack = take(use_split_gemm(L) && n >= (size_t)kSplitGemmMinRows
-                      ? split_gemm_pack_bytes((int)n, (int)kmax)
-                      : 1);
+    // the activation records of the hand-written split GEMM: the current
+    // product's, and kv_b_proj's (written by the latent rows kernel)
+    const bool sg = use_split_gemm(L) && n >= (size_t)kSplitGemmMinRows;
+    w.pack = take(sg ? split_gemm_pack_bytes((int)n, (int)kmax) : 1);
+    w.pack2 = take(sg ? split_gemm_pack_bytes((int)n, g.kv_lora_rank) : 1);
     pre_end = off;
   }
   w.total = std::max(dec_end, pre_end);
@@ -1063,34 +1177,35 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
     qa.mscale = (float)g.rope_mscale;
     void *pack = ws + w.pack;
     QMLA_TRY(launch_split_gemm(qa, pack, s));
-    QMLA_TRY(latent_to_cache(L, kva, batch, seq, rows, cache, s));
+    // the latent rows: cache rows, kv_b_proj's activation records and k_rope
+    uint8_t *krec = reinterpret_cast<uint8_t *>(ws + w.pack2);
+    {
+      const LatentRowsArgs la = latent_rows_args(L, kva, seq, nullptr, cache);
+      const dim3 grid((n + 31) / 32 * 8);  // 4 tokens a block, n rounded up to 32
+      if (bfa)
+        k_prefill_rows<uint16_t><<<grid, dim3(256), 0, s>>>(la, n, krec, (uint16_t *)kr,
+                                                            cache->d_lens);
+      else
+        k_prefill_rows<float><<<grid, dim3(256), 0, s>>>(la, n, krec, kr, cache->d_lens);
+      QMLA_LAUNCH_CHECK("k_prefill_rows");
+      for (int32_t i = 0; i < batch; ++i) cache->h_lens[i] += seq;
+    }
     SplitGemmArgs ka = a;
     ka.w_frag = L->wkvbf;
     ka.N = H * (dn + dv);
     ka.K = r;
-    ka.x = rows;
-    ka.ldx = r + dr;
     ka.bias = L->bkvb;
     ka.epi = kSgEpiKvb;
     ka.out0 = k;
     ka.out1 = v;
-    QMLA_TRY(launch_split_gemm(ka, pack, s));
+    QMLA_TRY(launch_split_gemm_packed(ka, krec, s));
     qmla_prefill_dims pd{batch, H, seq, seq, dn, dr, dv, 1, 0};
-    if (bfa) {
-      if (dr > 0) {
-        k_rows_rope<uint16_t><<<dim3(n), dim3(64), 0, s>>>(rows, r, dr, (uint16_t *)kr);
-        QMLA_LAUNCH_CHECK("k_rows_rope");
-      }
+    if (bfa)
       QMLA_TRY(launch_prefill_bf16(pd, (const uint16_t *)qn, (const uint16_t *)qr,
                                    (const uint16_t *)k, (const uint16_t *)kr, (const uint16_t *)v,
                                    (float)g.softmax_scale, 1, (uint16_t *)ctx, s));
-    } else {
-      if (dr > 0) {
-        k_rows_rope<float><<<dim3(n), dim3(64), 0, s>>>(rows, r, dr, kr);
-        QMLA_LAUNCH_CHECK("k_rows_rope");
-      }
+    else
       QMLA_TRY(launch_prefill_f32(pd, qn, qr, k, kr, v, (float)g.softmax_scale, 1, ctx, s));
-    }
     SplitGemmArgs oa = a;
     oa.w_frag = L->wof;
     oa.N = g.hidden;

@@ -365,16 +365,41 @@ size_t split_gemm_pack_bytes(int M, int K) {
   return (size_t)((M + 31) / 32) * (K / 16) * kFrag;
 }
 
-qmla_status launch_split_gemm(const SplitGemmArgs &a, void *pack, hipStream_t s) {
+namespace {
+qmla_status sg_check(const SplitGemmArgs &a) {
   QMLA_REQUIRE(split_gemm_supported(a.N, a.K) && a.M > 0, QMLA_ERR_UNSUPPORTED,
                "split GEMM M %d N %d K %d", a.M, a.N, a.K);
-  QMLA_REQUIRE(a.seq > 0 && pack, QMLA_ERR_SHAPE, "split GEMM seq %d / no pack buffer", a.seq);
+  QMLA_REQUIRE(a.seq > 0, QMLA_ERR_SHAPE, "split GEMM seq %d", a.seq);
   QMLA_REQUIRE(a.x_heads == 0 || (a.dv > 0 && a.dv % 16 == 0 && a.K == a.heads * a.dv),
                QMLA_ERR_SHAPE, "split GEMM head-major x: dv %d, K %d", a.dv, a.K);
   QMLA_REQUIRE(a.epi != kSgEpiQkv || (a.dn % 4 == 0 && a.dr % 4 == 0 && a.lens && a.inv_freq),
                QMLA_ERR_SHAPE, "split GEMM q split needs widths that are multiples of 4");
   QMLA_REQUIRE(a.epi != kSgEpiKvb || (a.dn % 4 == 0 && a.dv % 4 == 0), QMLA_ERR_SHAPE,
                "split GEMM k/v split needs widths that are multiples of 4");
+  return QMLA_OK;
+}
+
+// Many rows: 256 x 256 tiles; fewer: 64 x 128 tiles, so that the grid
+// still fills the device (at 2048 rows a 256 x 256 tiling of q_proj |
+// kv_a has 120 blocks).
+qmla_status sg_run(const SplitGemmArgs &a, const uint8_t *xrec, bool xlo, hipStream_t s) {
+  using Big = SgCfg<4, 2, 2, 1, 3>;
+  using Small = SgCfg<1, 1, 2, 2, 3>;
+  if (a.M >= kSplitGemmBigRows)
+    return xlo ? sg_launch<Big, true>(a, xrec, s) : sg_launch<Big, false>(a, xrec, s);
+  return xlo ? sg_launch<Small, true>(a, xrec, s) : sg_launch<Small, false>(a, xrec, s);
+}
+}  // namespace
+
+qmla_status launch_split_gemm_packed(const SplitGemmArgs &a, const void *xrec, hipStream_t s) {
+  QMLA_TRY(sg_check(a));
+  QMLA_REQUIRE(a.x_heads == 0 && xrec, QMLA_ERR_SHAPE, "packed activations: f32 rows only");
+  return sg_run(a, static_cast<const uint8_t *>(xrec), true, s);
+}
+
+qmla_status launch_split_gemm(const SplitGemmArgs &a, void *pack, hipStream_t s) {
+  QMLA_TRY(sg_check(a));
+  QMLA_REQUIRE(pack, QMLA_ERR_SHAPE, "split GEMM without a pack buffer");
   // the activations as records (one pass over x)
   const int64_t recs = (int64_t)((a.M + 31) / 32) * (a.K / 16);
   QMLA_REQUIRE(recs / 4 + 1 <= 0x7fffffff, QMLA_ERR_SHAPE, "split GEMM pack grid");
@@ -388,14 +413,7 @@ qmla_status launch_split_gemm(const SplitGemmArgs &a, void *pack, hipStream_t s)
   else
     k_pack_rows<kSgXHeadsF32><<<pg, pb, 0, s>>>(a, xrec);
   QMLA_LAUNCH_CHECK("k_pack_rows");
-  // Many rows: 256 x 256 tiles; fewer: 64 x 128 tiles, so that the grid
-  // still fills the device (at 2048 rows a 256 x 256 tiling of q_proj |
-  // kv_a has 120 blocks).
-  using Big = SgCfg<4, 2, 2, 1, 3>;
-  using Small = SgCfg<1, 1, 2, 2, 3>;
-  if (a.M >= kSplitGemmBigRows)
-    return xlo ? sg_launch<Big, true>(a, xrec, s) : sg_launch<Big, false>(a, xrec, s);
-  return xlo ? sg_launch<Small, true>(a, xrec, s) : sg_launch<Small, false>(a, xrec, s);
+  return sg_run(a, xrec, xlo, s);
 }
 
 }  // namespace qmla
