@@ -305,8 +305,8 @@ __global__ __launch_bounds__(256) void k_latent_rows(LatentRowsArgs a) {
 // so positions are the token indices, lens is not read, and the wave of
 // each sequence's token 0 sets its length to s.  The grid covers n rounded
 // up to 32 tokens (the padding rows of the records are zeroed).  r % 32 == 0,
-// r <= 2048, dr % 8 == 0.
-template <typename KT>
+// r <= 512 U, dr % 8 == 0.
+template <typename KT, int U>
 __global__ __launch_bounds__(256) void k_prefill_rows(LatentRowsArgs a, int n, uint8_t *rec,
                                                       KT *k_rope, int32_t *lens) {
   const int tok = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -327,7 +327,7 @@ __global__ __launch_bounds__(256) void k_prefill_rows(LatentRowsArgs a, int n, u
   uint8_t *dst = a.table.row(b, i, (int64_t)(r + dr) * (a.bf16 ? 2 : 4));
   // LayerNorm as candle_nn::LayerNorm (src/model.rs:136): mean, biased
   // variance of the centred values, divide by sqrt(var + eps), weight, bias
-  constexpr int kMaxC8 = 4;  // r <= 2048
+  constexpr int kMaxC8 = U;  // r <= 512 U: each lane holds U groups of 8
   floatx4_t x[kMaxC8][2];
   float sum = 0.f;
 #pragma unroll
@@ -352,18 +352,27 @@ __global__ __launch_bounds__(256) void k_prefill_rows(LatentRowsArgs a, int n, u
         sq += d * d;
       }
   for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
-  const float den = sqrtf(sq / (float)r + a.eps);
+  const float inv = 1.f / sqrtf(sq / (float)r + a.eps);
 #pragma unroll
   for (int u = 0; u < kMaxC8; ++u) {
     const int c8 = lane + 64 * u;
     if (c8 >= C8) continue;
-    float v[8];
+    float v[8], w[8], bb[8];
     uint16_t hi[8], lo[8];
+    *reinterpret_cast<floatx4_t *>(w) = *reinterpret_cast<const floatx4_t *>(a.ln_w + 8 * c8);
+    *reinterpret_cast<floatx4_t *>(w + 4) =
+        *reinterpret_cast<const floatx4_t *>(a.ln_w + 8 * c8 + 4);
+    if (a.ln_b) {
+      *reinterpret_cast<floatx4_t *>(bb) = *reinterpret_cast<const floatx4_t *>(a.ln_b + 8 * c8);
+      *reinterpret_cast<floatx4_t *>(bb + 4) =
+          *reinterpret_cast<const floatx4_t *>(a.ln_b + 8 * c8 + 4);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) bb[e] = 0.f;
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int c = 8 * c8 + e;
-      const float t = (x[u][e >> 2][e & 3] - mean) / den * a.ln_w[c];
-      v[e] = a.ln_b ? t + a.ln_b[c] : t;
+      v[e] = (x[u][e >> 2][e & 3] - mean) * inv * w[e] + bb[e];
       hi[e] = f32_to_bf16_bits(v[e]);
       lo[e] = f32_to_bf16_bits(v[e] - bf16_bits_to_f32(hi[e]));
     }
@@ -627,7 +636,7 @@ qmla_status make_skinny_weights(qmla_layer *L, const float *wq, const float *bq,
 bool use_split_gemm(const qmla_layer *L) {
   const auto &g = L->cfg;
   const int H = g.heads, dn = g.qk_nope, dr = g.qk_rope, dv = g.v_dim, r = g.kv_lora_rank;
-  return L->skinny && L->wkvbf && r <= 2048 &&
+  return L->skinny && L->wkvbf && r <= 512 &&
          split_gemm_supported(H * (dn + dr) + r + dr, g.hidden) &&
          split_gemm_supported(H * (dn + dv), r) && split_gemm_supported(g.hidden, H * dv) &&
          dn % 4 == 0 && dr % 8 == 0 && dv % 32 == 0;
@@ -1182,11 +1191,12 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
     {
       const LatentRowsArgs la = latent_rows_args(L, kva, seq, nullptr, cache);
       const dim3 grid((n + 31) / 32 * 8);  // 4 tokens a block, n rounded up to 32
+      // r <= 512 (use_split_gemm): one group of 8 values per lane
       if (bfa)
-        k_prefill_rows<uint16_t><<<grid, dim3(256), 0, s>>>(la, n, krec, (uint16_t *)kr,
-                                                            cache->d_lens);
+        k_prefill_rows<uint16_t, 1><<<grid, dim3(256), 0, s>>>(la, n, krec, (uint16_t *)kr,
+                                                               cache->d_lens);
       else
-        k_prefill_rows<float><<<grid, dim3(256), 0, s>>>(la, n, krec, kr, cache->d_lens);
+        k_prefill_rows<float, 1><<<grid, dim3(256), 0, s>>>(la, n, krec, kr, cache->d_lens);
       QMLA_LAUNCH_CHECK("k_prefill_rows");
       for (int32_t i = 0; i < batch; ++i) cache->h_lens[i] += seq;
     }

@@ -89,13 +89,13 @@ __global__ __launch_bounds__(256) void k_pack_rows(SplitGemmArgs a, uint8_t *__r
   constexpr bool LO = XM != kSgXHeadsBf16;
   constexpr int RB = LO ? 2048 : 1024;  // bytes per record
   const int KS = a.K / 16;
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int64_t nrec = (int64_t)((a.M + 31) / 32) * KS;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);  // < 2^31 (host check)
+  const int nrec = (a.M + 31) / 32 * KS;
   if (r >= nrec) return;
   const int lane = threadIdx.x & 63;
-  const int mb = (int)(r / KS), ks = (int)(r - (int64_t)mb * KS);
+  const int mb = r / KS, ks = r - mb * KS;
   const int m = mb * 32 + (lane & 31), k = ks * 16 + 8 * (lane >> 5);
-  uint8_t *dst = rec + r * RB + lane * 16;
+  uint8_t *dst = rec + (int64_t)r * RB + lane * 16;
   if (m >= a.M) {
     *reinterpret_cast<u32x4_t *>(dst) = u32x4_t{0, 0, 0, 0};
     if constexpr (LO) *reinterpret_cast<u32x4_t *>(dst + 1024) = u32x4_t{0, 0, 0, 0};
@@ -402,7 +402,7 @@ qmla_status launch_split_gemm(const SplitGemmArgs &a, void *pack, hipStream_t s)
   QMLA_REQUIRE(pack, QMLA_ERR_SHAPE, "split GEMM without a pack buffer");
   // the activations as records (one pass over x)
   const int64_t recs = (int64_t)((a.M + 31) / 32) * (a.K / 16);
-  QMLA_REQUIRE(recs / 4 + 1 <= 0x7fffffff, QMLA_ERR_SHAPE, "split GEMM pack grid");
+  QMLA_REQUIRE(recs + 3 <= 0x7fffffff, QMLA_ERR_SHAPE, "split GEMM pack grid");
   uint8_t *xrec = static_cast<uint8_t *>(pack);
   const dim3 pg((unsigned)((recs + 3) / 4)), pb(256);
   const bool xlo = !(a.x_heads && a.x_bf16);
