@@ -702,7 +702,13 @@ LayerWs layer_ws(const qmla_layer *L, int32_t batch, int32_t seq, size_t dec_byt
     off += al(bytes);
     return o;
   };
-  w.q = take(sizeof(float) * n * H * (g.qk_nope + g.qk_rope));
+  // forward_prefill on the hand-written split GEMMs writes q, k, v and the
+  // cache rows from the GEMM epilogues: it needs neither the f32 q, the
+  // rocBLAS split of the activations, the LayerNorm'd rows nor the kv_b
+  // output, only the activation records
+  const bool sg = use_split_gemm(L) && n >= (size_t)kSplitGemmMinRows;
+  const bool sg_only = sg && use == WsFor::kPrefill;
+  w.q = take(sg_only ? 1 : sizeof(float) * n * H * (g.qk_nope + g.qk_rope));
   w.kva = take(sizeof(float) * n * (g.kv_lora_rank + g.qk_rope));
   w.qn = take(sizeof(float) * n * H * g.qk_nope);
   w.qr = take(sizeof(float) * n * H * g.qk_rope + 4);
@@ -716,7 +722,8 @@ LayerWs layer_ws(const qmla_layer *L, int32_t batch, int32_t seq, size_t dec_byt
   w.part = take(sizeof(float) * (w.part_elems ? w.part_elems : 1));
   // bf16 halves of a projection's activations (rocBLAS split GEMMs, many rows)
   const size_t kmax = std::max<size_t>({(size_t)g.hidden, H * g.v_dim, (size_t)g.kv_lora_rank});
-  w.xsplit = take(n >= (size_t)kSplitRows ? split_bytes((int64_t)n, (int64_t)kmax) : 1);
+  w.xsplit =
+      take(n >= (size_t)kSplitRows && !sg_only ? split_bytes((int64_t)n, (int64_t)kmax) : 1);
   const size_t shared = off;
   size_t dec_end = shared, pre_end = shared;
   if (use != WsFor::kPrefill) {
@@ -733,15 +740,14 @@ LayerWs layer_ws(const qmla_layer *L, int32_t batch, int32_t seq, size_t dec_byt
   }
   if (use != WsFor::kDecode) {
     off = shared;
-    w.rows = take(sizeof(float) * n * (g.kv_lora_rank + g.qk_rope));
-    w.kvb = take(sizeof(float) * n * H * (g.qk_nope + g.v_dim));
+    w.rows = take(sg ? 1 : sizeof(float) * n * (g.kv_lora_rank + g.qk_rope));
+    w.kvb = take(sg ? 1 : sizeof(float) * n * H * (g.qk_nope + g.v_dim));
     w.k = take(sizeof(float) * n * H * g.qk_nope);
     w.v = take(sizeof(float) * n * H * g.v_dim);
     w.kr = take(sizeof(float) * n * g.qk_rope + 4);
     w.ctx = take(sizeof(float) * n * H * g.v_dim);
     // the activation records of the hand-written split GEMM: the current
     // product's, and kv_b_proj's (written by the latent rows kernel)
-    const bool sg = use_split_gemm(L) && n >= (size_t)kSplitGemmMinRows;
     w.pack = take(sg ? split_gemm_pack_bytes((int)n, (int)kmax) : 1);
     w.pack2 = take(sg ? split_gemm_pack_bytes((int)n, g.kv_lora_rank) : 1);
     pre_end = off;
