@@ -253,8 +253,16 @@ struct SplitGemmArgs {
   const int32_t *lens;     // QKV: token s of sequence b sits at position lens[b] + s
   const float *inv_freq;   // [dr / 2]
   float mscale;
+  // split-K: ksplit slices of K each write raw partial sums part[z][M][N]
+  // (f32), which a second launch adds in slice order before the epilogue
+  int ksplit;
+  float *part;
 };
 bool split_gemm_supported(int N, int K);
+// K slices the split GEMM uses for an M x N x K product (1 when its tiles
+// already fill the device), and the partial-sum bytes they need.
+int split_gemm_slices(int M, int N, int K);
+size_t split_gemm_part_bytes(int M, int N, int K);
 // Rows from which the split GEMM runs its 256 x 256 tiles, and below which
 // the layer keeps its rocBLAS path (few rows stream the weights; the split
 // GEMM's tiles would leave most of the device idle).

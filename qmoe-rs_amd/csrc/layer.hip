@@ -678,8 +678,8 @@ SkinnyGemmArgs skinny_args(const void *w_frag, const float *x, int64_t ldx, int6
 inline size_t al(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct LayerWs {
-  size_t q, kva, rows, qn, qr, qlat, olat, o, dec, kvb, k, v, kr, ctx, pack, pack2, part, part_elems,
-      xsplit,
+  size_t q, kva, rows, qn, qr, qlat, olat, o, dec, kvb, k, v, kr, ctx, pack, pack2, sgpart, part,
+      part_elems, xsplit,
       qn1, qr1, kva1,
       total;
 };
@@ -750,6 +750,14 @@ LayerWs layer_ws(const qmla_layer *L, int32_t batch, int32_t seq, size_t dec_byt
     // product's, and kv_b_proj's (written by the latent rows kernel)
     w.pack = take(sg ? split_gemm_pack_bytes((int)n, (int)kmax) : 1);
     w.pack2 = take(sg ? split_gemm_pack_bytes((int)n, g.kv_lora_rank) : 1);
+    // the split GEMMs' K-slice partial sums (few rows), one product at a time
+    const int N1 = (int)H * (g.qk_nope + g.qk_rope) + g.kv_lora_rank + g.qk_rope;
+    const int Nkv = (int)H * (g.qk_nope + g.v_dim);
+    w.sgpart = take(sg ? std::max({split_gemm_part_bytes((int)n, N1, g.hidden),
+                                   split_gemm_part_bytes((int)n, Nkv, g.kv_lora_rank),
+                                   split_gemm_part_bytes((int)n, g.hidden, (int)H * g.v_dim),
+                                   (size_t)1})
+                       : 1);
     pre_end = off;
   }
   w.total = std::max(dec_end, pre_end);
@@ -1175,6 +1183,8 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
     a.dr = dr;
     a.dv = dv;
     a.out_bf16 = bfa ? 1 : 0;
+    a.ksplit = 1;  // the launcher picks the K slices
+    a.part = (float *)(ws + w.sgpart);
     SplitGemmArgs qa = a;
     qa.w_frag = L->w1f;
     qa.N = H * (dn + dr) + r + dr;

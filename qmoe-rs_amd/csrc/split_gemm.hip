@@ -132,6 +132,71 @@ __global__ __launch_bounds__(256) void k_pack_rows(SplitGemmArgs a, uint8_t *__r
   }
 }
 
+// The epilogue of four consecutive outputs n0 .. n0 + 3 of row m (bias
+// included in v).
+template <int EPI, typename OutT>
+__device__ __forceinline__ void sg_store4(const SplitGemmArgs &a, int m, int n0,
+                                          const float (&v)[4]) {
+  const int b = m / a.seq, s = m - b * a.seq;
+  if constexpr (EPI == kSgEpiFinal) {
+    sg_put4<float>(a.y + (int64_t)m * a.ldy + n0, v);
+  } else if constexpr (EPI == kSgEpiQkv) {
+    const int qw = a.dn + a.dr, nq = a.heads * qw;
+    if (n0 >= nq) {
+      sg_put4<float>(a.kva + (int64_t)m * a.kva_ld + (n0 - nq), v);
+      return;
+    }
+    const int hd = n0 / qw, d = n0 - hd * qw;
+    const int64_t row = ((int64_t)b * a.heads + hd) * a.seq + s;
+    if (d < a.dn) {
+      sg_put4<OutT>(reinterpret_cast<OutT *>(a.out0) + row * a.dn + d, v);
+    } else {
+      // interleaved pairs (2p, 2p + 1) of q_rope (src/model.rs:70-84)
+      const int p = (d - a.dn) >> 1;
+      const float pos = (float)(a.lens[b] + s);
+      float r[4];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const float ang = pos * a.inv_freq[p + u];
+        const float cs = cosf(ang) * a.mscale, sn = sinf(ang) * a.mscale;
+        r[2 * u] = v[2 * u] * cs - v[2 * u + 1] * sn;
+        r[2 * u + 1] = v[2 * u + 1] * cs + v[2 * u] * sn;
+      }
+      sg_put4<OutT>(reinterpret_cast<OutT *>(a.out1) + row * a.dr + (d - a.dn), r);
+    }
+  } else {  // kSgEpiKvb
+    const int kw = a.dn + a.dv;
+    const int hd = n0 / kw, d = n0 - hd * kw;
+    const int64_t row = ((int64_t)b * a.heads + hd) * a.seq + s;
+    if (d < a.dn)
+      sg_put4<OutT>(reinterpret_cast<OutT *>(a.out0) + row * a.dn + d, v);
+    else
+      sg_put4<OutT>(reinterpret_cast<OutT *>(a.out1) + row * a.dv + (d - a.dn), v);
+  }
+}
+
+// Split-K: the sum of the slices' partials in slice order, the bias, then
+// the epilogue; one thread per four outputs of a row.
+template <int EPI, typename OutT>
+__global__ __launch_bounds__(256) void k_sg_reduce(SplitGemmArgs a) {
+  const int NQ = a.N / 4;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (int64_t)a.M * NQ) return;
+  const int m = (int)(t / NQ), n0 = 4 * (int)(t - (int64_t)m * NQ);
+  const int64_t plane = (int64_t)a.M * a.N;
+  const float *src = a.part + (int64_t)m * a.N + n0;
+  floatx4_t acc = *reinterpret_cast<const floatx4_t *>(src);
+  for (int z = 1; z < a.ksplit; ++z) {
+    const floatx4_t p = *reinterpret_cast<const floatx4_t *>(src + z * plane);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += p[e];
+  }
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = acc[e] + (a.bias ? a.bias[n0 + e] : 0.f);
+  sg_store4<EPI, OutT>(a, m, n0, v);
+}
+
 // Tile shape and pipeline of one instantiation: NBW x MBW 32-blocks per
 // wave, WN waves along N (8 / WN along M), KSC k-steps of 16 per chunk and
 // NST chunks in the LDS ring.
@@ -171,7 +236,9 @@ __global__ __launch_bounds__(kSgThreads) void k_split_gemm(SplitGemmArgs a, cons
   const int grp = (kk / (kSgGn * kSgGm)) * 8 + xcd, pos = kk % (kSgGn * kSgGm);
   const int bn = (grp % GNT) * kSgGn + pos % kSgGn, bm = (grp / GNT) * kSgGm + pos / kSgGn;
   if (bn >= NT || bm >= MT) return;  // a slot of a partial group
-  const int NB = (a.N + 31) / 32, MB = (a.M + 31) / 32, KS = a.K / 16, NC = KS / KSC;
+  const int NB = (a.N + 31) / 32, MB = (a.M + 31) / 32, KS = a.K / 16;
+  // this block's K slice: chunks [cz, cz + NC) of the KS / KSC
+  const int NC = KS / KSC / a.ksplit, cz = blockIdx.y * NC;
 
   // DMA slot u of this wave: instruction i = wave DW + u of the chunk.
   // Instructions [0, 2 KSC NBT) move weight records (record j KSC + ks of
@@ -187,13 +254,13 @@ __global__ __launch_bounds__(kSgThreads) void k_split_gemm(SplitGemmArgs a, cons
         const int rec = i >> 1, half = i & 1, j = rec / KSC, ks = rec % KSC;
         const int nb = min(bn * NBT + j, NB - 1);
         src = reinterpret_cast<const uint8_t *>(a.w_frag) +
-              ((int64_t)nb * KS + KSC * c + ks) * kFrag + half * 1024;
+              ((int64_t)nb * KS + KSC * (cz + c) + ks) * kFrag + half * 1024;
       } else {
         const int xi = i - 2 * KSC * NBT;
         const int rec = XLO ? xi >> 1 : xi, half = XLO ? xi & 1 : 0;
         const int j = rec / KSC, ks = rec % KSC;
         const int mb = min(bm * MBT + j, MB - 1);
-        src = xrec + ((int64_t)mb * KS + KSC * c + ks) * XR + half * 1024;
+        src = xrec + ((int64_t)mb * KS + KSC * (cz + c) + ks) * XR + half * 1024;
       }
       pipe::dma16(pipe::fresh(src), (uint32_t)(lane * 16), pipe::fresh(st + (uint32_t)(i * 1024)));
     }
@@ -269,49 +336,21 @@ __global__ __launch_bounds__(kSgThreads) void k_split_gemm(SplitGemmArgs a, cons
   const int half = lane >> 5, mr = lane & 31;
   auto emit = [&](const floatx16_t &v16, int nb, int m) __attribute__((always_inline)) {
     if (m >= a.M) return;
-    const int b = m / a.seq, s = m - b * a.seq;
 #pragma unroll
     for (int jq = 0; jq < 4; ++jq) {
       const int n0 = nb * 32 + 8 * jq + 4 * half;
       if (n0 >= a.N) continue;
       float v[4];
+      if (a.ksplit > 1) {
+        // raw partial sums of this slice
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = v16[4 * jq + e];
+        sg_put4<float>(a.part + ((int64_t)blockIdx.y * a.M + m) * a.N + n0, v);
+        continue;
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = v16[4 * jq + e] + (a.bias ? a.bias[n0 + e] : 0.f);
-      if constexpr (EPI == kSgEpiFinal) {
-        sg_put4<float>(a.y + (int64_t)m * a.ldy + n0, v);
-      } else if constexpr (EPI == kSgEpiQkv) {
-        const int qw = a.dn + a.dr, nq = a.heads * qw;
-        if (n0 >= nq) {
-          sg_put4<float>(a.kva + (int64_t)m * a.kva_ld + (n0 - nq), v);
-          continue;
-        }
-        const int hd = n0 / qw, d = n0 - hd * qw;
-        const int64_t row = ((int64_t)b * a.heads + hd) * a.seq + s;
-        if (d < a.dn) {
-          sg_put4<OutT>(reinterpret_cast<OutT *>(a.out0) + row * a.dn + d, v);
-        } else {
-          // interleaved pairs (2p, 2p + 1) of q_rope (src/model.rs:70-84)
-          const int p = (d - a.dn) >> 1;
-          const float pos = (float)(a.lens[b] + s);
-          float r[4];
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const float ang = pos * a.inv_freq[p + u];
-            const float cs = cosf(ang) * a.mscale, sn = sinf(ang) * a.mscale;
-            r[2 * u] = v[2 * u] * cs - v[2 * u + 1] * sn;
-            r[2 * u + 1] = v[2 * u + 1] * cs + v[2 * u] * sn;
-          }
-          sg_put4<OutT>(reinterpret_cast<OutT *>(a.out1) + row * a.dr + (d - a.dn), r);
-        }
-      } else {  // kSgEpiKvb
-        const int kw = a.dn + a.dv;
-        const int hd = n0 / kw, d = n0 - hd * kw;
-        const int64_t row = ((int64_t)b * a.heads + hd) * a.seq + s;
-        if (d < a.dn)
-          sg_put4<OutT>(reinterpret_cast<OutT *>(a.out0) + row * a.dn + d, v);
-        else
-          sg_put4<OutT>(reinterpret_cast<OutT *>(a.out1) + row * a.dv + (d - a.dn), v);
-      }
+      sg_store4<EPI, OutT>(a, m, n0, v);
     }
   };
   [&]<int... IJ>(std::integer_sequence<int, IJ...>) {
@@ -339,21 +378,32 @@ qmla_status sg_launch(const SplitGemmArgs &a, const uint8_t *xrec, hipStream_t s
   QMLA_REQUIRE(blocks <= 0x7fffffff, QMLA_ERR_SHAPE, "split GEMM grid of %lld blocks",
                (long long)blocks);
   const size_t lds = sg_lds_bytes<CF, XLO>();
-  auto go = [&](auto kern) -> qmla_status {
+  QMLA_REQUIRE(a.ksplit >= 1 && a.ksplit <= 65535 && (a.K / 16 / CF::KSC) % a.ksplit == 0 &&
+                   (a.ksplit == 1 || a.part),
+               QMLA_ERR_SHAPE, "split GEMM: %d K slices", a.ksplit);
+  const int64_t outs = (int64_t)a.M * (a.N / 4);  // reduce threads
+  QMLA_REQUIRE(outs / 256 + 1 <= 0x7fffffff, QMLA_ERR_SHAPE, "split GEMM reduce grid");
+  auto go = [&](auto kern, auto reduce) -> qmla_status {
     QMLA_TRY(ensure_dynamic_lds((const void *)kern, lds));
-    kern<<<dim3((unsigned)blocks), dim3(kSgThreads), lds, s>>>(a, xrec);
+    kern<<<dim3((unsigned)blocks, (unsigned)a.ksplit), dim3(kSgThreads), lds, s>>>(a, xrec);
     QMLA_LAUNCH_CHECK("k_split_gemm");
+    if (a.ksplit > 1) {
+      reduce<<<dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s>>>(a);
+      QMLA_LAUNCH_CHECK("k_sg_reduce");
+    }
     return QMLA_OK;
   };
   switch (a.epi) {
     case kSgEpiQkv:
-      if (a.out_bf16) return go(k_split_gemm<CF, XLO, kSgEpiQkv, uint16_t>);
-      return go(k_split_gemm<CF, XLO, kSgEpiQkv, float>);
+      if (a.out_bf16)
+        return go(k_split_gemm<CF, XLO, kSgEpiQkv, uint16_t>, k_sg_reduce<kSgEpiQkv, uint16_t>);
+      return go(k_split_gemm<CF, XLO, kSgEpiQkv, float>, k_sg_reduce<kSgEpiQkv, float>);
     case kSgEpiKvb:
-      if (a.out_bf16) return go(k_split_gemm<CF, XLO, kSgEpiKvb, uint16_t>);
-      return go(k_split_gemm<CF, XLO, kSgEpiKvb, float>);
+      if (a.out_bf16)
+        return go(k_split_gemm<CF, XLO, kSgEpiKvb, uint16_t>, k_sg_reduce<kSgEpiKvb, uint16_t>);
+      return go(k_split_gemm<CF, XLO, kSgEpiKvb, float>, k_sg_reduce<kSgEpiKvb, float>);
     default:
-      return go(k_split_gemm<CF, XLO, kSgEpiFinal, float>);
+      return go(k_split_gemm<CF, XLO, kSgEpiFinal, float>, k_sg_reduce<kSgEpiFinal, float>);
   }
 }
 
@@ -363,6 +413,25 @@ bool split_gemm_supported(int N, int K) { return N > 0 && N % 4 == 0 && K > 0 &&
 
 size_t split_gemm_pack_bytes(int M, int K) {
   return (size_t)((M + 31) / 32) * (K / 16) * kFrag;
+}
+
+// Below the 256 x 256 tiling, a product whose 64 x 128 tiles leave the
+// device short of blocks splits K (powers of two, up to 8) until about 512
+// blocks are in flight, keeping at least 8 chunks of 32 k per slice: each
+// block streams its slice of K with a latency-bound ring, so more, shorter
+// blocks finish sooner.
+int split_gemm_slices(int M, int N, int K) {
+  if (M >= kSplitGemmBigRows || M <= 0 || N <= 0 || K <= 0) return 1;
+  const int64_t tiles = (int64_t)((N + 63) / 64) * ((M + 127) / 128);
+  const int nc = K / 32;  // chunks of the 64 x 128 tiling
+  int s = 1;
+  while (s < 8 && tiles * s * 2 <= 512 && nc % (2 * s) == 0 && nc / (2 * s) >= 8) s *= 2;
+  return s;
+}
+
+size_t split_gemm_part_bytes(int M, int N, int K) {
+  const int s = split_gemm_slices(M, N, K);
+  return s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
 }
 
 namespace {
@@ -382,9 +451,15 @@ qmla_status sg_check(const SplitGemmArgs &a) {
 // Many rows: 256 x 256 tiles; fewer: 64 x 128 tiles, so that the grid
 // still fills the device (at 2048 rows a 256 x 256 tiling of q_proj |
 // kv_a has 120 blocks).
-qmla_status sg_run(const SplitGemmArgs &a, const uint8_t *xrec, bool xlo, hipStream_t s) {
+qmla_status sg_run(const SplitGemmArgs &a0, const uint8_t *xrec, bool xlo, hipStream_t s) {
   using Big = SgCfg<4, 2, 2, 1, 3>;
   using Small = SgCfg<1, 1, 2, 2, 3>;
+  static_assert(Small::KSC == 2, "split_gemm_slices counts chunks of 32 k");
+  SplitGemmArgs a = a0;
+  a.ksplit = split_gemm_slices(a.M, a.N, a.K);
+  QMLA_REQUIRE(a.ksplit == 1 || a.part, QMLA_ERR_WORKSPACE,
+               "split GEMM of %d x %d x %d needs %zu bytes of partial sums", a.M, a.N, a.K,
+               split_gemm_part_bytes(a.M, a.N, a.K));
   if (a.M >= kSplitGemmBigRows)
     return xlo ? sg_launch<Big, true>(a, xrec, s) : sg_launch<Big, false>(a, xrec, s);
   return xlo ? sg_launch<Small, true>(a, xrec, s) : sg_launch<Small, false>(a, xrec, s);

@@ -463,21 +463,21 @@ def test_layer_calls_from_several_threads(qmla_gpu):
         np.testing.assert_array_equal(got[i], want[i])
 
 
-@pytest.mark.parametrize("b", [1, 2])
+@pytest.mark.parametrize("b,s", [(1, 128), (1, 512), (1, 2048), (2, 2048)])
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
-def test_layer_prefill_at_bench_widths(qmla_gpu, dt, b):
+def test_layer_prefill_at_bench_widths(qmla_gpu, dt, b, s):
     """forward_prefill at the widths the layer-prefill bench line runs:
     hidden 2048, 16 heads, kv_lora_rank 512, dn 128 / dr 64 / dv 128, b
-    sequences of 2048 tokens (the split GEMM projections, the kv_b
-    decompression and the attention at full size; 2048 rows run the GEMM's
-    64 x 128 tiles, 4096 rows its one-wave-per-SIMD 256 x 256 tiles),
-    against the oracle's decompressed path: 1e-4 with an f32 cache, 2e-2
-    with a bf16 cache.  Then one decode step on the filled cache."""
+    sequences of s tokens, through the hand-written split GEMMs: 128 and
+    512 rows split K over several blocks (partial sums added by a second
+    launch), 2048 rows run the 64 x 128 tiles whole, 4096 rows the 256 x
+    256 tiles.  Against the oracle's decompressed path: 1e-4 with an f32
+    cache, 2e-2 with a bf16 cache.  Then one decode step on the filled
+    cache."""
     q = qmla_gpu
     hidden, H, dn, dr, dv, r = 2048, 16, 128, 64, 128, 512
     w = O.MlaWeights.random(hidden, H, dn, dr, dv, r, seed=1900)
     layer = q.MlaLayer(w)
-    s = 2048
     xs = O.normal((b, s, hidden), 1901)
     cache = q.KVCache([s + 1] * b, r, dr, q.F32 if dt == "f32" else q.BF16)
     out = layer.forward_prefill(xs, cache)
