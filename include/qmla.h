@@ -345,7 +345,9 @@ QMLA_API qmla_status qmla_layer_prefill_workspace_bytes(const qmla_layer *layer,
                                                const qmla_kv_cache *cache, int32_t batch,
                                                int32_t seq, size_t *bytes);
 /* MlaAttention::forward_with_cache, src/model.rs:256-307, over the latent
- * cache: xs [batch, seq, hidden] f32 device, out [batch, seq, hidden] f32.
+ * cache: xs [batch, seq, hidden] f32 device, out [batch, seq, hidden] f32
+ * (both 16-byte aligned, the workspace 256-byte aligned, as device
+ * allocations are; otherwise QMLA_ERR_INVALID_ARG / QMLA_ERR_WORKSPACE).
  * Appends the seq new latent rows of sequences 0..batch-1 to the cache and
  * attends all cached + new tokens without a mask (as :297-302).  Lengths
  * may differ across the batch (a ragged batch; the reference's KVCache is
@@ -363,7 +365,8 @@ QMLA_API qmla_status qmla_layer_forward_with_cache(const qmla_layer *layer, cons
                                           qmla_stream stream);
 /* MlaAttention::forward_prefill, src/model.rs:193-253: causal attention
  * over the seq tokens, which are appended to the (empty) cache sequences
- * 0..batch-1 -- the latent replacement of the KVCache it returns (:250). */
+ * 0..batch-1 -- the latent replacement of the KVCache it returns (:250).
+ * Same pointer alignment as qmla_layer_forward_with_cache. */
 QMLA_API qmla_status qmla_layer_forward_prefill(const qmla_layer *layer, const float *xs, int32_t batch,
                                        int32_t seq, qmla_kv_cache *cache, float *out,
                                        void *workspace, size_t workspace_bytes,

@@ -199,11 +199,13 @@ struct SkinnyGemmArgs {
   const int32_t *lens;
   const float *inv_freq;
   float mscale;
-  // K split over `groups` (1 or 2) blocks per 32-output tile; group 0 adds
-  // the bias.  With 2 groups (QKV only) group 1 writes its half to
-  // q_nope1, q_rope1 and kva1, and the consumers add the two halves.
+  // K split over `groups` (1, 2, 4 or 8) blocks per 32-output tile; group 0
+  // adds the bias.  QKV (2 groups): group 1 writes its half to q_nope1,
+  // q_rope1 and kva1, and the consumers add the two halves.  FINAL: group g
+  // writes its partial sums to y + g sgrp, and the caller adds the planes.
   int groups;
   float *q_nope1, *q_rope1, *kva1;
+  int64_t sgrp;
   // optional second plane of x (f32, x's strides): the operand is x + x2
   const float *x2;
   // Optional elementwise work spread over the product's blocks (about one

@@ -654,6 +654,27 @@ bool use_skinny(const qmla_layer *L, int n) {
 
 // Arguments of a skinny product y = x W^T (+ bias) with the FINAL store:
 // x [Z][M][K] (row stride ldx, z-stride sx), y [Z][M][N] (ldy, sy).
+// o_proj of the decode step with its K range split over kOprojGroups
+// blocks per 32-output tile (4 x the blocks streaming the weight); the
+// groups' partial planes are added in group order by k_add_planes.
+constexpr int kOprojGroups = 4;
+
+// out[i] = sum over g < G of planes[g plane + i] (in g order), four
+// elements per thread.
+__global__ __launch_bounds__(256) void k_add_planes(const float *__restrict__ planes, int G,
+                                                    int64_t plane, int64_t n4,
+                                                    float *__restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  floatx4_t v = reinterpret_cast<const floatx4_t *>(planes)[i];
+  for (int g = 1; g < G; ++g) {
+    const floatx4_t p = reinterpret_cast<const floatx4_t *>(planes + g * plane)[i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] += p[e];
+  }
+  reinterpret_cast<floatx4_t *>(out)[i] = v;
+}
+
 SkinnyGemmArgs skinny_args(const void *w_frag, const float *x, int64_t ldx, int64_t sx,
                            const float *bias, int64_t sb, float *y, int64_t ldy, int64_t sy,
                            int M, int N, int K, int Z) {
@@ -769,6 +790,9 @@ qmla_status check_layer_call(const qmla_layer *L, const float *xs, int32_t batch
   QMLA_REQUIRE(L && c, QMLA_ERR_INVALID_ARG, "NULL layer or cache");
   QMLA_REQUIRE(batch > 0 && seq > 0, QMLA_ERR_SHAPE, "batch and seq must be > 0");
   QMLA_REQUIRE(xs && out, QMLA_ERR_INVALID_ARG, "NULL xs or out");
+  // the kernels move rows in 16-byte vectors
+  QMLA_REQUIRE((reinterpret_cast<uintptr_t>(xs) | reinterpret_cast<uintptr_t>(out)) % 16 == 0,
+               QMLA_ERR_INVALID_ARG, "xs and out must be 16-byte aligned");
   QMLA_REQUIRE(batch <= c->num_seqs, QMLA_ERR_SHAPE, "batch %d > cache sequences %d", batch,
                c->num_seqs);
   QMLA_REQUIRE(c->r == L->cfg.kv_lora_rank && c->dr == L->cfg.qk_rope, QMLA_ERR_SHAPE,
@@ -1018,6 +1042,8 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
   const LayerWs w = layer_ws(L, batch, seq, dec_bytes, WsFor::kDecode);
   QMLA_REQUIRE(workspace && workspace_bytes >= w.total, QMLA_ERR_WORKSPACE,
                "workspace of %zu bytes < required %zu", workspace_bytes, w.total);
+  QMLA_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, QMLA_ERR_WORKSPACE,
+               "the workspace must be 256-byte aligned (device allocations are)");
   QMLA_TRY(make_room(cache, 0, batch, seq, as_stream(stream)));
   char *ws = static_cast<char *>(workspace);
   float *q = (float *)(ws + w.q), *kva = (float *)(ws + w.kva);
@@ -1100,10 +1126,25 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
                                       L->buv, dv, o, 0, dv, M, dv, r, H);
       uv.mode = kSkinnyPackB;
       QMLA_TRY(launch_skinny_gemm(uv, s));
-      SkinnyGemmArgs op = skinny_args(L->wof, o, 0, 0, L->bo, 0, out + (size_t)m0 * g.hidden,
-                                      g.hidden, 0, M, g.hidden, H * dv, 1);
+      const int64_t plane = (int64_t)M * g.hidden;
+      const bool split = g.hidden % 4 == 0 && (H * dv) % (16 * kOprojGroups) == 0 &&
+                         skinny_supported(M, H * dv / kOprojGroups) &&
+                         (size_t)kOprojGroups * plane <= w.part_elems;
+      SkinnyGemmArgs op = skinny_args(L->wof, o, 0, 0, L->bo, 0,
+                                      split ? part : out + (size_t)m0 * g.hidden, g.hidden, 0, M,
+                                      g.hidden, H * dv, 1);
       op.x_packed = true;
+      if (split) {
+        op.groups = kOprojGroups;
+        op.sgrp = plane;
+      }
       QMLA_TRY(launch_skinny_gemm(op, s));
+      if (split) {
+        const int64_t n4 = plane / 4;
+        k_add_planes<<<dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s>>>(
+            part, kOprojGroups, plane, n4, out + (size_t)m0 * g.hidden);
+        QMLA_LAUNCH_CHECK("k_add_planes");
+      }
     }
     return QMLA_OK;
   }
@@ -1155,6 +1196,8 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
   const LayerWs w = layer_ws(L, batch, seq, 0, WsFor::kPrefill);
   QMLA_REQUIRE(workspace && workspace_bytes >= w.total, QMLA_ERR_WORKSPACE,
                "workspace of %zu bytes < required %zu", workspace_bytes, w.total);
+  QMLA_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, QMLA_ERR_WORKSPACE,
+               "the workspace must be 256-byte aligned (device allocations are)");
   QMLA_TRY(make_room(cache, 0, batch, seq, as_stream(stream)));
   char *ws = static_cast<char *>(workspace);
   float *q = (float *)(ws + w.q), *kva = (float *)(ws + w.kva), *rows = (float *)(ws + w.rows);

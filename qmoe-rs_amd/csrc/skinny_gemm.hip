@@ -202,7 +202,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_gemm(SkinnyGemmArgs a, Laten
       if (n + 1 < a.N) v1 += bias[n + 1];
     }
     if (a.mode == kSkinnyFinal) {
-      float *y = a.y + z * a.sy + (int64_t)m * a.ldy + n;
+      float *y = a.y + z * a.sy + grp * a.sgrp + (int64_t)m * a.ldy + n;
       y[0] = v0;
       if (n + 1 < a.N) y[1] = v1;
       continue;
@@ -290,15 +290,17 @@ bool skinny_supported(int M, int K) { return M >= 1 && M <= 32 && K > 0 && skinn
 qmla_status launch_skinny_gemm(const SkinnyGemmArgs &a, hipStream_t stream,
                                const LatentRowsArgs *rows, int n_rows) {
   const int G = a.groups ? a.groups : 1;
-  QMLA_REQUIRE(G == 1 || G == 2, QMLA_ERR_SHAPE, "skinny GEMM groups %d", G);
+  QMLA_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, QMLA_ERR_SHAPE, "skinny GEMM groups %d", G);
   QMLA_REQUIRE(a.K % (16 * G) == 0 && skinny_supported(a.M, a.K / G), QMLA_ERR_UNSUPPORTED,
                "skinny GEMM M %d K %d groups %d", a.M, a.K, G);
   QMLA_REQUIRE(a.N > 0 && a.Z > 0 && a.Z <= 65535, QMLA_ERR_SHAPE, "skinny GEMM N %d Z %d", a.N,
                a.Z);
   QMLA_REQUIRE(a.mode != kSkinnyQkv || (a.N % 2 == 0 && a.dn % 2 == 0 && a.dr % 2 == 0),
                QMLA_ERR_SHAPE, "q/kv split needs even widths");
-  QMLA_REQUIRE(G == 1 || (a.mode == kSkinnyQkv && a.q_nope1 && a.q_rope1 && a.kva1),
-               QMLA_ERR_SHAPE, "a K split in two needs the second half's destination");
+  QMLA_REQUIRE(G == 1 || (a.mode == kSkinnyQkv && G == 2 && a.q_nope1 && a.q_rope1 && a.kva1) ||
+                   (a.mode == kSkinnyFinal && a.sgrp >= (int64_t)a.Z * a.sy &&
+                    a.sgrp >= (int64_t)a.M * a.ldy),
+               QMLA_ERR_SHAPE, "a K split needs a destination plane per group");
   QMLA_REQUIRE(!(a.x_packed && a.x2), QMLA_ERR_SHAPE, "packed activations have one plane");
   const int nw = skinny_waves(a.K / G);
   const int extra = rows ? n_rows : 0;

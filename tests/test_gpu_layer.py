@@ -89,6 +89,20 @@ def test_layer_argument_errors(qmla_gpu):
     with pytest.raises(q.QmlaError) as e:
         layer.forward_with_cache(O.normal((1, 1, 512), 1), wrong)
     assert e.value.status == 2
+    # rows and workspace must be aligned (16 and 256 bytes); the rejected
+    # calls leave the cache as it was
+    cache.set_lengths([3, 3])
+    x = q.DeviceBuffer.from_numpy(O.normal((2, 1, 512), 2))
+    out = q.DeviceBuffer(2 * 512 * 4 + 64)
+    need = layer.workspace_bytes(cache, 2, 1)
+    ws = q.DeviceBuffer(need + 512)
+    f = q.lib().qmla_layer_forward_with_cache
+    assert f(layer.handle, x.ptr, 2, 1, cache.handle, out.ptr + 4, ws.ptr, need, None) == 1
+    assert f(layer.handle, x.ptr, 2, 1, cache.handle, out.ptr, ws.ptr + 16, need, None) == 7
+    assert list(cache.lengths()) == [3, 3]
+    assert f(layer.handle, x.ptr, 2, 1, cache.handle, out.ptr + 16, ws.ptr + 256, need, None) == 0
+    q.check(q.lib().qmla_stream_synchronize(None))
+    assert list(cache.lengths()) == [4, 4]
 
 
 @pytest.mark.parametrize("dims", [
