@@ -416,13 +416,16 @@ size_t split_gemm_pack_bytes(int M, int K) {
 }
 
 // Below the 256 x 256 tiling, a product whose 64 x 128 tiles leave the
-// device short of blocks splits K (powers of two, up to 8) until about 512
-// blocks are in flight, keeping at least 8 chunks of 32 k per slice: each
-// block streams its slice of K with a latency-bound ring, so more, shorter
-// blocks finish sooner.
+// device short of blocks (fewer than 256) splits K (powers of two, up to 8)
+// until about 512 blocks are in flight, keeping at least 8 chunks of 32 k
+// per slice: each block streams its slice of K with a latency-bound ring,
+// so more, shorter blocks finish sooner.  The second launch that adds the
+// slices costs 4-8 us, which a product with K < 1024 does not win back
+// (kv_b_proj, K = 512: 18.4 -> 15.0 + 4.2 us at 256 rows).
 int split_gemm_slices(int M, int N, int K) {
-  if (M >= kSplitGemmBigRows || M <= 0 || N <= 0 || K <= 0) return 1;
+  if (M >= kSplitGemmBigRows || M <= 0 || N <= 0 || K < 1024) return 1;
   const int64_t tiles = (int64_t)((N + 63) / 64) * ((M + 127) / 128);
+  if (tiles >= 256) return 1;
   const int nc = K / 32;  // chunks of the 64 x 128 tiling
   int s = 1;
   while (s < 8 && tiles * s * 2 <= 512 && nc % (2 * s) == 0 && nc / (2 * s) >= 8) s *= 2;
