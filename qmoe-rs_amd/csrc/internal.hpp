@@ -167,10 +167,16 @@ qmla_status launch_prefill_f32(const qmla_prefill_dims &d, const float *q_nope,
                                hipStream_t stream);
 // (dn, dr, dv) combinations the bf16 MFMA prefill takes.
 bool prefill_bf16_supported(int dn, int dr, int dv);
+// Shapes whose bf16 prefill can write the context as records (below).
+bool prefill_bf16_records_supported(int dn, int dr, int dv);
+// With out_records, out receives the context as the split GEMM's activation
+// records of the rows [b s][H dv] (hi halves only; dv 128, seq_q % 32 == 0)
+// instead of [b, H, s, dv].
 qmla_status launch_prefill_bf16(const qmla_prefill_dims &d, const uint16_t *q_nope,
                                 const uint16_t *q_rope, const uint16_t *k,
                                 const uint16_t *k_rope, const uint16_t *v, float scale,
-                                int causal, uint16_t *out, hipStream_t stream);
+                                int causal, uint16_t *out, hipStream_t stream,
+                                int out_records = 0);
 
 // Skinny projections (skinny_gemm.hip): y[m][n] = sum_k x[m][k] W[n][k]
 // (+ bias[n]) for M <= 32 token rows, per z (a head) with z-strides; W in
@@ -274,9 +280,11 @@ constexpr int kSplitGemmMinRows = 128;
 size_t split_gemm_pack_bytes(int M, int K);
 // Packs x into `pack` (split_gemm_pack_bytes(M, K) bytes), then runs the GEMM.
 qmla_status launch_split_gemm(const SplitGemmArgs &a, void *pack, hipStream_t stream);
-// The GEMM over activation records a producer already wrote (f32 x split
-// into hi/lo records of split_gemm_pack_bytes(M, K) bytes; a.x unused).
-qmla_status launch_split_gemm_packed(const SplitGemmArgs &a, const void *xrec, hipStream_t stream);
+// The GEMM over activation records a producer already wrote (split_gemm_
+// pack_bytes(M, K) bytes at most; a.x unused): hi | lo records of f32
+// activations, or with hi_only the hi records of bf16 ones.
+qmla_status launch_split_gemm_packed(const SplitGemmArgs &a, const void *xrec, hipStream_t stream,
+                                     bool hi_only = false);
 
 // Cache row writer shared by the cache API and the layer: copies/converts
 // n_seqs x n_new rows (row-major [n_seqs, n_new, row_elems]) into sequences

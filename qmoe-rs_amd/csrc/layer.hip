@@ -1269,10 +1269,15 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
     ka.out1 = v;
     QMLA_TRY(launch_split_gemm_packed(ka, krec, s));
     qmla_prefill_dims pd{batch, H, seq, seq, dn, dr, dv, 1, 0};
+    // the bf16 attention can write the context straight as o_proj's
+    // activation records (whole 32-token blocks per sequence)
+    const bool ctx_rec = bfa && seq % 32 == 0 && prefill_bf16_records_supported(dn, dr, dv);
     if (bfa)
       QMLA_TRY(launch_prefill_bf16(pd, (const uint16_t *)qn, (const uint16_t *)qr,
                                    (const uint16_t *)k, (const uint16_t *)kr, (const uint16_t *)v,
-                                   (float)g.softmax_scale, 1, (uint16_t *)ctx, s));
+                                   (float)g.softmax_scale, 1,
+                                   ctx_rec ? (uint16_t *)pack : (uint16_t *)ctx, s,
+                                   ctx_rec ? 1 : 0));
     else
       QMLA_TRY(launch_prefill_f32(pd, qn, qr, k, kr, v, (float)g.softmax_scale, 1, ctx, s));
     SplitGemmArgs oa = a;
@@ -1286,6 +1291,7 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
     oa.epi = kSgEpiFinal;
     oa.y = out;
     oa.ldy = g.hidden;
+    if (ctx_rec) return launch_split_gemm_packed(oa, pack, s, /*hi_only=*/true);
     return launch_split_gemm(oa, pack, s);
   }
 

@@ -363,7 +363,7 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
     const uint16_t *__restrict__ q_nope, const uint16_t *__restrict__ q_rope,
     const uint16_t *__restrict__ k, const uint16_t *__restrict__ k_rope,
     const uint16_t *__restrict__ v, qmla_prefill_dims d, float scale_log2, int causal,
-    uint16_t *__restrict__ out, int n_qtiles, int pair_tiles) {
+    uint16_t *__restrict__ out, int n_qtiles, int pair_tiles, int out_records) {
   using SH = PrefillShape<DN, DR, DV>;
   extern __shared__ __attribute__((aligned(16))) char pring_raw[];
   lds_char *ring = (lds_char *)pring_raw;
@@ -630,9 +630,31 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
     constexpr int CPR = DV / 8;        // 16-byte chunks per row
     constexpr int RPI = 64 / CPR;      // rows per store instruction
     constexpr int NI = 32 / RPI;       // store instructions per wave
-    const int lr = lane / CPR, lc = lane % CPR;
+    static_assert(DV % 16 == 0 && DV / 16 == NI, "one record per store instruction");
     bf16x8_t rows[NI];
     wait_lgkm<0>();
+    if (out_records) {
+      // The context as o_proj's activation records (hi halves only): the
+      // rows [b s][H dv], record (token block, k-step), lane l holding row
+      // l % 32 at k = 16 ks + 8 (l / 32) .. + 7.  seq_q % 32 == 0, so the
+      // wave's 32 rows are one token block (host check).
+      if (row_first < d.seq_q) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+          rows[i] = ds_b128<0>(wb + (lane & 31) * STR + (2 * i + (lane >> 5)) * 16);
+        wait_lgkm<0>();
+        const int64_t tb = ((int64_t)b * d.seq_q + row_first) / 32;
+        uint8_t *rec = reinterpret_cast<uint8_t *>(out) +
+                       ((tb * d.heads + h) * NI) * 1024 + lane * 16;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          arrived(rows[i]);
+          *reinterpret_cast<bf16x8_t *>(rec + i * 1024) = rows[i];
+        }
+      }
+      return;
+    }
+    const int lr = lane / CPR, lc = lane % CPR;
 #pragma unroll
     for (int i = 0; i < NI; ++i) rows[i] = ds_b128<0>(wb + (i * RPI + lr) * STR + lc * 16);
     wait_lgkm<0>();
@@ -643,6 +665,7 @@ __global__ __launch_bounds__(kPWaves * 64) void k_prefill_mfma(
       if (r < d.seq_q) *reinterpret_cast<bf16x8_t *>(out + (bhq + r) * DV + lc * 8) = rows[i];
     }
   } else {
+    if (out_records) return;  // the host allows records only with the staged store
     const int row = row_first + n;
     if (row < d.seq_q) {
       uint16_t *dst = out + (bhq + row) * DV;
@@ -663,8 +686,13 @@ template <int DN, int DR, int DV>
 qmla_status launch_prefill_shape(const qmla_prefill_dims &d, const uint16_t *q_nope,
                                  const uint16_t *q_rope, const uint16_t *k,
                                  const uint16_t *k_rope, const uint16_t *v, float scale,
-                                 int causal, uint16_t *out, hipStream_t stream) {
+                                 int causal, uint16_t *out, hipStream_t stream,
+                                 int out_records) {
   using SH = PrefillShape<DN, DR, DV>;
+  constexpr bool kStaged = kPWaves * 32 * (DV * 2 + 16) <= kPStages * SH::STAGE_BYTES;
+  QMLA_REQUIRE(!out_records || (kStaged && DV % 16 == 0 && DV / 16 == 32 / (64 / (DV / 8)) &&
+                                d.seq_q % 32 == 0),
+               QMLA_ERR_UNSUPPORTED, "context records need dv 128 and seq_q %% 32 == 0");
   const int n_qtiles = (d.seq_q + kPRows - 1) / kPRows;
   const int64_t nblocks = (int64_t)d.batch * d.heads * n_qtiles;
   QMLA_REQUIRE(nblocks <= 0x7fffffff, QMLA_ERR_SHAPE, "too many query tiles");
@@ -680,7 +708,7 @@ qmla_status launch_prefill_shape(const qmla_prefill_dims &d, const uint16_t *q_n
   QMLA_TRY(ensure_dynamic_lds((const void *)kern, lds));
   kern<<<dim3((unsigned)nblocks), dim3(kPWaves * 64), lds, stream>>>(
       q_nope, q_rope, k, k_rope, v, d, scale * 1.4426950408889634f, causal, out, n_qtiles,
-      pair_tiles);
+      pair_tiles, out_records);
   QMLA_LAUNCH_CHECK("k_prefill_mfma");
   return QMLA_OK;
 }
@@ -693,26 +721,39 @@ bool prefill_bf16_supported(int dn, int dr, int dv) {
          (dn == 64 && dr == 64 && dv == 64);
 }
 
+bool prefill_bf16_records_supported(int dn, int dr, int dv) {
+  auto staged = [](auto shape) {
+    using SH = decltype(shape);
+    return kPWaves * 32 * (SH::DV * 2 + 16) <= kPStages * SH::STAGE_BYTES;
+  };
+  if (dn == 128 && dr == 64 && dv == 128) return staged(PrefillShape<128, 64, 128>{});
+  if (dn == 32 && dr == 16 && dv == 32) return staged(PrefillShape<32, 16, 32>{});
+  if (dn == 16 && dr == 16 && dv == 32) return staged(PrefillShape<16, 16, 32>{});
+  if (dn == 32 && dr == 0 && dv == 32) return staged(PrefillShape<32, 0, 32>{});
+  if (dn == 64 && dr == 64 && dv == 64) return staged(PrefillShape<64, 64, 64>{});
+  return false;
+}
+
 qmla_status launch_prefill_bf16(const qmla_prefill_dims &d, const uint16_t *q_nope,
                                 const uint16_t *q_rope, const uint16_t *k,
                                 const uint16_t *k_rope, const uint16_t *v, float scale,
-                                int causal, uint16_t *out, hipStream_t stream) {
+                                int causal, uint16_t *out, hipStream_t stream, int out_records) {
   const int dn = d.qk_nope, dr = d.qk_rope, dv = d.v_dim;
   if (dn == 128 && dr == 64 && dv == 128)
     return launch_prefill_shape<128, 64, 128>(d, q_nope, q_rope, k, k_rope, v, scale, causal, out,
-                                              stream);
+                                              stream, out_records);
   if (dn == 32 && dr == 16 && dv == 32)
     return launch_prefill_shape<32, 16, 32>(d, q_nope, q_rope, k, k_rope, v, scale, causal, out,
-                                            stream);
+                                            stream, out_records);
   if (dn == 16 && dr == 16 && dv == 32)
     return launch_prefill_shape<16, 16, 32>(d, q_nope, q_rope, k, k_rope, v, scale, causal, out,
-                                            stream);
+                                            stream, out_records);
   if (dn == 32 && dr == 0 && dv == 32)
     return launch_prefill_shape<32, 0, 32>(d, q_nope, q_rope, k, k_rope, v, scale, causal, out,
-                                           stream);
+                                           stream, out_records);
   if (dn == 64 && dr == 64 && dv == 64)
     return launch_prefill_shape<64, 64, 64>(d, q_nope, q_rope, k, k_rope, v, scale, causal, out,
-                                            stream);
+                                            stream, out_records);
   return fail(QMLA_ERR_UNSUPPORTED,
               "bf16 prefill for (qk_nope, qk_rope, v_dim) = (%d, %d, %d); supported: "
               "(128,64,128) (64,64,64) (32,16,32) (16,16,32) (32,0,32)",

@@ -469,10 +469,11 @@ qmla_status sg_run(const SplitGemmArgs &a0, const uint8_t *xrec, bool xlo, hipSt
 }
 }  // namespace
 
-qmla_status launch_split_gemm_packed(const SplitGemmArgs &a, const void *xrec, hipStream_t s) {
+qmla_status launch_split_gemm_packed(const SplitGemmArgs &a, const void *xrec, hipStream_t s,
+                                     bool hi_only) {
   QMLA_TRY(sg_check(a));
-  QMLA_REQUIRE(a.x_heads == 0 && xrec, QMLA_ERR_SHAPE, "packed activations: f32 rows only");
-  return sg_run(a, static_cast<const uint8_t *>(xrec), true, s);
+  QMLA_REQUIRE(xrec, QMLA_ERR_SHAPE, "packed activations without records");
+  return sg_run(a, static_cast<const uint8_t *>(xrec), !hi_only, s);
 }
 
 qmla_status launch_split_gemm(const SplitGemmArgs &a, void *pack, hipStream_t s) {
