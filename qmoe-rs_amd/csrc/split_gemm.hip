@@ -331,33 +331,151 @@ __global__ __launch_bounds__(kSgThreads) void k_split_gemm(SplitGemmArgs a, cons
     compute(c, c + NST - 1 < NC ? c + NST - 1 : -1);
   }
 
-  // ---- epilogue: one call per (output block, row block), with
-  // compile-time indices so that the accumulators stay in registers
+  // ---- epilogue, staged through the idle ring.  Stored straight from the
+  // accumulators, each store instruction would write 16 bytes into each of
+  // 32 rows; instead each wave writes its accumulators for PN outputs of
+  // 32 rows into its own staging rows and reads them back as whole row
+  // segments (16 lanes per 64 outputs), so each store instruction covers
+  // RPI rows of contiguous outputs.  Per-row and per-column address parts
+  // are computed once (incremental sequence positions, one division per
+  // pass).
+  sg_barrier();  // every wave is done with the ring
+  constexpr int PA = NBW >= 2 ? 2 : 1;  // accumulator columns per pass
+  constexpr int PN = 32 * PA;           // outputs per pass
+  constexpr int SROW = PN * 4 + 16;     // staged row stride in bytes (padded)
+  constexpr int CPR = PN / 4;           // 16-byte chunks per staged row
+  constexpr int RPI = 64 / CPR;         // rows per read instruction
+  constexpr int NI = 32 / RPI;
+  static_assert(8 * 32 * SROW <= NST * STAGE, "staging fits the ring");
+  char *wst = sg_lds + wave * 32 * SROW;
   const int half = lane >> 5, mr = lane & 31;
-  auto emit = [&](const floatx16_t &v16, int nb, int m) __attribute__((always_inline)) {
-    if (m >= a.M) return;
+  const int lrow = lane / CPR, lch = lane % CPR;
+  const bool partial = a.ksplit > 1;
+  // one call per row block j, with compile-time j and pass indices so that
+  // the accumulators stay in registers
+  auto row_block = [&](auto jc) __attribute__((always_inline)) {
+    constexpr int j = decltype(jc)::value;
+    const int m0 = bm * BM + (wm * MBW + j) * 32;
+    if (m0 >= a.M) return;
+    // this lane's rows m0 + lrow + RPI ii: sequence b and position s
+    int rb[NI], rs[NI];
+    {
+      const int mf = m0 + lrow;
+      int b = mf / a.seq, sq = mf - b * a.seq;
 #pragma unroll
-    for (int jq = 0; jq < 4; ++jq) {
-      const int n0 = nb * 32 + 8 * jq + 4 * half;
-      if (n0 >= a.N) continue;
-      float v[4];
-      if (a.ksplit > 1) {
-        // raw partial sums of this slice
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = v16[4 * jq + e];
-        sg_put4<float>(a.part + ((int64_t)blockIdx.y * a.M + m) * a.N + n0, v);
-        continue;
+      for (int ii = 0; ii < NI; ++ii) {
+        rb[ii] = b;
+        rs[ii] = sq;
+        sq += RPI;
+        while (sq >= a.seq) {
+          sq -= a.seq;
+          ++b;
+        }
       }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = v16[4 * jq + e] + (a.bias ? a.bias[n0 + e] : 0.f);
-      sg_store4<EPI, OutT>(a, m, n0, v);
     }
+    auto pass = [&](auto pc) __attribute__((always_inline)) {
+      constexpr int pp = decltype(pc)::value;
+      // the pass's accumulators into this wave's staging rows
+#pragma unroll
+      for (int ii = 0; ii < PA; ++ii)
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq)
+          *reinterpret_cast<floatx4_t *>(wst + mr * SROW + (ii * 32 + 8 * jq + 4 * half) * 4) =
+              floatx4_t{acc[pp * PA + ii][j][4 * jq], acc[pp * PA + ii][j][4 * jq + 1],
+                        acc[pp * PA + ii][j][4 * jq + 2], acc[pp * PA + ii][j][4 * jq + 3]};
+      // this lane's four outputs n0 .. n0 + 3 of the pass: destination and
+      // column part of the address
+      const int n0 = bn * BN + (wn * NBW + pp * PA) * 32 + lch * 4;
+      const bool col_ok = n0 < a.N;
+      int kind = 0;  // 0 rows y / partials, 1 q_nope, 2 q_rope, 3 kv_a, 4 k, 5 v
+      int64_t coff = n0;
+      int p = 0;
+      float bias4[4] = {0.f, 0.f, 0.f, 0.f};
+      if (!partial && col_ok) {
+        if (a.bias)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bias4[e] = a.bias[n0 + e];
+        if constexpr (EPI == kSgEpiQkv) {
+          const int qw = a.dn + a.dr, nq = a.heads * qw;
+          if (n0 >= nq) {
+            kind = 3;
+            coff = n0 - nq;
+          } else {
+            const int hd = n0 / qw, d = n0 - hd * qw;
+            if (d < a.dn) {
+              kind = 1;
+              coff = (int64_t)hd * a.seq * a.dn + d;
+            } else {
+              kind = 2;
+              p = (d - a.dn) >> 1;
+              coff = (int64_t)hd * a.seq * a.dr + (d - a.dn);
+            }
+          }
+        } else if constexpr (EPI == kSgEpiKvb) {
+          const int kw = a.dn + a.dv, hd = n0 / kw, d = n0 - hd * kw;
+          if (d < a.dn) {
+            kind = 4;
+            coff = (int64_t)hd * a.seq * a.dn + d;
+          } else {
+            kind = 5;
+            coff = (int64_t)hd * a.seq * a.dv + (d - a.dn);
+          }
+        }
+      }
+      pipe::wait_lgkm<0>();  // the staging writes are done
+#pragma unroll
+      for (int ii = 0; ii < NI; ++ii) {
+        const int r = lrow + RPI * ii, m = m0 + r;
+        const floatx4_t q = *reinterpret_cast<const floatx4_t *>(wst + r * SROW + lch * 16);
+        if (m >= a.M || !col_ok) continue;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = q[e] + bias4[e];
+        if (partial) {
+          sg_put4<float>(a.part + ((int64_t)blockIdx.y * a.M + m) * a.N + n0, v);
+          continue;
+        }
+        if constexpr (EPI == kSgEpiFinal) {
+          sg_put4<float>(a.y + (int64_t)m * a.ldy + coff, v);
+        } else {
+          // (b H + h) s_len + s = b H s_len + s + h s_len: the row part
+          const int64_t rowp = ((int64_t)rb[ii] * a.heads) * a.seq + rs[ii];
+          if constexpr (EPI == kSgEpiQkv) {
+            if (kind == 3) {
+              sg_put4<float>(a.kva + (int64_t)m * a.kva_ld + coff, v);
+            } else if (kind == 1) {
+              sg_put4<OutT>(reinterpret_cast<OutT *>(a.out0) + rowp * a.dn + coff, v);
+            } else {
+              // interleaved pairs (2p, 2p + 1) of q_rope (src/model.rs:70-84)
+              const float pos = (float)(a.lens[rb[ii]] + rs[ii]);
+              float rr[4];
+#pragma unroll
+              for (int u = 0; u < 2; ++u) {
+                const float ang = pos * a.inv_freq[p + u];
+                const float cs = cosf(ang) * a.mscale, sn = sinf(ang) * a.mscale;
+                rr[2 * u] = v[2 * u] * cs - v[2 * u + 1] * sn;
+                rr[2 * u + 1] = v[2 * u + 1] * cs + v[2 * u] * sn;
+              }
+              sg_put4<OutT>(reinterpret_cast<OutT *>(a.out1) + rowp * a.dr + coff, rr);
+            }
+          } else {  // kSgEpiKvb
+            if (kind == 4)
+              sg_put4<OutT>(reinterpret_cast<OutT *>(a.out0) + rowp * a.dn + coff, v);
+            else
+              sg_put4<OutT>(reinterpret_cast<OutT *>(a.out1) + rowp * a.dv + coff, v);
+          }
+        }
+      }
+      // the next pass rewrites the staging rows after this lane's reads
+      pipe::wait_lgkm<0>();
+    };
+    [&]<int... P>(std::integer_sequence<int, P...>) {
+      (pass(std::integral_constant<int, P>{}), ...);
+    }(std::make_integer_sequence<int, NBW / PA>{});
   };
-  [&]<int... IJ>(std::integer_sequence<int, IJ...>) {
-    (emit(acc[IJ / MBW][IJ % MBW], bn * NBT + wn * NBW + IJ / MBW,
-          bm * BM + (wm * MBW + IJ % MBW) * 32 + mr),
-     ...);
-  }(std::make_integer_sequence<int, NBW * MBW>{});
+  [&]<int... J>(std::integer_sequence<int, J...>) {
+    (row_block(std::integral_constant<int, J>{}), ...);
+  }(std::make_integer_sequence<int, MBW>{});
 }
 
 template <class CF, bool XLO>
