@@ -98,6 +98,15 @@ __device__ inline uint32_t pack_bf16x2(float a, float b) {
          (static_cast<uint32_t>(f32_to_bf16_bits(b)) << 16);
 }
 
+// cos(ang) * mscale and sin(ang) * mscale of a RoPE angle (src/model.rs:
+// 63-64): one shared argument reduction for both.
+__device__ __forceinline__ void rope_cs(float ang, float mscale, float &cs, float &sn) {
+  float s, c;
+  sincosf(ang, &s, &c);
+  cs = c * mscale;
+  sn = s * mscale;
+}
+
 constexpr int kWave = 64;
 
 // Combines a value with the one held by lane (l ^ 32): returns own and

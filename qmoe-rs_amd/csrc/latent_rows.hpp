@@ -80,7 +80,8 @@ __device__ inline void latent_row(const LatentRowsArgs &a, int tok, float *lds) 
   const float pos = (float)(len + i);
   for (int p = threadIdx.x; p < dr / 2; p += blockDim.x) {
     const float ang = pos * a.inv_freq[p];
-    const float cs = cosf(ang) * a.mscale, sn = sinf(ang) * a.mscale;
+    float cs, sn;
+    rope_cs(ang, a.mscale, cs, sn);
     const float e = x[r + 2 * p], o = x[r + 2 * p + 1];
     put(r + 2 * p, e * cs - o * sn);
     put(r + 2 * p + 1, o * cs + e * sn);

@@ -395,7 +395,8 @@ __global__ __launch_bounds__(256) void k_prefill_rows(LatentRowsArgs a, int n, u
   const float pos = (float)i;
   for (int p = lane; p < dr / 2; p += 64) {
     const float ang = pos * a.inv_freq[p];
-    const float cs = cosf(ang) * a.mscale, sn = sinf(ang) * a.mscale;
+    float cs, sn;
+    rope_cs(ang, a.mscale, cs, sn);
     const float e = src[r + 2 * p], o = src[r + 2 * p + 1];
     const float re = e * cs - o * sn, ro = o * cs + e * sn;
     if (a.bf16) {
@@ -476,7 +477,8 @@ __global__ __launch_bounds__(64) void k_split_rope_q(const float *__restrict__ q
   const float pos = (float)(lens[b] + i);
   for (int p = threadIdx.x; p < dr / 2; p += blockDim.x) {
     const float ang = pos * inv_freq[p];
-    const float cs = cosf(ang) * mscale, sn = sinf(ang) * mscale;
+    float cs, sn;
+    rope_cs(ang, mscale, cs, sn);
     const float e = src[dn + 2 * p], od = src[dn + 2 * p + 1];
     put(q_rope + o * dr + 2 * p, e * cs - od * sn);
     put(q_rope + o * dr + 2 * p + 1, od * cs + e * sn);

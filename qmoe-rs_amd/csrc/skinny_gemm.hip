@@ -242,7 +242,8 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_gemm(SkinnyGemmArgs a, Laten
       const int b = mg / a.seq, i = mg - b * a.seq;
       const float pos = (float)(a.lens[b] + i);
       const float ang = pos * a.inv_freq[p];
-      const float cs = cosf(ang) * a.mscale, sn = sinf(ang) * a.mscale;
+      float cs, sn;
+      rope_cs(ang, a.mscale, cs, sn);
       float *y = (grp ? a.q_rope1 : a.q_rope) + ((int64_t)mg * a.heads + hd) * a.dr + 2 * p;
       y[0] = v0 * cs - v1 * sn;
       y[1] = v1 * cs + v0 * sn;

@@ -158,7 +158,8 @@ __device__ __forceinline__ void sg_store4(const SplitGemmArgs &a, int m, int n0,
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const float ang = pos * a.inv_freq[p + u];
-        const float cs = cosf(ang) * a.mscale, sn = sinf(ang) * a.mscale;
+        float cs, sn;
+        rope_cs(ang, a.mscale, cs, sn);
         r[2 * u] = v[2 * u] * cs - v[2 * u + 1] * sn;
         r[2 * u + 1] = v[2 * u + 1] * cs + v[2 * u] * sn;
       }
@@ -452,7 +453,8 @@ __global__ __launch_bounds__(kSgThreads) void k_split_gemm(SplitGemmArgs a, cons
 #pragma unroll
               for (int u = 0; u < 2; ++u) {
                 const float ang = pos * a.inv_freq[p + u];
-                const float cs = cosf(ang) * a.mscale, sn = sinf(ang) * a.mscale;
+                float cs, sn;
+                rope_cs(ang, a.mscale, cs, sn);
                 rr[2 * u] = v[2 * u] * cs - v[2 * u + 1] * sn;
                 rr[2 * u + 1] = v[2 * u + 1] * cs + v[2 * u] * sn;
               }
