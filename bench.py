@@ -59,6 +59,9 @@ ROW_ELEMS = 576            # kv_lora_rank 512 + rope 64
 ROW_BYTES = ROW_ELEMS * 2  # bf16
 SCALE = 192 ** -0.5
 METRIC = "MLA decode tok/s + HBM GB/s (% of peak); prefill TFLOP/s (% MFMA peak)"
+# Warm-up time of every secondary line (beyond its --warmup steps): the
+# clock settles ~20 ms into sustained load after a start from idle.
+WARM_MS = 25.0
 
 
 def log(*a):
@@ -79,17 +82,38 @@ def fill_bf16(dst_ptr: int, n: int, seed: int, tmp: qmla.DeviceBuffer, stream):
 STATS = {}  # per-step event statistics of the last time_steps call
 
 
-def time_steps(step, steps: int, warmup: int, stream):
+def time_steps(step, steps: int, warmup: int, stream, min_warm_ms: float = 0.0, max_extra: int = 1 << 30):
     """Runs warmup steps, then times exactly `steps` back-to-back steps on
     the launch stream twice, synchronised on both sides of each pass.  Pass
     1 is bracketed by one HIP event pair and gives the mean: nothing is
     enqueued between its steps.  Pass 2 records an event after every step
     for the per-step distribution (median, p10, p90 in STATS); each such
     event leaves the GPU idle for ~3 us before the next step, which pass 1
-    excludes.  Returns (wall ms per step, event ms per step) of pass 1."""
+    excludes.  Returns (wall ms per step, event ms per step) of pass 1.
+
+    With min_warm_ms the warmup continues past `warmup` steps until that
+    much GPU time has run (the secondary lines: the power controller's
+    transient after a start from idle lasts ~20 ms of sustained load, and a
+    fixed step count covers very different times for 40 us and 1 ms
+    steps).  The headline uses exactly `warmup` steps."""
     for i in range(warmup):
         step(i)
     stream.sync()
+    done = warmup
+    if min_warm_ms > 0:
+        e0, e1 = qmla.Event(), qmla.Event()
+        e0.record(stream)
+        step(done)
+        done += 1
+        e1.record(stream)
+        stream.sync()
+        per = max(e0.elapsed_ms(e1), 1e-3)
+        extra = max(0, min(int(math.ceil(min_warm_ms / per)), max_extra - 1))
+        for i in range(extra):
+            step(done + i)
+        done += extra
+        stream.sync()
+    warmup = done
     e0, e1 = qmla.Event(), qmla.Event()
     t0 = time.perf_counter()
     e0.record(stream)
@@ -107,7 +131,7 @@ def time_steps(step, steps: int, warmup: int, stream):
     stream.sync()
     per = np.array([ev[i].elapsed_ms(ev[i + 1]) for i in range(steps)])
     STATS.clear()
-    STATS.update({"p10_ms": float(np.percentile(per, 10)), "median_ms": float(np.median(per)),
+    STATS.update({"warmup_steps": warmup, "p10_ms": float(np.percentile(per, 10)), "median_ms": float(np.median(per)),
                   "p90_ms": float(np.percentile(per, 90)), "min_ms": float(per.min()), "max_ms": float(per.max()),
                   "per_step_events": True,
                   "pass": "a second pass of the same K steps with an event after every step; each event leaves "
@@ -150,8 +174,8 @@ class DecodeBench:
         qmla.decode_absorbed(self.caches[i % self.replicas], self.batch, self.heads, self.q_lat, self.q_rope,
                              SCALE, self.out, self.lse, qmla.BF16, self.ws, self.ws_bytes, stream=self.stream)
 
-    def run(self, steps, warmup):
-        wall, ev = time_steps(self.step, steps, warmup, self.stream)
+    def run(self, steps, warmup, min_warm_ms=0.0):
+        wall, ev = time_steps(self.step, steps, warmup, self.stream, min_warm_ms)
         t = ev * 1e-3
         gbs = self.cache_bytes / t / 1e9
         flops = self.tokens * self.heads * (2 * ROW_ELEMS + 2 * 512)
@@ -193,8 +217,8 @@ class PrefillBench:
         qmla.fused_prefill_attn(*self.bufs, SCALE, True, dims=self.dims, dtype=qmla.BF16, out=self.out,
                                 stream=self.stream)
 
-    def run(self, steps, warmup):
-        wall, ev = time_steps(self.step, steps, warmup, self.stream)
+    def run(self, steps, warmup, min_warm_ms=0.0):
+        wall, ev = time_steps(self.step, steps, warmup, self.stream, min_warm_ms)
         tf = self.flops / (ev * 1e-3) / 1e12
         return {"tflops": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS, "ms_per_step": ev,
                 "wall_ms_per_step": wall, "gflop_per_step": self.flops / 1e9,
@@ -269,11 +293,14 @@ class LayerDecodeBench:
             layer.handle, self.xs.ptr, self.batch, 1, cache.handle, self.out.ptr, self.ws.ptr,
             self.ws_bytes, qmla._sh(self.stream)))
 
-    def run(self, steps, warmup):
+    def run(self, steps, warmup, min_warm_ms=0.0):
         nc = len(self.caches)
         assert (warmup + 2 * steps) / nc <= 512, "each page pool has room for 512 new tokens per sequence"
         pools0 = [c.pool_info() for c in self.caches]
-        wall, ev = time_steps(self.step, steps, warmup, self.stream)
+        # extra warmup steps only while every pool keeps room for the timed steps
+        wall, ev = time_steps(self.step, steps, warmup, self.stream, min_warm_ms,
+                              max_extra=512 * nc - warmup - 2 * steps - nc)
+        warmup = STATS["warmup_steps"]
         assert all(c.pool_info()[0] == p[0] for c, p in zip(self.caches, pools0)), "a pool grew: a step allocated"
         t = ev * 1e-3
         mean_ctx = self.ctx + (warmup + (steps + 1) / 2.0) / nc
@@ -319,9 +346,9 @@ class LayerPrefillBench:
             self.layer.handle, self.xs.ptr, self.batch, self.seq, c.handle, self.out.ptr, self.ws.ptr,
             self.ws_bytes, qmla._sh(self.stream)))
 
-    def run(self, steps, warmup):
+    def run(self, steps, warmup, min_warm_ms=0.0):
         b, s, H = self.batch, self.seq, self.heads
-        wall, ev = time_steps(self.step, steps, warmup, self.stream)
+        wall, ev = time_steps(self.step, steps, warmup, self.stream, min_warm_ms)
         step_ms = dict(STATS)
         # the decompression alone, over a cache the steps above filled
         c = self.caches[0]
@@ -545,8 +572,8 @@ class MoEBench:
         self.layers[i % len(self.layers)].forward_device(self.xs, self.tokens, self.out, self.ws, self.ws_bytes,
                                                          self.idx, None, self.stream)
 
-    def run(self, steps, warmup):
-        wall, ev = time_steps(self.step, steps, warmup, self.stream)
+    def run(self, steps, warmup, min_warm_ms=0.0):
+        wall, ev = time_steps(self.step, steps, warmup, self.stream, min_warm_ms)
         active = len(np.unique(self.idx.to_numpy(np.int32, (self.tokens, self.cfg.top_k), self.stream)))
         c = self.cfg
         hbm = active * self.expert_bytes + 4 * (c.num_experts * c.hidden_dim + 2 * self.tokens * c.hidden_dim)
@@ -814,15 +841,15 @@ def main():
         return
     if args.moe_only:
         mb = MoEBench(stream)
-        print(json.dumps({"moe_layer": mb.run(args.steps, args.warmup)}), flush=True)
+        print(json.dumps({"moe_layer": mb.run(args.steps, args.warmup, WARM_MS)}), flush=True)
         return
     if args.layer_only:
         lb = LayerDecodeBench(stream, seed=51)
-        print(json.dumps({"layer_decode_step": lb.run(args.steps, args.warmup)}), flush=True)
+        print(json.dumps({"layer_decode_step": lb.run(args.steps, args.warmup, WARM_MS)}), flush=True)
         return
     if args.layer_prefill_only:
         lp = LayerPrefillBench(stream, seed=61)
-        print(json.dumps({"layer_prefill": lp.run(max(3, args.steps // 5), 3)}), flush=True)
+        print(json.dumps({"layer_prefill": lp.run(max(3, args.steps // 5), 3, WARM_MS)}), flush=True)
         return
     if args.sweeps_only:
         sw = Batch1Sweeps(stream, seed=71)
@@ -833,7 +860,7 @@ def main():
         res = {}
         for name, dims in (("causal_prefill", (4, 16, 2048, 2048, 0)), ("chunked_prefill", (8, 128, 512, 8704, 8192))):
             pb = PrefillBench(*dims, stream, seed=31 if name == "causal_prefill" else 41)
-            res[name] = pb.run(args.steps, args.warmup)
+            res[name] = pb.run(args.steps, args.warmup, WARM_MS)
             del pb
         print(json.dumps(res), flush=True)
         return
@@ -849,21 +876,21 @@ def main():
     secondary = {}
     if not args.no_secondary:
         d2 = DecodeBench(np.full(32, 4097, np.int32), 16, stream, seed=21)
-        secondary["v2lite_decode"] = {"workload": "16 heads, batch 32, 4096 cached + 1, bf16 latent", **d2.run(args.steps, args.warmup)}
+        secondary["v2lite_decode"] = {"workload": "16 heads, batch 32, 4096 cached + 1, bf16 latent", **d2.run(args.steps, args.warmup, WARM_MS)}
         if not args.no_cpu_baseline:
             secondary["v2lite_decode"]["cpu_baseline"] = cpu_baseline_v2lite()
         log("v2lite decode", json.dumps(secondary["v2lite_decode"]))
         del d2
         p3 = PrefillBench(4, 16, 2048, 2048, 0, stream, seed=31)
         secondary["causal_prefill"] = {"workload": "batch 4, 2048 tokens, 16 heads, dn 128 dr 64 dv 128, bf16, causal",
-                                       **p3.run(args.steps, args.warmup)}
+                                       **p3.run(args.steps, args.warmup, WARM_MS)}
         if not args.no_cpu_baseline:
             secondary["causal_prefill"]["cpu_baseline"] = cpu_baseline_prefill()
         log("causal prefill", json.dumps(secondary["causal_prefill"]))
         del p3
         p5 = PrefillBench(8, 128, 512, 8704, 8192, stream, seed=41)
         secondary["chunked_prefill"] = {"workload": "batch 8, 8192 cached + 512 new, 128 heads, bf16, causal in chunk",
-                                        **p5.run(args.steps, max(1, args.warmup // 2))}
+                                        **p5.run(args.steps, max(1, args.warmup // 2), WARM_MS)}
         if not args.no_cpu_baseline:
             secondary["chunked_prefill"]["cpu_baseline"] = cpu_baseline_chunked()
         log("chunked prefill", json.dumps(secondary["chunked_prefill"]))
@@ -873,7 +900,7 @@ def main():
             "workload": "MlaAttention forward_with_cache, hidden 2048, 16 heads, r 512, batch 32, "
                         "4096 cached + 1, f32 weights, bf16 latent cache in growth mode (256-row pages "
                         "taken from a pre-sized pool)",
-            **lb.run(args.steps, args.warmup)}
+            **lb.run(args.steps, args.warmup, WARM_MS)}
         if not args.no_cpu_baseline:
             secondary["layer_decode_step"]["cpu_baseline"] = cpu_baseline_layer()
         log("layer decode step", json.dumps(secondary["layer_decode_step"]))
@@ -883,7 +910,7 @@ def main():
             "workload": "MlaAttention forward_prefill, batch 4 x 2048 tokens, hidden 2048, 16 heads, r 512, "
                         "f32 weights (projections as split bf16 GEMMs, f32 accumulation), bf16 latent cache "
                         "(attention on the bf16 MFMA prefill)",
-            **lp.run(max(3, args.steps // 5), 3)}
+            **lp.run(max(3, args.steps // 5), 3, WARM_MS)}
         if not args.no_cpu_baseline:
             secondary["layer_prefill"]["cpu_baseline"] = cpu_baseline_layer_prefill()
         log("layer prefill", json.dumps(secondary["layer_prefill"]))
@@ -912,7 +939,7 @@ def main():
             "cpu_baseline": None if cb1 is None else {k: cb1[k] for k in ("cores", "kind", "cpu_model", "what")}}
         log("batch-1 sweeps", json.dumps({"decode": dsw, "prefill": psw}))
         mb = MoEBench(stream)
-        moe = mb.run(args.steps, args.warmup)
+        moe = mb.run(args.steps, args.warmup, WARM_MS)
         del mb
         secondary["moe_layer"] = {
             "workload": "QMoELayer forward, 16 tokens, 32 experts, top-4, hidden 2048, intermediate 1408, "
