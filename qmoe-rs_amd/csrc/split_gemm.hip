@@ -17,9 +17,11 @@
 // + 8 (l / 32) .. + 7, first the hi halves of the 64 lanes (1 KB), then the
 // lo halves (1 KB).  The weights are packed once when the layer is created
 // (skinny_pack); the activations are packed per call by k_pack_rows (a
-// pass that reads x once), so that the GEMM moves both operands with
-// direct-to-LDS DMA of contiguous 1 KB runs and holds nothing in flight in
-// registers.
+// pass that reads x once) or written as records by the kernel that
+// produces them (the prefill's latent rows kernel for kv_b_proj, the bf16
+// attention's epilogue for o_proj), so that the GEMM moves both operands
+// with direct-to-LDS DMA of contiguous 1 KB runs and holds nothing in
+// flight in registers.
 //
 // Block: 8 waves (two per SIMD) on a BN x BM output tile; wave (wn, wm)
 // owns NBW 32-output blocks x MBW 32-row blocks (BN = 32 NBW WN, BM = 32
@@ -31,9 +33,13 @@
 // rows run 256 x 256 tiles (each wave 128 outputs x 64 rows, one k-step per
 // chunk, three stages: 96 KB of LDS); fewer rows 64 x 128 tiles.
 //
+// Few rows: K is split over up to 8 blocks per tile, whose raw partial sums
+// a second launch (k_sg_reduce) adds in slice order before the epilogue.
+//
 // Epilogues (lane l of a 32 x 32 accumulator holds row m = l % 32 and
 // outputs n = 8 (j / 4) + 4 (l / 32) + j % 4, j < 16: four runs of 4
-// consecutive outputs):
+// consecutive outputs), staged through the idle LDS ring so that rows
+// leave as contiguous segments:
 //   FINAL  y[m ldy + n] (+ bias), f32
 //   QKV    [q_proj | kv_a_proj_with_mqa]: q_nope and the roped q_rope in
 //          the attention's [b, H, s, d] layout (positions lens[b] + s,
