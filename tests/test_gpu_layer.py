@@ -157,6 +157,35 @@ def test_bf16_cache_prefill_spans_query_tiles(qmla_gpu):
     assert list(cache.lengths()) == [s] * b
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("b,s", [(2, 96), (1, 160)])
+def test_prefill_split_gemms_at_small_latent_dims(qmla_gpu, dt, b, s):
+    """forward_prefill through the hand-written split GEMMs at the tiny
+    CPU-path head shapes (hidden 512, 8 heads, kv_lora_rank 64, dn 32, dr 16,
+    dv 32): K = 64 for kv_b_proj (two chunks), the latent rows kernel with
+    eight lanes per row, and with a bf16 cache the context written as
+    records (s % 32 == 0).  Against the oracle's decompressed path, then two
+    decode steps."""
+    q = qmla_gpu
+    hidden, H, dn, dr, dv, r = 512, 8, 32, 16, 32, 64
+    w = O.MlaWeights.random(hidden, H, dn, dr, dv, r, seed=2100 + s)
+    layer = q.MlaLayer(w)
+    xs = O.normal((b, s, hidden), 2101)
+    cache = q.KVCache([s + 2] * b, r, dr, q.F32 if dt == "f32" else q.BF16)
+    out = layer.forward_prefill(xs, cache)
+    ref, (k, v, kr) = O.mla_forward_prefill(w, xs)
+    tol = TOL if dt == "f32" else 2e-2
+    err = rel_err(out, ref)
+    print(f"small-dims prefill {b}x{s} {dt} rel_err={err:.2e}", flush=True)
+    assert err < tol
+    for step in range(2):
+        x1 = O.normal((b, 1, hidden), 2110 + step)
+        out1 = layer.forward_with_cache(x1, cache)
+        ref1, (k, v, kr) = O.mla_forward_with_cache(w, x1, k, v, kr, return_cache=True)
+        assert rel_err(out1, ref1) < tol
+    assert list(cache.lengths()) == [s + 2] * b
+
+
 def _ragged_cache(q, lens, r, dr, dtype, seed, spare=2):
     """A cache whose sequences hold `lens` random latent rows (N(0,1); bf16
     rounded for a bf16 cache) with `spare` free rows each; returns the cache
