@@ -353,7 +353,7 @@ __global__ __launch_bounds__(kSgThreads) void k_split_gemm(SplitGemmArgs a, cons
   constexpr int CPR = PN / 4;           // 16-byte chunks per staged row
   constexpr int RPI = 64 / CPR;         // rows per read instruction
   constexpr int NI = 32 / RPI;
-  static_assert(8 * 32 * SROW <= NST * STAGE, "staging fits the ring");
+  // (the launch sizes the ring for the staging rows when they need more)
   char *wst = sg_lds + wave * 32 * SROW;
   const int half = lane >> 5, mr = lane & 31;
   const int lrow = lane / CPR, lch = lane % CPR;
@@ -486,10 +486,14 @@ __global__ __launch_bounds__(kSgThreads) void k_split_gemm(SplitGemmArgs a, cons
   }(std::make_integer_sequence<int, MBW>{});
 }
 
+// The ring, or the epilogue's staging rows (8 waves x 32 rows of 32 or 64
+// f32 outputs, padded) when they need more.
 template <class CF, bool XLO>
 constexpr size_t sg_lds_bytes() {
   constexpr int MBT = CF::MBW * (8 / CF::WN), NBT = CF::NBW * CF::WN;
-  return (size_t)CF::NST * CF::KSC * (NBT * kFrag + MBT * (XLO ? 2048 : 1024));
+  constexpr size_t ring = (size_t)CF::NST * CF::KSC * (NBT * kFrag + MBT * (XLO ? 2048 : 1024));
+  constexpr size_t staging = (size_t)8 * 32 * (32 * (CF::NBW >= 2 ? 2 : 1) * 4 + 16);
+  return ring > staging ? ring : staging;
 }
 
 template <class CF, bool XLO>
