@@ -138,47 +138,85 @@ __global__ __launch_bounds__(256) void k_pack_rows(SplitGemmArgs a, uint8_t *__r
   }
 }
 
-// The epilogue of four consecutive outputs n0 .. n0 + 3 of row m (bias
-// included in v).
-template <int EPI, typename OutT>
-__device__ __forceinline__ void sg_store4(const SplitGemmArgs &a, int m, int n0,
-                                          const float (&v)[4]) {
-  const int b = m / a.seq, s = m - b * a.seq;
-  if constexpr (EPI == kSgEpiFinal) {
-    sg_put4<float>(a.y + (int64_t)m * a.ldy + n0, v);
-  } else if constexpr (EPI == kSgEpiQkv) {
+// The epilogue's destination of four consecutive outputs n0 .. n0 + 3
+// (n0 % 4 == 0), split into a column part, computed once per column group,
+// and a row part.  Kinds: rows of y (FINAL), q_nope, q_rope (pair p) and the
+// kv_a rows (QKV), k and v (KVB).
+enum SgKind { kSgY, kSgQNope, kSgQRope, kSgKva, kSgK, kSgV };
+struct SgCol {
+  int kind;
+  int p;         // q_rope: first pair of the four outputs
+  int64_t coff;  // column part of the element offset
+};
+
+template <int EPI>
+__device__ __forceinline__ SgCol sg_col(const SplitGemmArgs &a, int n0) {
+  SgCol c{kSgY, 0, n0};
+  if constexpr (EPI == kSgEpiQkv) {
     const int qw = a.dn + a.dr, nq = a.heads * qw;
     if (n0 >= nq) {
-      sg_put4<float>(a.kva + (int64_t)m * a.kva_ld + (n0 - nq), v);
-      return;
-    }
-    const int hd = n0 / qw, d = n0 - hd * qw;
-    const int64_t row = ((int64_t)b * a.heads + hd) * a.seq + s;
-    if (d < a.dn) {
-      sg_put4<OutT>(reinterpret_cast<OutT *>(a.out0) + row * a.dn + d, v);
+      c.kind = kSgKva;
+      c.coff = n0 - nq;
     } else {
-      // interleaved pairs (2p, 2p + 1) of q_rope (src/model.rs:70-84)
-      const int p = (d - a.dn) >> 1;
-      const float pos = (float)(a.lens[b] + s);
-      float r[4];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const float ang = pos * a.inv_freq[p + u];
-        float cs, sn;
-        rope_cs(ang, a.mscale, cs, sn);
-        r[2 * u] = v[2 * u] * cs - v[2 * u + 1] * sn;
-        r[2 * u + 1] = v[2 * u + 1] * cs + v[2 * u] * sn;
+      // head hd's rows of [b, H, s, d]: ((b H + hd) s_len + s) d_w + d is the
+      // row part (b H s_len + s) d_w plus the column part hd s_len d_w + d
+      const int hd = n0 / qw, d = n0 - hd * qw;
+      if (d < a.dn) {
+        c.kind = kSgQNope;
+        c.coff = (int64_t)hd * a.seq * a.dn + d;
+      } else {
+        c.kind = kSgQRope;
+        c.p = (d - a.dn) >> 1;
+        c.coff = (int64_t)hd * a.seq * a.dr + (d - a.dn);
       }
-      sg_put4<OutT>(reinterpret_cast<OutT *>(a.out1) + row * a.dr + (d - a.dn), r);
     }
-  } else {  // kSgEpiKvb
-    const int kw = a.dn + a.dv;
-    const int hd = n0 / kw, d = n0 - hd * kw;
-    const int64_t row = ((int64_t)b * a.heads + hd) * a.seq + s;
-    if (d < a.dn)
-      sg_put4<OutT>(reinterpret_cast<OutT *>(a.out0) + row * a.dn + d, v);
-    else
-      sg_put4<OutT>(reinterpret_cast<OutT *>(a.out1) + row * a.dv + (d - a.dn), v);
+  } else if constexpr (EPI == kSgEpiKvb) {
+    const int kw = a.dn + a.dv, hd = n0 / kw, d = n0 - hd * kw;
+    if (d < a.dn) {
+      c.kind = kSgK;
+      c.coff = (int64_t)hd * a.seq * a.dn + d;
+    } else {
+      c.kind = kSgV;
+      c.coff = (int64_t)hd * a.seq * a.dv + (d - a.dn);
+    }
+  }
+  return c;
+}
+
+// Stores v (bias included) for row m, token s of sequence b, at column
+// group c.
+template <int EPI, typename OutT>
+__device__ __forceinline__ void sg_write(const SplitGemmArgs &a, const SgCol &c, int m, int b,
+                                         int s, const float (&v)[4]) {
+  if constexpr (EPI == kSgEpiFinal) {
+    sg_put4<float>(a.y + (int64_t)m * a.ldy + c.coff, v);
+  } else {
+    const int64_t rowp = (int64_t)b * a.heads * a.seq + s;
+    if constexpr (EPI == kSgEpiQkv) {
+      if (c.kind == kSgKva) {
+        sg_put4<float>(a.kva + (int64_t)m * a.kva_ld + c.coff, v);
+      } else if (c.kind == kSgQNope) {
+        sg_put4<OutT>(reinterpret_cast<OutT *>(a.out0) + rowp * a.dn + c.coff, v);
+      } else {
+        // interleaved pairs (2p, 2p + 1) of q_rope at position lens[b] + s
+        // (src/model.rs:70-84, :199-203)
+        const float pos = (float)(a.lens[b] + s);
+        float r[4];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          float cs, sn;
+          rope_cs(pos * a.inv_freq[c.p + u], a.mscale, cs, sn);
+          r[2 * u] = v[2 * u] * cs - v[2 * u + 1] * sn;
+          r[2 * u + 1] = v[2 * u + 1] * cs + v[2 * u] * sn;
+        }
+        sg_put4<OutT>(reinterpret_cast<OutT *>(a.out1) + rowp * a.dr + c.coff, r);
+      }
+    } else {  // kSgEpiKvb
+      if (c.kind == kSgK)
+        sg_put4<OutT>(reinterpret_cast<OutT *>(a.out0) + rowp * a.dn + c.coff, v);
+      else
+        sg_put4<OutT>(reinterpret_cast<OutT *>(a.out1) + rowp * a.dv + c.coff, v);
+    }
   }
 }
 
@@ -201,7 +239,8 @@ __global__ __launch_bounds__(256) void k_sg_reduce(SplitGemmArgs a) {
   float v[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) v[e] = acc[e] + (a.bias ? a.bias[n0 + e] : 0.f);
-  sg_store4<EPI, OutT>(a, m, n0, v);
+  const int b = m / a.seq;
+  sg_write<EPI, OutT>(a, sg_col<EPI>(a, n0), m, b, m - b * a.seq, v);
 }
 
 // Tile shape and pipeline of one instantiation: NBW x MBW 32-blocks per
@@ -394,40 +433,13 @@ __global__ __launch_bounds__(kSgThreads) void k_split_gemm(SplitGemmArgs a, cons
       // column part of the address
       const int n0 = bn * BN + (wn * NBW + pp * PA) * 32 + lch * 4;
       const bool col_ok = n0 < a.N;
-      int kind = 0;  // 0 rows y / partials, 1 q_nope, 2 q_rope, 3 kv_a, 4 k, 5 v
-      int64_t coff = n0;
-      int p = 0;
+      SgCol col{kSgY, 0, n0};
       float bias4[4] = {0.f, 0.f, 0.f, 0.f};
       if (!partial && col_ok) {
         if (a.bias)
 #pragma unroll
           for (int e = 0; e < 4; ++e) bias4[e] = a.bias[n0 + e];
-        if constexpr (EPI == kSgEpiQkv) {
-          const int qw = a.dn + a.dr, nq = a.heads * qw;
-          if (n0 >= nq) {
-            kind = 3;
-            coff = n0 - nq;
-          } else {
-            const int hd = n0 / qw, d = n0 - hd * qw;
-            if (d < a.dn) {
-              kind = 1;
-              coff = (int64_t)hd * a.seq * a.dn + d;
-            } else {
-              kind = 2;
-              p = (d - a.dn) >> 1;
-              coff = (int64_t)hd * a.seq * a.dr + (d - a.dn);
-            }
-          }
-        } else if constexpr (EPI == kSgEpiKvb) {
-          const int kw = a.dn + a.dv, hd = n0 / kw, d = n0 - hd * kw;
-          if (d < a.dn) {
-            kind = 4;
-            coff = (int64_t)hd * a.seq * a.dn + d;
-          } else {
-            kind = 5;
-            coff = (int64_t)hd * a.seq * a.dv + (d - a.dn);
-          }
-        }
+        col = sg_col<EPI>(a, n0);
       }
       pipe::wait_lgkm<0>();  // the staging writes are done
 #pragma unroll
@@ -442,37 +454,7 @@ __global__ __launch_bounds__(kSgThreads) void k_split_gemm(SplitGemmArgs a, cons
           sg_put4<float>(a.part + ((int64_t)blockIdx.y * a.M + m) * a.N + n0, v);
           continue;
         }
-        if constexpr (EPI == kSgEpiFinal) {
-          sg_put4<float>(a.y + (int64_t)m * a.ldy + coff, v);
-        } else {
-          // (b H + h) s_len + s = b H s_len + s + h s_len: the row part
-          const int64_t rowp = ((int64_t)rb[ii] * a.heads) * a.seq + rs[ii];
-          if constexpr (EPI == kSgEpiQkv) {
-            if (kind == 3) {
-              sg_put4<float>(a.kva + (int64_t)m * a.kva_ld + coff, v);
-            } else if (kind == 1) {
-              sg_put4<OutT>(reinterpret_cast<OutT *>(a.out0) + rowp * a.dn + coff, v);
-            } else {
-              // interleaved pairs (2p, 2p + 1) of q_rope (src/model.rs:70-84)
-              const float pos = (float)(a.lens[rb[ii]] + rs[ii]);
-              float rr[4];
-#pragma unroll
-              for (int u = 0; u < 2; ++u) {
-                const float ang = pos * a.inv_freq[p + u];
-                float cs, sn;
-                rope_cs(ang, a.mscale, cs, sn);
-                rr[2 * u] = v[2 * u] * cs - v[2 * u + 1] * sn;
-                rr[2 * u + 1] = v[2 * u + 1] * cs + v[2 * u] * sn;
-              }
-              sg_put4<OutT>(reinterpret_cast<OutT *>(a.out1) + rowp * a.dr + coff, rr);
-            }
-          } else {  // kSgEpiKvb
-            if (kind == 4)
-              sg_put4<OutT>(reinterpret_cast<OutT *>(a.out0) + rowp * a.dn + coff, v);
-            else
-              sg_put4<OutT>(reinterpret_cast<OutT *>(a.out1) + rowp * a.dv + coff, v);
-          }
-        }
+        sg_write<EPI, OutT>(a, col, m, rb[ii], rs[ii], v);
       }
       // the next pass rewrites the staging rows after this lane's reads
       pipe::wait_lgkm<0>();
