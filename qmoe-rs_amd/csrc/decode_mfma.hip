@@ -524,6 +524,16 @@ struct SegDesc {
 // are scanned by wave 0 alone (lane-local runs, then a shuffle scan: one
 // barrier in all); longer arrays by all NT threads (log-step, two barriers
 // per step).
+// The piece of this block.  Blocks are dealt to the 8 XCDs round-robin, so
+// block i maps to piece (i % 8) * (grid / 8) + i / 8: consecutive pieces,
+// i.e. the pieces of one sequence, sit on one XCD and its query rows come
+// from that XCD's L2 after the first load (16-head decode 41.0-41.4 ->
+// 40.5-40.8 us per step in a same-box A/B; the 128-head decode within noise).
+__device__ __forceinline__ int decode_piece() {
+  const int g = gridDim.x, b = blockIdx.x;
+  return (g & 7) ? b : (b & 7) * (g >> 3) + (b >> 3);
+}
+
 template <int NT>
 __device__ int32_t lds_exscan(int32_t *a, int32_t n, int32_t *tmp) {
   if (n <= 512) {
@@ -589,7 +599,7 @@ __device__ void plan_round(const int32_t *__restrict__ lens, int32_t pending, in
                            int32_t from, int32_t seg_tokens, int32_t *scratch, SegDesc *list,
                            int32_t *meta, int2 *__restrict__ seq_info) {
   const int tid = threadIdx.x;
-  const int blocks = gridDim.x, piece = blockIdx.x;
+  const int blocks = gridDim.x, piece = decode_piece();
   int32_t *P = scratch, *SB = scratch + batch + 1, *tmp = SB + batch + 1;
   for (int b = tid; b < batch; b += NT) P[b] = lens[b] + pending + seg_tokens;
   __syncthreads();
@@ -663,7 +673,7 @@ __device__ WavePlan plan_wave(const int32_t *__restrict__ lens, int32_t pending,
                               int32_t seg_tokens, int2 *__restrict__ seq_info) {
   static_assert(kSegCap >= 64, "one round per piece");
   const int lane = threadIdx.x & 63;
-  const int blocks = gridDim.x, piece = blockIdx.x;
+  const int blocks = gridDim.x, piece = decode_piece();
   const bool live = lane < batch;
   const int32_t x = live ? lens[lane] + pending + seg_tokens : 0;
   const int32_t incl = wave_incl_scan(x);  // P[b + 1]
