@@ -243,8 +243,10 @@ def v2lite_weights(seed, hidden=2048, heads=16):
     return w
 
 
-def weight_bytes_of(w):
-    return 4 * (w.wq.size + w.wkva.size + w.wkvb.size + w.wo.size)
+def weight_bytes_of(w, proj_dtype=qmla.F32):
+    """Weight bytes a step streams: 4 per weight (f32, held as bf16 hi + lo
+    halves), 2 with bf16 operands (the hi halves)."""
+    return (4 if proj_dtype == qmla.F32 else 2) * (w.wq.size + w.wkva.size + w.wkvb.size + w.wo.size)
 
 
 class LayerDecodeBench:
@@ -259,14 +261,17 @@ class LayerDecodeBench:
     could still hold.  Each cache grows by one token per use in growth mode:
     each sequence holds exactly its 4096 rows (16 pages of 256) and takes a
     page from the pool's free list (sized for 512 more tokens per sequence
-    at creation) when it crosses a page boundary."""
+    at creation) when it crosses a page boundary.  proj_dtype BF16 runs the
+    projections with bf16 operands (qmla_layer_set_projection_dtype)."""
 
     def __init__(self, stream, seed, batch=32, ctx=4096, hidden=2048, heads=16, layers=2,
-                 min_cache_bytes=512 << 20):
+                 min_cache_bytes=512 << 20, proj_dtype=qmla.F32):
         r, dr = 512, 64
         ws = [v2lite_weights(seed + 7 * i, hidden, heads) for i in range(layers)]
         self.layers = [qmla.MlaLayer(w) for w in ws]
-        self.weight_bytes = weight_bytes_of(ws[0])
+        for layer in self.layers:
+            layer.set_projection_dtype(proj_dtype)
+        self.weight_bytes = weight_bytes_of(ws[0], proj_dtype)
         self.batch, self.ctx, self.stream = batch, ctx, stream
         ncache = max(2, math.ceil(min_cache_bytes / (batch * ctx * ROW_BYTES)))
         tmp = qmla.DeviceBuffer(64 << 20)
@@ -324,11 +329,15 @@ class LayerPrefillBench:
     o_proj, and fills the cache.  The decompression is also timed on its
     own, through qmla_cache_materialise over the same 4 x 2048 cached latent
     rows (the kv_b_proj product batched over heads, plus the gather of the
-    rows and the head-broadcast k_rope copy)."""
+    rows and the head-broadcast k_rope copy).  proj_dtype BF16 runs the
+    projections with bf16 operands (qmla_layer_set_projection_dtype); the
+    decompression is then not timed."""
 
-    def __init__(self, stream, seed, batch=4, seq=2048, hidden=2048, heads=16):
+    def __init__(self, stream, seed, batch=4, seq=2048, hidden=2048, heads=16, proj_dtype=qmla.F32):
         H, dr, r = heads, 64, 512
         self.layer = qmla.MlaLayer(v2lite_weights(seed, hidden, heads))
+        self.layer.set_projection_dtype(proj_dtype)
+        self.proj_dtype = proj_dtype
         self.batch, self.seq, self.heads, self.hidden, self.stream = batch, seq, H, hidden, stream
         self.caches = [qmla.KVCache([seq] * batch, r, dr, qmla.BF16) for _ in range(2)]
         self.xs = qmla.DeviceBuffer(batch * seq * hidden * 4)
@@ -350,6 +359,13 @@ class LayerPrefillBench:
         b, s, H = self.batch, self.seq, self.heads
         wall, ev = time_steps(self.step, steps, warmup, self.stream, min_warm_ms)
         step_ms = dict(STATS)
+        att = b * H * (s * (s + 1) // 2) * 2 * (192 + 128)
+        kvb = 2 * b * s * 512 * H * (128 + 128)
+        proj = 2 * b * s * self.hidden * (H * 192 + 576 + H * 128)
+        gflop = {"attention": att / 1e9, "kv_b_decompress": kvb / 1e9, "projections": proj / 1e9}
+        if self.proj_dtype != qmla.F32:
+            return {"tok_s": b * s / (ev * 1e-3), "ms_per_step": ev, "wall_ms_per_step": wall,
+                    "gflop": gflop, "step_ms": step_ms}
         # the decompression alone, over a cache the steps above filled
         c = self.caches[0]
         n = C.c_size_t()
@@ -364,17 +380,13 @@ class LayerPrefillBench:
                                                          mws.ptr, n.value, qmla._sh(self.stream)))
 
         _, evm = time_steps(mstep, steps, 2, self.stream)
-        att = b * H * (s * (s + 1) // 2) * 2 * (192 + 128)
-        kvb = 2 * b * s * 512 * H * (128 + 128)
-        proj = 2 * b * s * self.hidden * (H * 192 + 576 + H * 128)
         # the split form runs x w = x_hi w_hi + x_lo w_hi + x_hi w_lo (+ the
         # bias columns) as one bf16 GEMM over K' = 3 K + 2 columns padded to
         # a multiple of 64: the bf16 flops the MFMAs execute
         kp = -(-(3 * 512 + 2) // 64) * 64
         kvb_bf16 = kvb * kp / 512
         return {"tok_s": b * s / (ev * 1e-3), "ms_per_step": ev, "wall_ms_per_step": wall,
-                "gflop": {"attention": att / 1e9, "kv_b_decompress": kvb / 1e9, "projections": proj / 1e9},
-                "step_ms": step_ms,
+                "gflop": gflop, "step_ms": step_ms,
                 "decompress": {"ms": evm, "gflop": kvb / 1e9,
                                "f32_equivalent_tflops": kvb / (evm * 1e-3) / 1e12,
                                "bf16_gflop_executed": kvb_bf16 / 1e9,
@@ -827,6 +839,8 @@ def main():
                     help="only run the MLA layer prefill line (for profiling)")
     ap.add_argument("--sweeps-only", action="store_true",
                     help="only run the batch-1 decode and prefill sweeps (for profiling)")
+    ap.add_argument("--bf16-projections", action="store_true",
+                    help="with --layer-only / --layer-prefill-only: bf16-operand projections")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the decode path shards by batch "
@@ -843,12 +857,13 @@ def main():
         mb = MoEBench(stream)
         print(json.dumps({"moe_layer": mb.run(args.steps, args.warmup, WARM_MS)}), flush=True)
         return
+    pdt = qmla.BF16 if args.bf16_projections else qmla.F32
     if args.layer_only:
-        lb = LayerDecodeBench(stream, seed=51)
+        lb = LayerDecodeBench(stream, seed=51, proj_dtype=pdt)
         print(json.dumps({"layer_decode_step": lb.run(args.steps, args.warmup, WARM_MS)}), flush=True)
         return
     if args.layer_prefill_only:
-        lp = LayerPrefillBench(stream, seed=61)
+        lp = LayerPrefillBench(stream, seed=61, proj_dtype=pdt)
         print(json.dumps({"layer_prefill": lp.run(max(3, args.steps // 5), 3, WARM_MS)}), flush=True)
         return
     if args.sweeps_only:
@@ -914,6 +929,24 @@ def main():
         if not args.no_cpu_baseline:
             secondary["layer_prefill"]["cpu_baseline"] = cpu_baseline_layer_prefill()
         log("layer prefill", json.dumps(secondary["layer_prefill"]))
+        del lp
+        # the same two calls with bf16-operand projections (the bf16 tolerance)
+        bf16_note = ("projections with bf16 operands (qmla_layer_set_projection_dtype BF16: the weights' bf16 "
+                     "halves, activations rounded to bf16, f32 accumulation; the bf16 tolerance, 2e-2), "
+                     "bf16 latent cache")
+        lb = LayerDecodeBench(stream, seed=51, proj_dtype=qmla.BF16)
+        secondary["layer_decode_step_bf16_projections"] = {
+            "workload": "MlaAttention forward_with_cache, hidden 2048, 16 heads, r 512, batch 32, 4096 cached "
+                        "+ 1, " + bf16_note + "; CPU baseline: layer_decode_step's",
+            **lb.run(args.steps, args.warmup, WARM_MS)}
+        log("layer decode step, bf16 projections", json.dumps(secondary["layer_decode_step_bf16_projections"]))
+        del lb
+        lp = LayerPrefillBench(stream, seed=61, proj_dtype=qmla.BF16)
+        secondary["layer_prefill_bf16_projections"] = {
+            "workload": "MlaAttention forward_prefill, batch 4 x 2048 tokens, hidden 2048, 16 heads, r 512, "
+                        + bf16_note + "; CPU baseline: layer_prefill's",
+            **lp.run(max(3, args.steps // 5), 3, WARM_MS)}
+        log("layer prefill, bf16 projections", json.dumps(secondary["layer_prefill_bf16_projections"]))
         del lp
         sw = Batch1Sweeps(stream, seed=71)
         dsw = sw.decode(args.steps, args.warmup)

@@ -331,6 +331,22 @@ QMLA_API qmla_status qmla_layer_create(const qmla_layer_config *cfg, const float
                               const float *ln_b, const float *wkvb, const float *bkvb,
                               const float *wo, const float *bo, qmla_layer **out);
 QMLA_API qmla_status qmla_layer_destroy(qmla_layer *layer);
+/* Operand precision of the layer's hand-written projection kernels: q_proj
+ * with kv_a_proj_with_mqa, the W_UK / W_UV absorption products and o_proj of
+ * a decode step, and q_proj, kv_a_proj_with_mqa, kv_b_proj and o_proj of a
+ * prefill.  No counterpart in the reference, whose Linear layers compute in
+ * the weights' dtype (f32 there).
+ *   QMLA_F32 (the default): f32-exact products (each operand as bf16 hi + lo
+ *     halves, three bf16 MFMAs per step, f32 accumulation; ~2^-16 relative).
+ *   QMLA_BF16: bf16 operands with f32 accumulation -- the weights rounded to
+ *     bf16 (their hi halves), the activations rounded to nearest even; one
+ *     MFMA per step and half the weight bytes.  Results then hold the bf16
+ *     tolerance (2e-2), whatever the cache dtype.
+ * The rocBLAS paths (prefill below 128 tokens, decode shapes the skinny
+ * kernel does not take) and qmla_cache_materialise stay f32-exact.  Applies
+ * to calls issued after it returns: set it before the layer is shared with
+ * other threads.  QMLA_ERR_INVALID_ARG for a NULL layer or another dtype. */
+QMLA_API qmla_status qmla_layer_set_projection_dtype(qmla_layer *layer, qmla_dtype dtype);
 /* Device scratch that serves either forward call below for (batch, seq)
  * new tokens: the larger of the two calls' needs (their call-specific
  * regions overlay one another).  No counterpart in the reference, which
@@ -358,7 +374,8 @@ QMLA_API qmla_status qmla_layer_prefill_workspace_bytes(const qmla_layer *layer,
  * f32 cache: f32 throughout.  bf16 cache: the new rows are stored rounded
  * to bf16 and the attention core is the bf16 MFMA decode (kv_lora_rank /
  * rope 512/64, 128/32 or 64/16; other shapes return QMLA_ERR_UNSUPPORTED);
- * the projections stay f32. */
+ * the projections stay f32 unless qmla_layer_set_projection_dtype chose
+ * bf16 operands. */
 QMLA_API qmla_status qmla_layer_forward_with_cache(const qmla_layer *layer, const float *xs, int32_t batch,
                                           int32_t seq, qmla_kv_cache *cache, float *out,
                                           void *workspace, size_t workspace_bytes,

@@ -219,6 +219,9 @@ struct SkinnyGemmArgs {
   float *add_dst;
   const float *add_src;
   int64_t add_n;
+  // bf16 operands: the weights' hi halves and bf16(x), one MFMA per step
+  // (a PACKB output then carries its hi halves only)
+  int bf16ops;
 };
 struct LatentRowsArgs;
 int skinny_waves(int K);
@@ -265,6 +268,9 @@ struct SplitGemmArgs {
   // (f32), which a second launch adds in slice order before the epilogue
   int ksplit;
   float *part;
+  // bf16 operands: the weights' and activations' hi halves only (records of
+  // 1 KB, no lo halves), one MFMA per step, f32 accumulation
+  int bf16ops;
 };
 bool split_gemm_supported(int N, int K);
 // K slices the split GEMM uses for an M x N x K product (1 when its tiles
@@ -282,7 +288,7 @@ size_t split_gemm_pack_bytes(int M, int K);
 qmla_status launch_split_gemm(const SplitGemmArgs &a, void *pack, hipStream_t stream);
 // The GEMM over activation records a producer already wrote (split_gemm_
 // pack_bytes(M, K) bytes at most; a.x unused): hi | lo records of f32
-// activations, or with hi_only the hi records of bf16 ones.
+// activations, or with hi_only (or a.bf16ops) hi-only records of 1 KB.
 qmla_status launch_split_gemm_packed(const SplitGemmArgs &a, const void *xrec, hipStream_t stream,
                                      bool hi_only = false);
 

@@ -47,6 +47,10 @@ struct qmla_layer {
   float *b1 = nullptr;   // [bq | bkva]
   float *buv = nullptr;  // [H][dv]: b_V^h
   bool skinny = false;   // the split weights exist (every K a multiple of 16)
+  // bf16 operands in the hand-written projection kernels (the weights' hi
+  // halves and bf16 activations, f32 accumulation); qmla_layer_set_
+  // projection_dtype.  The rocBLAS paths and the materialise call stay exact.
+  bool proj_bf16 = false;
   // Split-form rows of wq, wkva, wkvb and wo for the GEMMs of products with
   // many rows: row n of a [N][K] weight becomes [w_hi | w_hi | w_lo | b_hi,
   // b_lo, 0...] in bf16 (split_cols(K) columns; hi = bf16(v), lo = bf16(v -
@@ -300,7 +304,8 @@ __global__ __launch_bounds__(256) void k_latent_rows(LatentRowsArgs a) {
 // the cache row [LayerNorm(c) | rope(k_pe)] at position i of its (empty)
 // sequence; the split GEMM's activation records of LayerNorm(c) (kv_b_proj's
 // input, K = r: record (tok / 32, c / 16), lane tok % 32 + 32 ((c / 8) % 2),
-// hi and lo halves); and rope(k_pe) as the attention's k_rope [b, 1, s, dr]
+// hi and lo halves, or with rec_lo = 0 (bf16 operands) hi-only records of
+// 1 KB); and rope(k_pe) as the attention's k_rope [b, 1, s, dr]
 // in bf16 or f32.  The sequences start empty (forward_prefill checks it),
 // so positions are the token indices, lens is not read, and the wave of
 // each sequence's token 0 sets its length to s.  The grid covers n rounded
@@ -308,17 +313,18 @@ __global__ __launch_bounds__(256) void k_latent_rows(LatentRowsArgs a) {
 // r <= 512 U, dr % 8 == 0.
 template <typename KT, int U>
 __global__ __launch_bounds__(256) void k_prefill_rows(LatentRowsArgs a, int n, uint8_t *rec,
-                                                      KT *k_rope, int32_t *lens) {
+                                                      int rec_lo, KT *k_rope, int32_t *lens) {
   const int tok = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int r = a.r, dr = a.dr, C8 = r / 8, KS = r / 16;
+  const int RB = rec_lo ? 2048 : 1024;  // bytes per record
   if (tok >= n) {
     // the padding rows of the last 32-row record group: zeros
     if (tok >= (n + 31) / 32 * 32) return;
     for (int c8 = lane; c8 < C8; c8 += 64) {
       uint8_t *rp =
-          rec + ((int64_t)(tok >> 5) * KS + (c8 >> 1)) * 2048 + ((tok & 31) + 32 * (c8 & 1)) * 16;
+          rec + ((int64_t)(tok >> 5) * KS + (c8 >> 1)) * RB + ((tok & 31) + 32 * (c8 & 1)) * 16;
       *reinterpret_cast<u32x4_t *>(rp) = u32x4_t{0, 0, 0, 0};
-      *reinterpret_cast<u32x4_t *>(rp + 1024) = u32x4_t{0, 0, 0, 0};
+      if (rec_lo) *reinterpret_cast<u32x4_t *>(rp + 1024) = u32x4_t{0, 0, 0, 0};
     }
     return;
   }
@@ -384,13 +390,14 @@ __global__ __launch_bounds__(256) void k_prefill_rows(LatentRowsArgs a, int n, u
       *reinterpret_cast<floatx4_t *>(dst + 32 * c8) = floatx4_t{v[0], v[1], v[2], v[3]};
       *reinterpret_cast<floatx4_t *>(dst + 32 * c8 + 16) = floatx4_t{v[4], v[5], v[6], v[7]};
     }
-    uint8_t *rp = rec + ((int64_t)(tok >> 5) * KS + (c8 >> 1)) * 2048 + ((tok & 31) + 32 * (c8 & 1)) * 16;
+    uint8_t *rp = rec + ((int64_t)(tok >> 5) * KS + (c8 >> 1)) * RB + ((tok & 31) + 32 * (c8 & 1)) * 16;
     *reinterpret_cast<u32x4_t *>(rp) =
         u32x4_t{hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16),
                 hi[4] | ((uint32_t)hi[5] << 16), hi[6] | ((uint32_t)hi[7] << 16)};
-    *reinterpret_cast<u32x4_t *>(rp + 1024) =
-        u32x4_t{lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16),
-                lo[4] | ((uint32_t)lo[5] << 16), lo[6] | ((uint32_t)lo[7] << 16)};
+    if (rec_lo)
+      *reinterpret_cast<u32x4_t *>(rp + 1024) =
+          u32x4_t{lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16),
+                  lo[4] | ((uint32_t)lo[5] << 16), lo[6] | ((uint32_t)lo[7] << 16)};
   }
   const float pos = (float)i;
   for (int p = lane; p < dr / 2; p += 64) {
@@ -997,6 +1004,14 @@ qmla_status qmla_layer_create(const qmla_layer_config *cfg, const float *wq, con
   return QMLA_OK;
 }
 
+qmla_status qmla_layer_set_projection_dtype(qmla_layer *layer, qmla_dtype dtype) {
+  QMLA_REQUIRE(layer, QMLA_ERR_INVALID_ARG, "NULL layer");
+  QMLA_REQUIRE(dtype == QMLA_F32 || dtype == QMLA_BF16, QMLA_ERR_INVALID_ARG,
+               "projection dtype %d", (int)dtype);
+  layer->proj_bf16 = dtype == QMLA_BF16;
+  return QMLA_OK;
+}
+
 qmla_status qmla_layer_destroy(qmla_layer *layer) {
   if (!layer) return QMLA_OK;
   for (void *p : layer->allocs) (void)hipFree(p);
@@ -1088,6 +1103,7 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
       a.q_nope1 = qn1;
       a.q_rope1 = qr1;
       a.kva1 = kva1;
+      a.bf16ops = L->proj_bf16 ? 1 : 0;
       QMLA_TRY(launch_skinny_gemm(a, s));
     }
     // q_lat[t, h, :] = W_UK^h^T q_nope[t, h, :]   (z = head), and the latent
@@ -1099,6 +1115,7 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
                                       nullptr, 0, qlat + (size_t)m0 * H * r, (int64_t)H * r, r,
                                       std::min(32, n - m0), r, dn, H);
       uk.x2 = qn1 + (size_t)m0 * H * dn;
+      uk.bf16ops = L->proj_bf16 ? 1 : 0;
       if (m0 == 0) {
         // the roped q_rope's two halves
         uk.add_dst = qr;
@@ -1127,6 +1144,7 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
       SkinnyGemmArgs uv = skinny_args(L->wuvf, olat + (size_t)m0 * H * r, (int64_t)H * r, r,
                                       L->buv, dv, o, 0, dv, M, dv, r, H);
       uv.mode = kSkinnyPackB;
+      uv.bf16ops = L->proj_bf16 ? 1 : 0;  // o_proj below then reads the hi halves only
       QMLA_TRY(launch_skinny_gemm(uv, s));
       const int64_t plane = (int64_t)M * g.hidden;
       const bool split = g.hidden % 4 == 0 && (H * dv) % (16 * kOprojGroups) == 0 &&
@@ -1136,6 +1154,7 @@ qmla_status qmla_layer_forward_with_cache(const qmla_layer *L, const float *xs, 
                                       split ? part : out + (size_t)m0 * g.hidden, g.hidden, 0, M,
                                       g.hidden, H * dv, 1);
       op.x_packed = true;
+      op.bf16ops = L->proj_bf16 ? 1 : 0;
       if (split) {
         op.groups = kOprojGroups;
         op.sgrp = plane;
@@ -1230,6 +1249,7 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
     a.out_bf16 = bfa ? 1 : 0;
     a.ksplit = 1;  // the launcher picks the K slices
     a.part = (float *)(ws + w.sgpart);
+    a.bf16ops = L->proj_bf16 ? 1 : 0;
     SplitGemmArgs qa = a;
     qa.w_frag = L->w1f;
     qa.N = H * (dn + dr) + r + dr;
@@ -1253,11 +1273,13 @@ qmla_status qmla_layer_forward_prefill(const qmla_layer *L, const float *xs, int
       const LatentRowsArgs la = latent_rows_args(L, kva, seq, nullptr, cache);
       const dim3 grid((n + 31) / 32 * 8);  // 4 tokens a block, n rounded up to 32
       // r <= 512 (use_split_gemm): one group of 8 values per lane
+      const int rec_lo = L->proj_bf16 ? 0 : 1;
       if (bfa)
-        k_prefill_rows<uint16_t, 1><<<grid, dim3(256), 0, s>>>(la, n, krec, (uint16_t *)kr,
-                                                               cache->d_lens);
+        k_prefill_rows<uint16_t, 1><<<grid, dim3(256), 0, s>>>(la, n, krec, rec_lo,
+                                                               (uint16_t *)kr, cache->d_lens);
       else
-        k_prefill_rows<float, 1><<<grid, dim3(256), 0, s>>>(la, n, krec, kr, cache->d_lens);
+        k_prefill_rows<float, 1><<<grid, dim3(256), 0, s>>>(la, n, krec, rec_lo, kr,
+                                                            cache->d_lens);
       QMLA_LAUNCH_CHECK("k_prefill_rows");
       for (int32_t i = 0; i < batch; ++i) cache->h_lens[i] += seq;
     }

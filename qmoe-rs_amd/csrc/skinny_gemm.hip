@@ -69,6 +69,13 @@ __device__ __forceinline__ void split8(const floatx4_t &a, const floatx4_t &b, b
   }
 }
 
+// bf16(x) of 8 f32 values (round to nearest even).
+__device__ __forceinline__ void hi8(const floatx4_t &a, const floatx4_t &b, bf16x8_t &hi) {
+  const float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) hi[i] = (__bf16)v[i];
+}
+
 constexpr int kChunk = 4;  // k-steps of 16 per load group (two groups in flight)
 
 // Byte offset of activation (m, k) in the fragment-major B layout: per
@@ -79,10 +86,11 @@ __device__ __forceinline__ int64_t packed_b_offset(int m, int64_t k) {
 }
 
 // XM: how the B operand is read -- kXF32 f32 x, kXPacked the pre-split
-// fragment-major records, kXSum the f32 sum x + x2 of two planes.
+// fragment-major records, kXSum the f32 sum x + x2 of two planes.  B16: bf16
+// operands (the weights' hi halves and bf16(x), one MFMA per step).
 constexpr int kXF32 = 0, kXPacked = 1, kXSum = 2;
 
-template <int NW, int XM>
+template <int NW, int XM, bool B16>
 __global__ __launch_bounds__(NW * 64) void k_skinny_gemm(SkinnyGemmArgs a, LatentRowsArgs rows,
                                                          int n_rows) {
   // LDS: the waves' partial tiles, or a latent row block's row
@@ -131,10 +139,11 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_gemm(SkinnyGemmArgs a, Laten
       const int st = min(s0 + c, steps - 1);
       const uint8_t *f = wf + (int64_t)st * 2048;
       ah[buf][c] = *reinterpret_cast<const bf16x8_t *>(f);
-      al[buf][c] = *reinterpret_cast<const bf16x8_t *>(f + 1024);
+      if constexpr (!B16) al[buf][c] = *reinterpret_cast<const bf16x8_t *>(f + 1024);
       if constexpr (XM == kXPacked) {
         xa[buf][c] = *reinterpret_cast<const floatx4_t *>(xf + (int64_t)st * 2048);
-        xb[buf][c] = *reinterpret_cast<const floatx4_t *>(xf + (int64_t)st * 2048 + 1024);
+        if constexpr (!B16)
+          xb[buf][c] = *reinterpret_cast<const floatx4_t *>(xf + (int64_t)st * 2048 + 1024);
       } else if constexpr (XM == kXSum) {
         xa[buf][c] = *reinterpret_cast<const floatx4_t *>(xp + st * 16) +
                      *reinterpret_cast<const floatx4_t *>(xp2 + st * 16);
@@ -153,13 +162,17 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_gemm(SkinnyGemmArgs a, Laten
         bf16x8_t xh, xl;
         if constexpr (XM == kXPacked) {
           xh = __builtin_bit_cast(bf16x8_t, xa[buf][c]);
-          xl = __builtin_bit_cast(bf16x8_t, xb[buf][c]);
+          if constexpr (!B16) xl = __builtin_bit_cast(bf16x8_t, xb[buf][c]);
+        } else if constexpr (B16) {
+          hi8(xa[buf][c], xb[buf][c], xh);
         } else {
           split8(xa[buf][c], xb[buf][c], xh, xl);
         }
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[buf][c], xh, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[buf][c], xl, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[buf][c], xh, acc, 0, 0, 0);
+        if constexpr (!B16) {
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[buf][c], xl, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[buf][c], xh, acc, 0, 0, 0);
+        }
       }
     }
   };
@@ -217,7 +230,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_gemm(SkinnyGemmArgs a, Laten
         const uint16_t lo = f32_to_bf16_bits(v[q] - bf16_bits_to_f32(hi));
         const int64_t off = packed_b_offset(m, k + q);
         *reinterpret_cast<uint16_t *>(yb + off) = hi;
-        *reinterpret_cast<uint16_t *>(yb + off + 1024) = lo;
+        if constexpr (!B16) *reinterpret_cast<uint16_t *>(yb + off + 1024) = lo;
       }
       continue;
     }
@@ -313,14 +326,21 @@ qmla_status launch_skinny_gemm(const SkinnyGemmArgs &a, hipStream_t stream,
   const size_t lds = std::max(sizeof(float) * nw * 16 * 64,
                               rows ? latent_row_lds_bytes(rows->r, rows->dr) : 0);
   if (a.x_packed) QMLA_REQUIRE(a.Z == 1, QMLA_ERR_SHAPE, "packed activations need Z = 1");
-  auto go = [&](auto xm) {
+  auto go2 = [&](auto xm, auto b16) {
     constexpr int XM = decltype(xm)::value;
+    constexpr bool B16 = decltype(b16)::value;
     switch (nw) {
-      case 8: k_skinny_gemm<8, XM><<<grid, dim3(512), lds, stream>>>(args, ra, extra); break;
-      case 4: k_skinny_gemm<4, XM><<<grid, dim3(256), lds, stream>>>(args, ra, extra); break;
-      case 2: k_skinny_gemm<2, XM><<<grid, dim3(128), lds, stream>>>(args, ra, extra); break;
-      default: k_skinny_gemm<1, XM><<<grid, dim3(64), lds, stream>>>(args, ra, extra); break;
+      case 8: k_skinny_gemm<8, XM, B16><<<grid, dim3(512), lds, stream>>>(args, ra, extra); break;
+      case 4: k_skinny_gemm<4, XM, B16><<<grid, dim3(256), lds, stream>>>(args, ra, extra); break;
+      case 2: k_skinny_gemm<2, XM, B16><<<grid, dim3(128), lds, stream>>>(args, ra, extra); break;
+      default: k_skinny_gemm<1, XM, B16><<<grid, dim3(64), lds, stream>>>(args, ra, extra); break;
     }
+  };
+  auto go = [&](auto xm) {
+    if (a.bf16ops)
+      go2(xm, std::true_type{});
+    else
+      go2(xm, std::false_type{});
   };
   if (a.x_packed)
     go(std::integral_constant<int, kXPacked>{});

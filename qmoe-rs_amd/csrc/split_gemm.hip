@@ -9,7 +9,9 @@
 // v_mfma_f32_32x32x16_bf16 with f32 accumulation:
 //   x w = x_hi w_hi + x_lo w_hi + x_hi w_lo   (x_lo w_lo < 2^-16 |x w|)
 // When x is bf16 (the bf16 attention's context) x_lo is zero: the x records
-// carry no lo half and the second product is skipped.
+// carry no lo half and the second product is skipped.  With bf16 operands
+// (SplitGemmArgs::bf16ops) both lo halves are left out: x_hi w_hi alone,
+// one MFMA per step, hi-only records of both operands in LDS.
 //
 // Operands as fragment-major records.  A record is one MFMA operand of a
 // 32-row block and a 16-wide k-step, exactly as the wave's lanes read it:
@@ -87,12 +89,13 @@ __device__ __forceinline__ void sg_put4<uint16_t>(uint16_t *p, const float (&v)[
 // 32][16 ks + 8 (l / 32) .. + 7]; rows past M are zero.  One thread per
 // lane of a record, 4 records per 256-thread block.  XM: kSgXRow f32 rows
 // x[m ldx + k]; kSgXHeads* the attention context [b, H, s, dv] read as the
-// row [b s][H dv] (k = h dv + d), bf16 (records without lo halves) or f32.
+// row [b s][H dv] (k = h dv + d), bf16 or f32.  LO: the records carry lo
+// halves (not for bf16 x, nor for bf16 operands).
 constexpr int kSgXRow = 0, kSgXHeadsBf16 = 1, kSgXHeadsF32 = 2;
 
-template <int XM>
+template <int XM, bool LO>
 __global__ __launch_bounds__(256) void k_pack_rows(SplitGemmArgs a, uint8_t *__restrict__ rec) {
-  constexpr bool LO = XM != kSgXHeadsBf16;
+  static_assert(!(LO && XM == kSgXHeadsBf16), "bf16 x has no lo halves");
   constexpr int RB = LO ? 2048 : 1024;  // bytes per record
   const int KS = a.K / 16;
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);  // < 2^31 (host check)
@@ -134,7 +137,7 @@ __global__ __launch_bounds__(256) void k_pack_rows(SplitGemmArgs a, uint8_t *__r
       lo[i] = l0 | ((uint32_t)l1 << 16);
     }
     *reinterpret_cast<u32x4_t *>(dst) = hi;
-    *reinterpret_cast<u32x4_t *>(dst + 1024) = lo;
+    if constexpr (LO) *reinterpret_cast<u32x4_t *>(dst + 1024) = lo;
   }
 }
 
@@ -251,18 +254,23 @@ struct SgCfg {
   static constexpr int NBW = NBW_, MBW = MBW_, WN = WN_, KSC = KSC_, NST = NST_;
 };
 
-template <class CF, bool XLO, int EPI, typename OutT>
+// XLO / WLO: the activation / weight records' lo halves take part (x_lo w_hi
+// and x_hi w_lo); both off is the bf16-operand product.
+template <class CF, bool XLO, bool WLO, int EPI, typename OutT>
 __global__ __launch_bounds__(kSgThreads) void k_split_gemm(SplitGemmArgs a, const uint8_t *xrec) {
   constexpr int NBW = CF::NBW, MBW = CF::MBW, WN = CF::WN, KSC = CF::KSC, NST = CF::NST;
   constexpr int WM = 8 / WN;
   constexpr int MBT = MBW * WM, NBT = NBW * WN;  // 32-row / 32-output blocks of the tile
   constexpr int BM = 32 * MBT, BN = 32 * NBT;
-  constexpr int XR = XLO ? 2048 : 1024;           // bytes per activation record
-  constexpr int WSEG = KSC * NBT * kFrag;         // a stage's weight records
+  constexpr int XR = XLO ? 2048 : 1024;           // LDS bytes per activation record
+  constexpr int WR = WLO ? 2048 : 1024;           // ... per weight record
+  constexpr int WI = KSC * NBT * (WLO ? 2 : 1);   // weight DMA instructions per chunk
+  constexpr int WSEG = KSC * NBT * WR;            // a stage's weight records
   constexpr int STAGE = WSEG + KSC * MBT * XR;    // ... and activation records
   constexpr int NDMA = STAGE / 1024;              // DMA instructions per chunk
-  static_assert(NDMA % 8 == 0, "DMA slots per wave");
-  constexpr int DW = NDMA / 8;                    // ... per wave
+  // ... per wave; when NDMA is not a multiple of 8, the waves past the last
+  // instruction repeat it (the same bytes into the same place)
+  constexpr int DW = (NDMA + 7) / 8;
   extern __shared__ __attribute__((aligned(16))) char sg_lds[];
   const uint32_t ring_u = (uint32_t)(uintptr_t)(sg_lds);
 
@@ -287,22 +295,23 @@ __global__ __launch_bounds__(kSgThreads) void k_split_gemm(SplitGemmArgs a, cons
   const int NC = KS / KSC / a.ksplit, cz = blockIdx.y * NC;
 
   // DMA slot u of this wave: instruction i = wave DW + u of the chunk.
-  // Instructions [0, 2 KSC NBT) move weight records (record j KSC + ks of
-  // tile block j, hi then lo), the rest activation records (tile row block
-  // j, k-step ks, hi [then lo]).  Tile blocks past N or M re-load the last
+  // Instructions [0, WI) move weight records (record j KSC + ks of tile
+  // block j, hi [then lo]), the rest activation records (tile row block j,
+  // k-step ks, hi [then lo]).  Tile blocks past N or M re-load the last
   // block (their outputs are dropped).
   auto dma_one = [&](int c, int u) __attribute__((always_inline)) {
     const uint32_t st = ring_u + (uint32_t)((c % NST) * STAGE);
     {
-      const int i = wave * DW + u;
+      const int i = NDMA % 8 ? min(wave * DW + u, NDMA - 1) : wave * DW + u;
       const uint8_t *src;
-      if (i < 2 * KSC * NBT) {
-        const int rec = i >> 1, half = i & 1, j = rec / KSC, ks = rec % KSC;
+      if (i < WI) {
+        const int rec = WLO ? i >> 1 : i, half = WLO ? i & 1 : 0;
+        const int j = rec / KSC, ks = rec % KSC;
         const int nb = min(bn * NBT + j, NB - 1);
         src = reinterpret_cast<const uint8_t *>(a.w_frag) +
               ((int64_t)nb * KS + KSC * (cz + c) + ks) * kFrag + half * 1024;
       } else {
-        const int xi = i - 2 * KSC * NBT;
+        const int xi = i - WI;
         const int rec = XLO ? xi >> 1 : xi, half = XLO ? xi & 1 : 0;
         const int j = rec / KSC, ks = rec % KSC;
         const int mb = min(bm * MBT + j, MB - 1);
@@ -336,9 +345,9 @@ __global__ __launch_bounds__(kSgThreads) void k_split_gemm(SplitGemmArgs a, cons
       bf16x8_t xh[MBW], xl[MBW], wh[NBW], wl[NBW];
 #pragma unroll
       for (int i = 0; i < NBW; ++i) {
-        const char *f = st + ((wn * NBW + i) * KSC + ks) * kFrag;
+        const char *f = st + ((wn * NBW + i) * KSC + ks) * WR;
         wh[i] = *reinterpret_cast<const bf16x8_t *>(f);
-        wl[i] = *reinterpret_cast<const bf16x8_t *>(f + 1024);
+        if constexpr (WLO) wl[i] = *reinterpret_cast<const bf16x8_t *>(f + 1024);
       }
 #pragma unroll
       for (int j = 0; j < MBW; ++j) {
@@ -353,7 +362,8 @@ __global__ __launch_bounds__(kSgThreads) void k_split_gemm(SplitGemmArgs a, cons
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wh[i], xh[j], acc[i][j], 0, 0, 0);
           if constexpr (XLO)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wh[i], xl[j], acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wl[i], xh[j], acc[i][j], 0, 0, 0);
+          if constexpr (WLO)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wl[i], xh[j], acc[i][j], 0, 0, 0);
           const int pr = (ks * NBW + i) * MBW + j;
 #pragma unroll
           for (int u = 0; u < DW; ++u)
@@ -470,18 +480,19 @@ __global__ __launch_bounds__(kSgThreads) void k_split_gemm(SplitGemmArgs a, cons
 
 // The ring, or the epilogue's staging rows (8 waves x 32 rows of 32 or 64
 // f32 outputs, padded) when they need more.
-template <class CF, bool XLO>
+template <class CF, bool XLO, bool WLO>
 constexpr size_t sg_lds_bytes() {
   constexpr int MBT = CF::MBW * (8 / CF::WN), NBT = CF::NBW * CF::WN;
-  constexpr size_t ring = (size_t)CF::NST * CF::KSC * (NBT * kFrag + MBT * (XLO ? 2048 : 1024));
+  constexpr size_t ring =
+      (size_t)CF::NST * CF::KSC * (NBT * (WLO ? 2048 : 1024) + MBT * (XLO ? 2048 : 1024));
   constexpr size_t staging = (size_t)8 * 32 * (32 * (CF::NBW >= 2 ? 2 : 1) * 4 + 16);
   return ring > staging ? ring : staging;
 }
 
-template <class CF, bool XLO>
+template <class CF, bool XLO, bool WLO>
 qmla_status sg_launch(const SplitGemmArgs &a, const uint8_t *xrec, hipStream_t s) {
   constexpr int BN = 32 * CF::NBW * CF::WN, BM = 32 * CF::MBW * (8 / CF::WN);
-  static_assert(sg_lds_bytes<CF, XLO>() <= 160 * 1024, "LDS");
+  static_assert(sg_lds_bytes<CF, XLO, WLO>() <= 160 * 1024, "LDS");
   // whole groups of kSgGn x kSgGm tile slots, dealt to the 8 XCDs
   const int64_t gn = ((a.N + BN - 1) / BN + kSgGn - 1) / kSgGn;
   const int64_t gm = ((a.M + BM - 1) / BM + kSgGm - 1) / kSgGm;
@@ -489,7 +500,9 @@ qmla_status sg_launch(const SplitGemmArgs &a, const uint8_t *xrec, hipStream_t s
   const int64_t blocks = groups * kSgGn * kSgGm;
   QMLA_REQUIRE(blocks <= 0x7fffffff, QMLA_ERR_SHAPE, "split GEMM grid of %lld blocks",
                (long long)blocks);
-  const size_t lds = sg_lds_bytes<CF, XLO>();
+  const size_t lds = sg_lds_bytes<CF, XLO, WLO>();
+  QMLA_REQUIRE(a.K % (16 * CF::KSC) == 0, QMLA_ERR_UNSUPPORTED,
+               "split GEMM K %d is not a whole number of %d-wide chunks", a.K, 16 * CF::KSC);
   QMLA_REQUIRE(a.ksplit >= 1 && a.ksplit <= 65535 && (a.K / 16 / CF::KSC) % a.ksplit == 0 &&
                    (a.ksplit == 1 || a.part),
                QMLA_ERR_SHAPE, "split GEMM: %d K slices", a.ksplit);
@@ -508,14 +521,14 @@ qmla_status sg_launch(const SplitGemmArgs &a, const uint8_t *xrec, hipStream_t s
   switch (a.epi) {
     case kSgEpiQkv:
       if (a.out_bf16)
-        return go(k_split_gemm<CF, XLO, kSgEpiQkv, uint16_t>, k_sg_reduce<kSgEpiQkv, uint16_t>);
-      return go(k_split_gemm<CF, XLO, kSgEpiQkv, float>, k_sg_reduce<kSgEpiQkv, float>);
+        return go(k_split_gemm<CF, XLO, WLO, kSgEpiQkv, uint16_t>, k_sg_reduce<kSgEpiQkv, uint16_t>);
+      return go(k_split_gemm<CF, XLO, WLO, kSgEpiQkv, float>, k_sg_reduce<kSgEpiQkv, float>);
     case kSgEpiKvb:
       if (a.out_bf16)
-        return go(k_split_gemm<CF, XLO, kSgEpiKvb, uint16_t>, k_sg_reduce<kSgEpiKvb, uint16_t>);
-      return go(k_split_gemm<CF, XLO, kSgEpiKvb, float>, k_sg_reduce<kSgEpiKvb, float>);
+        return go(k_split_gemm<CF, XLO, WLO, kSgEpiKvb, uint16_t>, k_sg_reduce<kSgEpiKvb, uint16_t>);
+      return go(k_split_gemm<CF, XLO, WLO, kSgEpiKvb, float>, k_sg_reduce<kSgEpiKvb, float>);
     default:
-      return go(k_split_gemm<CF, XLO, kSgEpiFinal, float>, k_sg_reduce<kSgEpiFinal, float>);
+      return go(k_split_gemm<CF, XLO, WLO, kSgEpiFinal, float>, k_sg_reduce<kSgEpiFinal, float>);
   }
 }
 
@@ -568,6 +581,9 @@ qmla_status sg_check(const SplitGemmArgs &a) {
 // kv_a has 120 blocks).
 qmla_status sg_run(const SplitGemmArgs &a0, const uint8_t *xrec, bool xlo, hipStream_t s) {
   using Big = SgCfg<4, 2, 2, 1, 3>;
+  // bf16 operands: two k-steps per chunk, so that a barrier still spans 16
+  // MFMAs per wave (the layer prefill 0.432 -> 0.427 ms in a same-box A/B)
+  using BigB16 = SgCfg<4, 2, 2, 2, 3>;
   using Small = SgCfg<1, 1, 2, 2, 3>;
   static_assert(Small::KSC == 2, "split_gemm_slices counts chunks of 32 k");
   SplitGemmArgs a = a0;
@@ -575,9 +591,13 @@ qmla_status sg_run(const SplitGemmArgs &a0, const uint8_t *xrec, bool xlo, hipSt
   QMLA_REQUIRE(a.ksplit == 1 || a.part, QMLA_ERR_WORKSPACE,
                "split GEMM of %d x %d x %d needs %zu bytes of partial sums", a.M, a.N, a.K,
                split_gemm_part_bytes(a.M, a.N, a.K));
+  if (a.bf16ops) {
+    if (a.M >= kSplitGemmBigRows) return sg_launch<BigB16, false, false>(a, xrec, s);
+    return sg_launch<Small, false, false>(a, xrec, s);
+  }
   if (a.M >= kSplitGemmBigRows)
-    return xlo ? sg_launch<Big, true>(a, xrec, s) : sg_launch<Big, false>(a, xrec, s);
-  return xlo ? sg_launch<Small, true>(a, xrec, s) : sg_launch<Small, false>(a, xrec, s);
+    return xlo ? sg_launch<Big, true, true>(a, xrec, s) : sg_launch<Big, false, true>(a, xrec, s);
+  return xlo ? sg_launch<Small, true, true>(a, xrec, s) : sg_launch<Small, false, true>(a, xrec, s);
 }
 }  // namespace
 
@@ -585,7 +605,7 @@ qmla_status launch_split_gemm_packed(const SplitGemmArgs &a, const void *xrec, h
                                      bool hi_only) {
   QMLA_TRY(sg_check(a));
   QMLA_REQUIRE(xrec, QMLA_ERR_SHAPE, "packed activations without records");
-  return sg_run(a, static_cast<const uint8_t *>(xrec), !hi_only, s);
+  return sg_run(a, static_cast<const uint8_t *>(xrec), !hi_only && !a.bf16ops, s);
 }
 
 qmla_status launch_split_gemm(const SplitGemmArgs &a, void *pack, hipStream_t s) {
@@ -596,13 +616,15 @@ qmla_status launch_split_gemm(const SplitGemmArgs &a, void *pack, hipStream_t s)
   QMLA_REQUIRE(recs + 3 <= 0x7fffffff, QMLA_ERR_SHAPE, "split GEMM pack grid");
   uint8_t *xrec = static_cast<uint8_t *>(pack);
   const dim3 pg((unsigned)((recs + 3) / 4)), pb(256);
-  const bool xlo = !(a.x_heads && a.x_bf16);
-  if (a.x_heads == 0)
-    k_pack_rows<kSgXRow><<<pg, pb, 0, s>>>(a, xrec);
-  else if (a.x_bf16)
-    k_pack_rows<kSgXHeadsBf16><<<pg, pb, 0, s>>>(a, xrec);
+  const bool xlo = !(a.x_heads && a.x_bf16) && !a.bf16ops;
+  if (a.x_heads && a.x_bf16)
+    k_pack_rows<kSgXHeadsBf16, false><<<pg, pb, 0, s>>>(a, xrec);
+  else if (a.x_heads == 0)
+    xlo ? k_pack_rows<kSgXRow, true><<<pg, pb, 0, s>>>(a, xrec)
+        : k_pack_rows<kSgXRow, false><<<pg, pb, 0, s>>>(a, xrec);
   else
-    k_pack_rows<kSgXHeadsF32><<<pg, pb, 0, s>>>(a, xrec);
+    xlo ? k_pack_rows<kSgXHeadsF32, true><<<pg, pb, 0, s>>>(a, xrec)
+        : k_pack_rows<kSgXHeadsF32, false><<<pg, pb, 0, s>>>(a, xrec);
   QMLA_LAUNCH_CHECK("k_pack_rows");
   return sg_run(a, xrec, xlo, s);
 }

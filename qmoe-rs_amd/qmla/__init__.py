@@ -120,6 +120,7 @@ SIGNATURES = {
     "qmla_layer_default_scales": (_st, [C.POINTER(LayerConfig)]),
     "qmla_layer_create": (_st, [C.POINTER(LayerConfig)] + [_vp] * 10 + [C.POINTER(_vp)]),
     "qmla_layer_destroy": (_st, [_vp]),
+    "qmla_layer_set_projection_dtype": (_st, [_vp, _st]),
     "qmla_layer_workspace_bytes": (_st, [_vp, _vp, _i32, _i32, C.POINTER(_sz)]),
     "qmla_layer_prefill_workspace_bytes": (_st, [_vp, _vp, _i32, _i32, C.POINTER(_sz)]),
     "qmla_layer_forward_with_cache": (_st, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
@@ -485,6 +486,11 @@ class MlaLayer:
                                       C.byref(h)))
         self.handle = h.value
         self.hidden = w.hidden
+
+    def set_projection_dtype(self, dtype: int) -> None:
+        """F32 (default): f32-exact projections; BF16: bf16 operands with f32
+        accumulation in the hand-written projection kernels."""
+        check(lib().qmla_layer_set_projection_dtype(self.handle, dtype))
 
     def workspace_bytes(self, cache: KVCache, batch: int, seq: int) -> int:
         """Scratch that serves either forward call for (batch, seq) tokens."""

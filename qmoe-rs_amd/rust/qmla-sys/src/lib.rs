@@ -246,6 +246,8 @@ extern "C" {
         wo: *const f32, bo: *const f32, out: *mut *mut qmla_layer
     ) -> qmla_status;
     pub fn qmla_layer_destroy(layer: *mut qmla_layer) -> qmla_status;
+    // no counterpart in the reference: bf16 operands in the projection kernels
+    pub fn qmla_layer_set_projection_dtype(layer: *mut qmla_layer, dtype: qmla_dtype) -> qmla_status;
     pub fn qmla_layer_workspace_bytes(
         layer: *const qmla_layer, cache: *const qmla_kv_cache, batch: i32, seq: i32,
         bytes: *mut usize

@@ -406,6 +406,12 @@ impl MlaAttention {
         Ok(MlaAttention { raw, config })
     }
 
+    /// Operand precision of the projection kernels: DType::F32 (default,
+    /// f32-exact) or DType::BF16 (bf16 operands, f32 accumulation).
+    pub fn set_projection_dtype(&mut self, dtype: DType) -> Result<()> {
+        ok(unsafe { qmla_layer_set_projection_dtype(self.raw, dtype.raw()) })
+    }
+
     /// Scratch that serves either forward call for (batch, seq) tokens.
     pub fn workspace_bytes(&self, cache: &KVCache, batch: usize, seq: usize) -> Result<usize> {
         let mut n = 0usize;

@@ -113,3 +113,4 @@ def test_materialise_and_layer_calls_validate_without_a_device():
     assert L.qmla_cache_materialise_workspace_bytes(None, None, 0, 1, C.byref(n)) == 1
     assert L.qmla_cache_materialise(None, None, 0, 1, None, None, None, None, 0, None) == 1
     assert L.qmla_layer_forward_with_cache(None, None, 1, 1, None, None, None, 0, None) == 1
+    assert L.qmla_layer_set_projection_dtype(None, qmla.BF16) == 1

@@ -536,3 +536,63 @@ def test_layer_prefill_at_bench_widths(qmla_gpu, dt, b, s):
     print(f"decode step after it, {dt} cache rel_err={err1:.2e}", flush=True)
     assert err1 < tol
     assert list(cache.lengths()) == [s + 1] * b
+
+
+@pytest.mark.parametrize("b,s", [(1, 128), (1, 512), (2, 2048)])
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_layer_bf16_projections(qmla_gpu, dt, b, s):
+    """qmla_layer_set_projection_dtype(BF16): the projection kernels take
+    bf16 operands (one MFMA per step; 128 rows split K, 512 rows the 64 x
+    128 tiles, 4096 rows the 256 x 256 tiles), then a decode step on the
+    skinny kernels.  Against the oracle's f32 path at the bf16 tolerance,
+    with either cache dtype; the results must differ from the f32-exact
+    projections (the mode took effect), and switching back to F32 gives the
+    f32-exact results bit for bit."""
+    q = qmla_gpu
+    hidden, H, dn, dr, dv, r = 2048, 16, 128, 64, 128, 512
+    w = O.MlaWeights.random(hidden, H, dn, dr, dv, r, seed=1950)
+    xs = O.normal((b, s, hidden), 1951)
+    x1 = O.normal((b, 1, hidden), 1952)
+    cdt = q.F32 if dt == "f32" else q.BF16
+    ref, (k, v, kr) = O.mla_forward_prefill(w, xs)
+    ref1 = O.mla_forward_with_cache(w, x1, k, v, kr)
+
+    def run(layer):
+        cache = q.KVCache([s + 1] * b, r, dr, cdt)
+        return layer.forward_prefill(xs, cache), layer.forward_with_cache(x1, cache)
+
+    layer = q.MlaLayer(w)
+    exact, exact1 = run(layer)
+    layer.set_projection_dtype(q.BF16)
+    out, out1 = run(layer)
+    err, err1 = rel_err(out, ref), rel_err(out1, ref1)
+    print(f"bf16 projections, {dt} cache, prefill {b}x{s} rel_err={err:.2e}, "
+          f"decode step rel_err={err1:.2e}", flush=True)
+    assert err < 2e-2 and err1 < 2e-2
+    assert rel_err(out, exact) > 1e-5 and rel_err(out1, exact1) > 1e-5
+    layer.set_projection_dtype(q.F32)
+    again, again1 = run(layer)
+    np.testing.assert_array_equal(again, exact)
+    np.testing.assert_array_equal(again1, exact1)
+
+
+@pytest.mark.parametrize("b,s", [(2, 96), (1, 160)])
+def test_layer_bf16_projections_at_small_latent_dims(qmla_gpu, b, s):
+    """bf16 operands at the tiny head shapes (hidden 512, 8 heads, dn 32 /
+    dr 16 / dv 32, kv_lora_rank 64: kv_b_proj's K = 64 is two chunks of the
+    64 x 128 tiling), bf16 cache, prefill then a decode step: 2e-2."""
+    q = qmla_gpu
+    w = O.MlaWeights.random(512, 8, 32, 16, 32, 64, seed=1960)
+    layer = q.MlaLayer(w)
+    layer.set_projection_dtype(q.BF16)
+    xs = O.normal((b, s, 512), 1961)
+    cache = q.KVCache([s + 1] * b, 64, 16, q.BF16)
+    out = layer.forward_prefill(xs, cache)
+    ref, (k, v, kr) = O.mla_forward_prefill(w, xs)
+    err = rel_err(out, ref)
+    x1 = O.normal((b, 1, 512), 1962)
+    err1 = rel_err(layer.forward_with_cache(x1, cache), O.mla_forward_with_cache(w, x1, k, v, kr))
+    print(f"bf16 projections small dims {b}x{s}: prefill {err:.2e}, step {err1:.2e}", flush=True)
+    assert err < 2e-2 and err1 < 2e-2
+    with pytest.raises(q.QmlaError):
+        layer.set_projection_dtype(7)
