@@ -131,6 +131,7 @@ __device__ int sel_bin(const int32_t *sel, int np, int e, int t0, int n, int *ou
 }
 
 constexpr int kRankTokens = 256;  // tokens the GEMV blocks rank themselves (LDS table)
+static_assert(kRankTokens <= kMfmaThreads, "rank_tokens gives every token a thread");
 
 // rank[t] = rank of expert e among token t's E logits lg[t][*]: the number of
 // experts before it in (logit descending, index ascending) order, the
