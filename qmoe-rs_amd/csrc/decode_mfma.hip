@@ -1031,9 +1031,10 @@ __global__ __launch_bounds__(256) void k_decode_merge_frag(
     }
   };
   // Up to kUp slots: every lse and block is requested at once, one round
-  // trip instead of a chain of them (the 16-head decode merges 8-9 slots:
-  // step 41.0 -> 40.5 us in a same-box A/B).  More slots: loops unrolled so
-  // that several slots' loads are in flight at once.
+  // trip instead of a chain of them.  Same-box traces against the loop
+  // alone: the 128-head merge 14.0-14.1 -> 13.3-13.6 us, the 16-head one
+  // (8-9 slots) 4.84 -> 4.76 us; kUp = 10 timed the same.  More slots:
+  // loops unrolled so that several slots' loads are in flight at once.
   constexpr int kUp = 16;
   if (ns <= kUp) {
     float ls[kUp];
