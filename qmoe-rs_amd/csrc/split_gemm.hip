@@ -25,7 +25,7 @@
 // with direct-to-LDS DMA of contiguous 1 KB runs and holds nothing in
 // flight in registers.
 //
-// Block: 8 waves (two per SIMD) on a BN x BM output tile; wave (wn, wm)
+// Block: 8 waves (two per SIMD; SgCfg::NWV) on a BN x BM output tile; wave (wn, wm)
 // owns NBW 32-output blocks x MBW 32-row blocks (BN = 32 NBW WN, BM = 32
 // MBW WM).  K goes in chunks of KSC k-steps through an NST-deep LDS ring:
 // the DMA of chunk c + NST - 1 is issued while chunk c is multiplied,
@@ -58,7 +58,6 @@ namespace qmla {
 
 namespace {
 
-constexpr int kSgThreads = 512;      // 8 waves
 constexpr int kSgGn = 4, kSgGm = 8;  // tiles of an XCD group (n x m)
 constexpr int kFrag = 2048;          // one record: hi 1 KB, lo 1 KB
 
@@ -247,19 +246,19 @@ __global__ __launch_bounds__(256) void k_sg_reduce(SplitGemmArgs a) {
 }
 
 // Tile shape and pipeline of one instantiation: NBW x MBW 32-blocks per
-// wave, WN waves along N (8 / WN along M), KSC k-steps of 16 per chunk and
-// NST chunks in the LDS ring.
-template <int NBW_, int MBW_, int WN_, int KSC_, int NST_>
+// wave, NWV waves (WN along N, NWV / WN along M), KSC k-steps of 16 per
+// chunk and NST chunks in the LDS ring.
+template <int NBW_, int MBW_, int WN_, int KSC_, int NST_, int NWV_ = 8>
 struct SgCfg {
-  static constexpr int NBW = NBW_, MBW = MBW_, WN = WN_, KSC = KSC_, NST = NST_;
+  static constexpr int NBW = NBW_, MBW = MBW_, WN = WN_, KSC = KSC_, NST = NST_, NWV = NWV_;
 };
 
 // XLO / WLO: the activation / weight records' lo halves take part (x_lo w_hi
 // and x_hi w_lo); both off is the bf16-operand product.
 template <class CF, bool XLO, bool WLO, int EPI, typename OutT>
-__global__ __launch_bounds__(kSgThreads) void k_split_gemm(SplitGemmArgs a, const uint8_t *xrec) {
+__global__ __launch_bounds__(CF::NWV * 64) void k_split_gemm(SplitGemmArgs a, const uint8_t *xrec) {
   constexpr int NBW = CF::NBW, MBW = CF::MBW, WN = CF::WN, KSC = CF::KSC, NST = CF::NST;
-  constexpr int WM = 8 / WN;
+  constexpr int NWV = CF::NWV, WM = NWV / WN;
   constexpr int MBT = MBW * WM, NBT = NBW * WN;  // 32-row / 32-output blocks of the tile
   constexpr int BM = 32 * MBT, BN = 32 * NBT;
   constexpr int XR = XLO ? 2048 : 1024;           // LDS bytes per activation record
@@ -268,9 +267,9 @@ __global__ __launch_bounds__(kSgThreads) void k_split_gemm(SplitGemmArgs a, cons
   constexpr int WSEG = KSC * NBT * WR;            // a stage's weight records
   constexpr int STAGE = WSEG + KSC * MBT * XR;    // ... and activation records
   constexpr int NDMA = STAGE / 1024;              // DMA instructions per chunk
-  // ... per wave; when NDMA is not a multiple of 8, the waves past the last
-  // instruction repeat it (the same bytes into the same place)
-  constexpr int DW = (NDMA + 7) / 8;
+  // ... per wave; when NDMA is not a multiple of NWV, the waves past the
+  // last instruction repeat it (the same bytes into the same place)
+  constexpr int DW = (NDMA + NWV - 1) / NWV;
   extern __shared__ __attribute__((aligned(16))) char sg_lds[];
   const uint32_t ring_u = (uint32_t)(uintptr_t)(sg_lds);
 
@@ -302,7 +301,7 @@ __global__ __launch_bounds__(kSgThreads) void k_split_gemm(SplitGemmArgs a, cons
   auto dma_one = [&](int c, int u) __attribute__((always_inline)) {
     const uint32_t st = ring_u + (uint32_t)((c % NST) * STAGE);
     {
-      const int i = NDMA % 8 ? min(wave * DW + u, NDMA - 1) : wave * DW + u;
+      const int i = NDMA % NWV ? min(wave * DW + u, NDMA - 1) : wave * DW + u;
       const uint8_t *src;
       if (i < WI) {
         const int rec = WLO ? i >> 1 : i, half = WLO ? i & 1 : 0;
@@ -482,16 +481,16 @@ __global__ __launch_bounds__(kSgThreads) void k_split_gemm(SplitGemmArgs a, cons
 // f32 outputs, padded) when they need more.
 template <class CF, bool XLO, bool WLO>
 constexpr size_t sg_lds_bytes() {
-  constexpr int MBT = CF::MBW * (8 / CF::WN), NBT = CF::NBW * CF::WN;
+  constexpr int MBT = CF::MBW * (CF::NWV / CF::WN), NBT = CF::NBW * CF::WN;
   constexpr size_t ring =
       (size_t)CF::NST * CF::KSC * (NBT * (WLO ? 2048 : 1024) + MBT * (XLO ? 2048 : 1024));
-  constexpr size_t staging = (size_t)8 * 32 * (32 * (CF::NBW >= 2 ? 2 : 1) * 4 + 16);
+  constexpr size_t staging = (size_t)CF::NWV * 32 * (32 * (CF::NBW >= 2 ? 2 : 1) * 4 + 16);
   return ring > staging ? ring : staging;
 }
 
 template <class CF, bool XLO, bool WLO>
 qmla_status sg_launch(const SplitGemmArgs &a, const uint8_t *xrec, hipStream_t s) {
-  constexpr int BN = 32 * CF::NBW * CF::WN, BM = 32 * CF::MBW * (8 / CF::WN);
+  constexpr int BN = 32 * CF::NBW * CF::WN, BM = 32 * CF::MBW * (CF::NWV / CF::WN);
   static_assert(sg_lds_bytes<CF, XLO, WLO>() <= 160 * 1024, "LDS");
   // whole groups of kSgGn x kSgGm tile slots, dealt to the 8 XCDs
   const int64_t gn = ((a.N + BN - 1) / BN + kSgGn - 1) / kSgGn;
@@ -510,7 +509,7 @@ qmla_status sg_launch(const SplitGemmArgs &a, const uint8_t *xrec, hipStream_t s
   QMLA_REQUIRE(outs / 256 + 1 <= 0x7fffffff, QMLA_ERR_SHAPE, "split GEMM reduce grid");
   auto go = [&](auto kern, auto reduce) -> qmla_status {
     QMLA_TRY(ensure_dynamic_lds((const void *)kern, lds));
-    kern<<<dim3((unsigned)blocks, (unsigned)a.ksplit), dim3(kSgThreads), lds, s>>>(a, xrec);
+    kern<<<dim3((unsigned)blocks, (unsigned)a.ksplit), dim3(CF::NWV * 64), lds, s>>>(a, xrec);
     QMLA_LAUNCH_CHECK("k_split_gemm");
     if (a.ksplit > 1) {
       reduce<<<dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s>>>(a);
