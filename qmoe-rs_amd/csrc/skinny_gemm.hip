@@ -12,7 +12,9 @@
 //   x w = x_hi w_hi + x_lo w_hi + x_hi w_lo  (+ x_lo w_lo, below 2^-16 |x w|)
 // takes three v_mfma_f32_32x32x16_bf16 with f32 accumulation.  The products
 // keep ~16 significant bits of each operand (relative error ~2^-16 per
-// product, f32 accumulation), well inside the f32 path's tolerance.
+// product, f32 accumulation), well inside the f32 path's tolerance.  With
+// bf16 operands (SkinnyGemmArgs::bf16ops) only w_hi and bf16(x) enter: one
+// MFMA per step, and only the hi half of each weight record is read.
 //
 // Weight layout (fragment-major, built when the layer is created): for z,
 // 32-output block nb and 16-wide k-step ks, one 2 KB record at
@@ -36,6 +38,7 @@
 // writes the output in the layout its consumer reads:
 //   FINAL  y[m][n]
 //   PACKB  the output as the bf16 hi/lo B operand of a following product
+//          (hi halves only with bf16 operands)
 //          (fragment-major, output index z sy + n as its k), so that product
 //          reads its activations as contiguous records without splitting
 //   QKV    q_proj | kv_a_proj_with_mqa concatenated: head-split q_nope,
