@@ -576,6 +576,28 @@ def test_layer_bf16_projections(qmla_gpu, dt, b, s):
     np.testing.assert_array_equal(again1, exact1)
 
 
+def test_layer_bf16_projections_leave_the_rocblas_paths_exact(qmla_gpu):
+    """Calls below the hand-written kernels' range stay f32-exact in the
+    bf16-operand mode: a 64-token prefill (rocBLAS projections) and a decode
+    step of 65 new tokens per sequence (more rows than the skinny kernel
+    takes) give the f32-exact results bit for bit."""
+    q = qmla_gpu
+    w = O.MlaWeights.random(512, 8, 32, 16, 32, 64, seed=1970)
+    xs = O.normal((1, 64, 512), 1971)
+    x1 = O.normal((1, 65, 512), 1972)
+
+    def run(dtype):
+        layer = q.MlaLayer(w)
+        layer.set_projection_dtype(dtype)
+        cache = q.KVCache([200], 64, 16, q.BF16)
+        return layer.forward_prefill(xs, cache), layer.forward_with_cache(x1, cache)
+
+    exact, exact1 = run(q.F32)
+    got, got1 = run(q.BF16)
+    np.testing.assert_array_equal(got, exact)
+    np.testing.assert_array_equal(got1, exact1)
+
+
 @pytest.mark.parametrize("b,s", [(2, 96), (1, 160)])
 def test_layer_bf16_projections_at_small_latent_dims(qmla_gpu, b, s):
     """bf16 operands at the tiny head shapes (hidden 512, 8 heads, dn 32 /
