@@ -263,6 +263,15 @@ impl MlaAttention {
         self
     }
 
+    /// The same layer with its projection kernels on bf16 operands and f32
+    /// accumulation (DType::BF16: the bf16 tolerance, whatever the cache
+    /// dtype) or f32-exact (DType::F32, the default).  No counterpart in the
+    /// reference, whose Linear layers compute in the weights' dtype.
+    pub fn with_projection_dtype(mut self, dtype: DType) -> Result<Self> {
+        gpu(self.device.set_projection_dtype(dtype))?;
+        Ok(self)
+    }
+
     fn run(&self, xs: &Tensor, cache: &mut KVCache, prefill: bool) -> Result<Tensor> {
         let (b, s, hid) = xs.dims3()?;
         if hid != self.hidden {
